@@ -1,0 +1,84 @@
+"""ctypes binding of libdsa.so, the C-ABI of the HIP kernels.
+
+Every call is asynchronous on the given HIP stream and returns a status code;
+``check`` turns a failure into the exception type the reference raises for the
+same condition (``ValueError`` for invalid arguments, ``RuntimeError`` for a
+runtime failure).  There is no fallback: if the library is missing, loading
+raises ``RuntimeError`` naming the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libdsa.so"
+
+DSA_OK = 0
+DSA_EINVAL = -1
+DSA_EUNSUPPORTED = -2
+DSA_ELAUNCH = -3
+
+_c_int = ctypes.c_int32
+_c_i64 = ctypes.c_int64
+_c_float = ctypes.c_float
+_c_ptr = ctypes.c_void_p
+_c_size = ctypes.c_size_t
+
+# name -> (restype, argtypes).  Must match include/dsa.h exactly.
+SIGNATURES = {
+    "dsa_version": (_c_int, ()),
+    "dsa_last_error": (ctypes.c_char_p, ()),
+    "dsa_bsa_fwd": (_c_int, (
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr,          # q, k, v, o
+        ctypes.POINTER(_c_i64),                    # strides[12]
+        _c_int, _c_int, _c_int, _c_int, _c_int,    # batch, q_tokens, kv_tokens, heads, head_dim
+        _c_int,                                    # block_size
+        _c_ptr, _c_ptr, _c_int,                    # row_ptr, col_idx, route_batches
+        _c_float, _c_ptr, _c_ptr,                  # scale, lse, stream
+    )),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """Load libdsa.so once and bind the signatures; raise if it is missing."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIBRARY_PATH.exists():
+            raise RuntimeError(
+                f"{LIBRARY_PATH} is not built; run "
+                "`python -c 'import __graft_entry__ as g; g.build()'` or "
+                "`python -m dit_sparse_atten_amd.csrc.build`")
+        lib = ctypes.CDLL(str(LIBRARY_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            function = getattr(lib, name)
+            function.restype = restype
+            function.argtypes = list(argtypes)
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    message = load().dsa_last_error()
+    return message.decode() if message else ""
+
+
+def check(status: int, what: str) -> None:
+    """Raise the reference's exception type for a failed libdsa call."""
+    if status == DSA_OK:
+        return
+    message = last_error() or f"{what} failed with status {status}"
+    if status in (DSA_EINVAL, DSA_EUNSUPPORTED):
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def int64_array(values):
+    values = [int(value) for value in values]
+    return (_c_i64 * len(values))(*values)
