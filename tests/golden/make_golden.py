@@ -1,0 +1,167 @@
+"""Write the golden fixtures of tests/golden/ by running the reference's own
+CPU functions (yangshuo1230/DiT_Sparse_Atten, read-only at /root/reference).
+
+Only functions whose exact output no reference test or closed form pins are
+run here:
+  * flex._top_mass_route        tie order / fp32 rounding of sum and cumsum
+  * flex._sampled_block_mass    sample-index choice and log-weights
+  * FlexReuseBackend._sampled_route   persistence prior + selection
+  * spatial.build_spatial_layout      Morton order and majority-vote neighbours
+  * sparse.MatrixSparseBackend  config-0 bootstrap route, mass and outputs
+This script runs in the build container only (it reads /root/reference);
+tests, smoke() and bench.py read the .npz files it writes and never the
+reference.  Regenerate with:  python tests/golden/make_golden.py
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE.parents[1]))
+REFERENCE = Path(os.environ.get("DSA_REFERENCE", "/root/reference"))
+
+from tests.golden.inputs import clustered_qkv  # noqa: E402
+
+
+def _reference_modules():
+    if not REFERENCE.exists():
+        raise SystemExit(f"reference not found at {REFERENCE}")
+    sys.path.insert(0, str(REFERENCE))
+    from attention_backends import context, flex, sparse, spatial  # noqa: PLC0415
+    return context, flex, sparse, spatial
+
+
+def _save(name, **arrays):
+    path = HERE / f"{name}.npz"
+    np.savez_compressed(path, **arrays)
+    print(f"wrote {path.name}: {sorted(arrays)} ({path.stat().st_size} bytes)")
+
+
+def top_mass_fixture(flex):
+    rng = np.random.default_rng(20261201)
+    cases = {}
+    # Softmax-like rows with a heavy head, as block mass looks in practice.
+    cases["dirichlet"] = (rng.dirichlet(np.full(450, 0.3), size=(2, 48)).astype(np.float32),
+                          0.95, 0.625)
+    cases["dirichlet_t90_k50"] = (rng.dirichlet(np.full(450, 0.5), size=(1, 48)).astype(
+        np.float32), 0.90, 0.5)
+    # Many exact ties, including ties that straddle the selection boundary.
+    ties = rng.integers(0, 4, size=(1, 32, 64)).astype(np.float32) / np.float32(64.0)
+    ties[0, 0] = 1.0 / 64
+    cases["ties"] = (ties, 0.95, 0.625)
+    # Rows where the cap, not the target, decides.
+    flat = np.full((1, 8, 16), 1.0 / 16, dtype=np.float32)
+    cases["flat_cap"] = (flat, 0.95, 0.625)
+    cases["known_answer"] = (np.array([[[0.50, 0.30, 0.15, 0.05]]], np.float32), 0.90, 0.50)
+    arrays = {}
+    for name, (mass, target, keep) in cases.items():
+        route = flex._top_mass_route(torch.from_numpy(mass), target, keep).numpy()
+        arrays[f"{name}__mass"] = mass
+        arrays[f"{name}__route"] = route
+        arrays[f"{name}__params"] = np.array([target, keep], dtype=np.float64)
+    _save("top_mass_route", **arrays)
+
+
+def sampled_mass_fixture(flex):
+    arrays = {}
+    specs = {
+        # name: (tokens, heads, head_dim, block, samples, dtype)
+        "fp32_partial_s2": (1000, 3, 64, 128, 2, torch.float32),
+        "fp32_partial_s16": (1000, 3, 64, 128, 16, torch.float32),
+        "bf16_s16": (1024, 2, 128, 128, 16, torch.bfloat16),
+        "bf16_partial_s16": (300, 2, 128, 128, 16, torch.bfloat16),
+    }
+    for index, (name, (tokens, heads, dim, block, samples, dtype)) in enumerate(specs.items()):
+        q, k, _ = clustered_qkv(tokens, heads, dim, group=block, seed=100 + index, dtype=dtype)
+        mass = flex._sampled_block_mass(q, k, block, samples=samples)
+        arrays[f"{name}__checksum"] = np.array([q.double().sum().item(),
+                                                k.double().sum().item()])
+        arrays[f"{name}__mass"] = mass.numpy()
+        arrays[f"{name}__params"] = np.array(
+            [tokens, heads, dim, block, samples, int(dtype == torch.bfloat16), 100 + index])
+    _save("sampled_mass", **arrays)
+
+
+def sampled_route_fixture(flex):
+    """Sampled update with a previous route (prior 0.5), no grid: 32 blocks."""
+    tokens, heads = 4096, 4
+    q, k, _ = clustered_qkv(tokens, heads, 128, group=128, seed=7, dtype=torch.bfloat16)
+    generator = torch.Generator().manual_seed(8)
+    previous = torch.rand(heads, 32, 32, generator=generator) < 0.625
+    backend = flex.FlexReuseBackend(flex.FlexReuseConfig(
+        route_samples=16, mass_target=0.95, keep=0.625, route_persistence=0.5))
+    state = {"route": previous, "grid": None, "layout": None}
+    result = backend._sampled_route(state, q, k, None)
+    mass = flex._sampled_block_mass(q, k, 128, samples=16)
+    _save("sampled_route", seed=np.array([7, 8]), previous=previous.numpy(),
+          mass=mass.numpy(), route=result["route"].numpy())
+
+
+def spatial_fixture(spatial):
+    grids = {
+        "g2x4x8_b8_m8": ((2, 4, 8), 8, 8),
+        "g1x4x64": ((1, 4, 64), 128, 32),
+        "g16x45x80": ((16, 45, 80), 128, 32),
+        "g21x30x52": ((21, 30, 52), 128, 32),
+        "g4x16x16": ((4, 16, 16), 128, 32),
+    }
+    arrays = {}
+    for name, (grid, block, max_tokens) in grids.items():
+        layout = spatial.build_spatial_layout(grid, block, max_tokens)
+        arrays[f"{name}__params"] = np.array([*grid, block, max_tokens])
+        arrays[f"{name}__microtile"] = np.array(layout.microtile_shape)
+        arrays[f"{name}__permutation"] = layout.permutation_cpu.numpy()
+        arrays[f"{name}__neighbors"] = layout.neighbors_cpu.numpy()
+        arrays[f"{name}__block_frames"] = layout.block_frames_cpu.numpy()
+    _save("spatial_layout", **arrays)
+
+
+def sparse_config0_fixture(context, sparse):
+    """BASELINE config 0 through MatrixSparseBackend: step 0 then step 1."""
+    grid, tile = (4, 16, 16), 64
+    tokens, heads = 1024, 12
+    layout = sparse._spatial_layout(grid, tile, tokens)
+    order = layout.to_tile_major(torch.arange(tokens).view(1, tokens, 1, 1)).flatten()
+    q, k, v = clustered_qkv(tokens, heads, 128, group=tile, seed=0, permutation=order)
+    backend = sparse.MatrixSparseBackend(sparse.SparseConfig(
+        tile=tile, keep=0.625, mass_target=0.95, prefetch_route=False))
+    context.reset_runtime_state()
+    context._STATE.attention_id = 1
+    context._STATE.cfg_branch = 0
+    context._STATE.grid_size = grid
+    context._STATE.denoising_step = 0
+    with torch.no_grad():
+        out0 = backend(q, k, v, dtype=torch.float32)
+        state = next(iter(backend.state.values()))
+        route, mass = state["mask"].clone(), state["mass"].clone()
+        context._STATE.denoising_step = 1
+        out1 = backend(q, k, v, dtype=torch.float32)
+    heads_kept = [0, 7]
+    _save("sparse_config0",
+          tile_shape=np.array([layout.tile_h, layout.tile_w]),
+          order=order.numpy().astype(np.int32),
+          route=route.numpy(), mass=mass.float().numpy(),
+          checksum=np.array([q.double().sum().item(), k.double().sum().item(),
+                             v.double().sum().item()]),
+          heads=np.array(heads_kept),
+          out0=out0[0, :256, heads_kept].numpy(), out1=out1[0, :256, heads_kept].numpy())
+
+
+def main():
+    torch.set_num_threads(4)
+    context, flex, sparse, spatial = _reference_modules()
+    top_mass_fixture(flex)
+    sampled_mass_fixture(flex)
+    sampled_route_fixture(flex)
+    spatial_fixture(spatial)
+    sparse_config0_fixture(context, sparse)
+
+
+if __name__ == "__main__":
+    main()
