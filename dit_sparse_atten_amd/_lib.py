@@ -38,6 +38,30 @@ SIGNATURES = {
         _c_ptr, _c_ptr, _c_int,                    # row_ptr, col_idx, route_batches
         _c_float, _c_ptr, _c_ptr,                  # scale, lse, stream
     )),
+    "dsa_sampled_mass": (_c_int, (
+        _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
+        _c_int, _c_int, _c_int, _c_int, _c_int,    # tokens, heads, head_dim, block, samples
+        _c_float, _c_ptr, _c_ptr,                  # scale, mass, stream
+    )),
+    "dsa_route_select": (_c_int, (
+        _c_ptr, _c_ptr, _c_int, _c_int,            # mass, previous, rows, keys
+        _c_float, _c_float, _c_int, _c_int,        # rho, target, cap, sink_blocks
+        _c_ptr, _c_ptr, _c_ptr,                    # route, counts, stream
+    )),
+    "dsa_route_to_csr": (_c_int, (
+        _c_ptr, _c_int, _c_int,                    # route, rows, keys
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,    # counts, counts_out, row_ptr, col_idx, nnz
+        _c_ptr,                                    # stream
+    )),
+    "dsa_pack_rows": (_c_int, (
+        _c_ptr, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,  # route, rows, keys, counts, indices, stream
+    )),
+    "dsa_permute_rows": (_c_int, (
+        _c_int, ctypes.POINTER(_c_ptr), ctypes.POINTER(_c_ptr),  # tensors, src[], dst[]
+        ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64),          # src/dst byte strides
+        _c_ptr, _c_int, _c_int, _c_int, _c_int,                  # perm, batch, tokens, heads, row_bytes
+        _c_ptr,                                                  # stream
+    )),
 }
 
 _lock = threading.Lock()
@@ -77,6 +101,11 @@ def check(status: int, what: str) -> None:
     if status in (DSA_EINVAL, DSA_EUNSUPPORTED):
         raise ValueError(message)
     raise RuntimeError(message)
+
+
+def pointer_array(values):
+    values = [int(value) for value in values]
+    return (_c_ptr * len(values))(*values)
 
 
 def int64_array(values):

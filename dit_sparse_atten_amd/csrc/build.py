@@ -15,10 +15,13 @@ from pathlib import Path
 
 CSRC = Path(__file__).resolve().parent
 PACKAGE = CSRC.parent
+INCLUDE = PACKAGE.parent / "include"
 LIBRARY = PACKAGE / "libdsa.so"
 SOURCES = (
     "dsa_api.hip",
     "bsa_fwd.hip",
+    "route.hip",
+    "permute.hip",
 )
 
 # Packed FP32 VALU forms are disabled: the device code relies on scalar and
@@ -46,7 +49,7 @@ def build_library(verbose: bool = False) -> Path:
     """Compile every HIP source into one shared library and return its path."""
     sources = [str(CSRC / name) for name in SOURCES]
     tmp = LIBRARY.with_suffix(".so.tmp")
-    command = [hipcc_path(), *HIPCC_FLAGS, "-I", str(CSRC), "-o", str(tmp), *sources]
+    command = [hipcc_path(), *HIPCC_FLAGS, "-I", str(CSRC), "-I", str(INCLUDE), "-o", str(tmp), *sources]
     if verbose:
         print(" ".join(command), flush=True)
     result = subprocess.run(command, capture_output=True, text=True)

@@ -1,11 +1,11 @@
 // Shared definitions for the libdsa HIP kernels (gfx950 / CDNA4 only).
 //
 // Every entry point reports failures through a negative status code and a
-// thread-local message that dsa_last_error() returns.  Device code uses only
-// vector memory operations; nothing here writes through the scalar cache.
+// thread-local message that dsa_last_error() returns.
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include "dsa.h"  // public C-ABI: definitions must match these declarations
 #include <stdint.h>
 #include <stdio.h>
 #include <stdarg.h>

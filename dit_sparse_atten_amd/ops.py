@@ -70,6 +70,10 @@ class RouteCSR:
     def device(self):
         return self.row_ptr.device
 
+    def nnz_value(self):
+        """Total number of routed blocks (one 8-byte device-to-host read)."""
+        return int(self.nnz.item())
+
     def to_route(self):
         """Dense boolean route [route_batches, heads, q_blocks, k_blocks]."""
         if self._route is not None:
@@ -83,27 +87,13 @@ class RouteCSR:
 
 
 def csr_from_route(route, block_size=128):
-    """Build a RouteCSR from a boolean route [H,Q,K] or [R,H,Q,K] (host-built).
+    """RouteCSR of a boolean route [H,Q,K] or [R,H,Q,K] on the device.
 
     Column indices are the ascending selected key blocks of each row, i.e. the
     selected prefix of the reference's stable packing
-    (attention_backends/layout_ops.py:128-151).
+    (attention_backends/layout_ops.py:128-151); built by the HIP CSR kernels.
     """
-    if route.dtype != torch.bool:
-        raise ValueError("route must be boolean")
-    if route.ndim == 3:
-        route = route.unsqueeze(0)
-    if route.ndim != 4:
-        raise ValueError("route must have shape [heads, Q, K] or [batch, heads, Q, K]")
-    route_batches, heads, q_blocks, k_blocks = route.shape
-    flat = route.reshape(-1, k_blocks)
-    counts = flat.sum(-1, dtype=torch.int32)
-    row_ptr = torch.zeros(flat.shape[0] + 1, dtype=torch.int32, device=route.device)
-    row_ptr[1:] = torch.cumsum(counts, 0, dtype=torch.int32)
-    col_idx = torch.nonzero(flat, as_tuple=True)[1].to(torch.int32)
-    return RouteCSR(row_ptr, col_idx, counts.reshape(route_batches, heads, q_blocks),
-                    route_batches, heads, q_blocks, k_blocks, block_size,
-                    nnz=int(col_idx.numel()), route=route)
+    return route_to_csr(route, block_size=block_size)
 
 
 def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_size=128):
@@ -168,3 +158,177 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
             _stream_handle(q.device))
     _lib.check(status, "dsa_bsa_fwd")
     return (out, lse) if return_lse else out
+
+
+def _require_bool_route(route):
+    _require_cuda("route", route)
+    if route.dtype != torch.bool:
+        raise ValueError("route must be a boolean tensor")
+    return route.contiguous()
+
+
+def sampled_block_mass(q, k, block_size, samples=2, scale=None):
+    """Sampled block mass [heads, blocks, blocks] fp32 of a batch-1 call.
+
+    Same contract as the reference's ``_sampled_block_mass``
+    (attention_backends/flex.py:205-251), computed by one fused HIP kernel.
+    """
+    lib = _lib.load()
+    if q.shape[0] != 1 or q.shape[1] != k.shape[1]:
+        raise ValueError("sampled route update supports batch-1 self-attention")
+    if samples <= 0 or samples > block_size:
+        raise ValueError("route_samples must be in [1, block_size]")
+    q = _kernel_view("q", q)
+    k = _kernel_view("k", k)
+    _, tokens, heads, head_dim = q.shape
+    if scale is None:
+        scale = head_dim ** -0.5
+    blocks = math.ceil(tokens / block_size)
+    mass = torch.empty((heads, blocks, blocks), dtype=torch.float32, device=q.device)
+    strides = _lib.int64_array([q.stride(1), q.stride(2), k.stride(1), k.stride(2)])
+    with torch.cuda.device(q.device):
+        status = lib.dsa_sampled_mass(
+            q.data_ptr(), k.data_ptr(), strides, tokens, heads, head_dim, block_size,
+            samples, float(scale), mass.data_ptr(), _stream_handle(q.device))
+    _lib.check(status, "dsa_sampled_mass")
+    return mass
+
+
+def route_select(mass, target, keep, previous=None, persistence=0.0, sink_blocks=0):
+    """Prior + top-mass selection + sink on the GPU.
+
+    mass: fp32 [..., K] (non-negative); previous: bool of the same shape or
+    None.  Returns (route bool [..., K], counts int32 [...]).  The cap is
+    max(1, ceil(K * keep)) exactly as the reference's ``_top_mass_route``
+    (attention_backends/flex.py:83-94).
+    """
+    lib = _lib.load()
+    _require_cuda("mass", mass)
+    if mass.dtype != torch.float32:
+        raise ValueError("mass must be float32")
+    if not 0 < keep <= 1:
+        raise ValueError("keep must be in (0, 1]")
+    if not 0 < target <= 1:
+        raise ValueError("mass_target must be in (0, 1]")
+    mass = mass.contiguous()
+    keys = mass.shape[-1]
+    rows = mass.numel() // keys
+    cap = max(1, math.ceil(keys * keep))
+    prev_ptr = None
+    if previous is not None and persistence:
+        previous = _require_bool_route(previous)
+        if previous.shape != mass.shape:
+            raise ValueError("previous route must match the mass shape")
+        prev_ptr = previous.data_ptr()
+    route = torch.empty(mass.shape, dtype=torch.bool, device=mass.device)
+    counts = torch.empty(mass.shape[:-1], dtype=torch.int32, device=mass.device)
+    with torch.cuda.device(mass.device):
+        status = lib.dsa_route_select(
+            mass.data_ptr(), prev_ptr, rows, keys, float(persistence), float(target), cap,
+            int(sink_blocks), route.data_ptr(), counts.data_ptr(), _stream_handle(mass.device))
+    _lib.check(status, "dsa_route_select")
+    return route, counts
+
+
+def route_to_csr(route, counts=None, block_size=128):
+    """GPU CSR of a boolean route [H,Q,K] or [R,H,Q,K] (ascending key blocks)."""
+    lib = _lib.load()
+    route = _require_bool_route(route)
+    if route.ndim == 3:
+        route = route.unsqueeze(0)
+    if route.ndim != 4:
+        raise ValueError("route must have shape [heads, Q, K] or [batch, heads, Q, K]")
+    route_batches, heads, q_blocks, k_blocks = route.shape
+    rows = route_batches * heads * q_blocks
+    device = route.device
+    counts_out = None
+    if counts is None:
+        counts_out = torch.empty((route_batches, heads, q_blocks), dtype=torch.int32,
+                                 device=device)
+    else:
+        counts = counts.reshape(route_batches, heads, q_blocks).to(torch.int32).contiguous()
+    row_ptr = torch.empty(rows + 1, dtype=torch.int32, device=device)
+    col_idx = torch.empty(max(1, route.numel()), dtype=torch.int32, device=device)
+    nnz = torch.empty(1, dtype=torch.int64, device=device)
+    with torch.cuda.device(device):
+        status = lib.dsa_route_to_csr(
+            route.data_ptr(), rows, k_blocks,
+            counts.data_ptr() if counts is not None else None,
+            counts_out.data_ptr() if counts_out is not None else None,
+            row_ptr.data_ptr(), col_idx.data_ptr(), nnz.data_ptr(), _stream_handle(device))
+    _lib.check(status, "dsa_route_to_csr")
+    return RouteCSR(row_ptr, col_idx, counts if counts is not None else counts_out,
+                    route_batches, heads, q_blocks, k_blocks, block_size, nnz=nnz,
+                    route=route)
+
+
+def pack_rows(route):
+    """(counts int32 [...], indices int32 [..., K]): selected ids ascending,
+    then unselected ids ascending (layout_ops.py:128-151 semantics)."""
+    lib = _lib.load()
+    route = _require_bool_route(route)
+    if route.ndim < 2:
+        raise ValueError("route must be a boolean tensor with at least two axes")
+    keys = route.shape[-1]
+    rows = route.numel() // keys
+    counts = torch.empty(route.shape[:-1], dtype=torch.int32, device=route.device)
+    indices = torch.empty(route.shape, dtype=torch.int32, device=route.device)
+    with torch.cuda.device(route.device):
+        status = lib.dsa_pack_rows(route.data_ptr(), rows, keys, counts.data_ptr(),
+                                   indices.data_ptr(), _stream_handle(route.device))
+    _lib.check(status, "dsa_pack_rows")
+    return counts, indices
+
+
+def permute_tokens(tensors, permutation, out=None, head_major=False):
+    """Gather along the token axis: out[n][b, t] = tensors[n][b, permutation[t]].
+
+    tensors: 1-3 CUDA tensors [B, T, H, D] sharing shape and dtype, any
+    strides with a contiguous last axis.  permutation: int32 [T] on the device.
+    Outputs are [B, T, H, D]; contiguous, or views of head-major (BHSD)
+    storage with ``head_major=True``.  Bit-exact.
+    """
+    lib = _lib.load()
+    tensors = list(tensors)
+    if not 1 <= len(tensors) <= 3:
+        raise ValueError("permute_tokens moves 1 to 3 tensors")
+    first = tensors[0]
+    for index, tensor in enumerate(tensors):
+        _require_cuda(f"tensor {index}", tensor)
+        if tensor.shape != first.shape or tensor.dtype != first.dtype:
+            raise ValueError("tensors must share shape and dtype")
+        if tensor.ndim != 4:
+            raise ValueError("tensors must have shape [batch, tokens, heads, dim]")
+    _require_cuda("permutation", permutation)
+    if permutation.ndim != 1 or permutation.numel() != first.shape[1]:
+        raise ValueError("permutation must contain one index per token")
+    permutation = permutation.to(torch.int32).contiguous()
+    batch, tokens, heads, dim = first.shape
+    element = first.element_size()
+    sources = []
+    for tensor in tensors:
+        ok = (tensor.stride(3) == 1
+              and all((stride * element) % 16 == 0 for stride in tensor.stride()[:3])
+              and tensor.data_ptr() % 16 == 0)
+        sources.append(tensor if ok else tensor.contiguous())
+    if out is None:
+        if head_major:
+            out = [torch.empty((batch, heads, tokens, dim), dtype=first.dtype,
+                               device=first.device).transpose(1, 2) for _ in sources]
+        else:
+            out = [torch.empty_like(first, memory_format=torch.contiguous_format)
+                   for _ in sources]
+    if (dim * element) % 16 != 0:
+        raise ValueError("rows must be a multiple of 16 bytes")
+    src_strides = _lib.int64_array(
+        [s * element for tensor in sources for s in tensor.stride()[:3]])
+    dst_strides = _lib.int64_array(
+        [s * element for tensor in out for s in tensor.stride()[:3]])
+    with torch.cuda.device(first.device):
+        status = lib.dsa_permute_rows(
+            len(sources), _lib.pointer_array([t.data_ptr() for t in sources]),
+            _lib.pointer_array([t.data_ptr() for t in out]), src_strides, dst_strides,
+            permutation.data_ptr(), batch, tokens, heads, dim * element,
+            _stream_handle(first.device))
+    _lib.check(status, "dsa_permute_rows")
+    return out

@@ -1,0 +1,122 @@
+/*
+ * libdsa: MI355X (gfx950) block-sparse self-attention hot path, C ABI.
+ *
+ * Drop-in device layer under the reference study's attention backends
+ * (yangshuo1230/DiT_Sparse_Atten, attention_backends/).  The reference is
+ * Python; its Python callers bind these symbols with ctypes (see
+ * dit_sparse_atten_amd/_lib.py).  Conventions:
+ *   - tensors are device pointers; bf16 is IEEE bfloat16, route/boolean
+ *     tensors are one byte per entry (0 / 1), indices are int32;
+ *   - q/k/v/o use [batch, tokens, heads, head_dim] logical order with
+ *     arbitrary batch/token/head strides (in elements) and a contiguous head dim;
+ *   - every call is asynchronous on `stream`, allocates nothing, and returns
+ *     0 on success or a negative status (DSA_EINVAL = -1 invalid argument,
+ *     DSA_EUNSUPPORTED = -2 valid but unsupported shape, DSA_ELAUNCH = -3 HIP
+ *     error); dsa_last_error() describes the last failure on this thread.
+ */
+#ifndef DSA_H_
+#define DSA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version (1). */
+int dsa_version(void);
+
+/* Message of the last failed call on the calling thread ("" if none). */
+const char* dsa_last_error(void);
+
+/*
+ * Block-sparse attention forward, bf16 in / bf16 out, fp32 online softmax.
+ * Replaces FlexAttention over a BlockMask (attention_backends/flex.py:379-399
+ * `_flex_output`, flex.py:360-376) and, with row_ptr == col_idx == NULL, dense
+ * SDPA (attention_backends/dense.py:14-48).
+ *   strides[12]: q (b,t,h), k (b,t,h), v (b,t,h), o (b,t,h), in elements,
+ *                each a multiple of 8; pointers 16-byte aligned.
+ *   head_dim: 128.  block_size: 128.
+ *   row_ptr/col_idx: CSR over rows ((rb * heads + h) * q_blocks + qb), rb <
+ *                route_batches (1 = shared by all batch items, else = batch);
+ *                col_idx lists key blocks (ascending order not required).
+ *                Requires q_tokens == kv_tokens.  Out-of-range key blocks are
+ *                skipped; a row with no key blocks yields zeros.
+ *   scale: softmax scale (d^-1/2 for softmax_scale=None).
+ *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
+ * Keys past kv_tokens in a partial last block are masked.
+ */
+int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, const int64_t* strides,
+                int32_t batch, int32_t q_tokens, int32_t kv_tokens, int32_t heads,
+                int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
+                const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
+                hipStream_t stream);
+
+/*
+ * Sampled block-mass estimate for one batch-1 self-attention call.
+ * Replaces `_sampled_block_mass` (attention_backends/flex.py:205-251):
+ * `samples` evenly spaced tokens per block, scores rounded like a bf16 matmul
+ * and bf16 scale multiply, fp32 softmax over all sampled keys plus
+ * log(block size / samples), mass[h, qb, kb] = mean over query samples of the
+ * sum over key samples.  strides[4]: q (t, h), k (t, h) in elements.
+ * samples: power of two <= min(32, block_size).  mass: [heads, blocks, blocks].
+ */
+int dsa_sampled_mass(const void* q, const void* k, const int64_t* strides, int32_t tokens,
+                     int32_t heads, int32_t head_dim, int32_t block_size, int32_t samples,
+                     float scale, float* mass, hipStream_t stream);
+
+/*
+ * Persistence prior + top-mass selection + first-frame sink, per row.
+ * Replaces the prior of `_sampled_route` (flex.py:535-541), `_top_mass_route`
+ * (flex.py:83-94, == sparse.py:171-181 `_row_mask`) and `_add_first_frame_sink`
+ * (flex.py:550-566).  mass: [rows, keys] fp32, non-negative; previous: [rows,
+ * keys] bytes or NULL (no prior); cap = max(1, ceil(keys * keep)); the first
+ * sink_blocks columns are set after the cap.  keys <= 512.  Outputs route
+ * [rows, keys] bytes and counts [rows] (selected blocks per row, sink included).
+ */
+int dsa_route_select(const float* mass, const uint8_t* previous, int32_t rows, int32_t keys,
+                     float rho, float target, int32_t cap, int32_t sink_blocks, uint8_t* route,
+                     int32_t* counts, hipStream_t stream);
+
+/*
+ * Boolean route rows -> CSR (ascending key blocks per row).
+ * Replaces the KV half of `_build_block_mask` / `_pack_route`
+ * (flex.py:275-338; full_kv_num_blocks / full_kv_indices).  counts may be
+ * given (e.g. from dsa_route_select) or NULL, in which case counts_out
+ * receives them.  row_ptr: [rows + 1]; col_idx: capacity >= number of set
+ * entries; nnz (optional, device int64) receives the total.
+ */
+int dsa_route_to_csr(const uint8_t* route, int32_t rows, int32_t keys,
+                     const int32_t* counts_or_null, int32_t* counts_out, int32_t* row_ptr,
+                     int32_t* col_idx, int64_t* nnz, hipStream_t stream);
+
+/*
+ * Stable partition of boolean rows: per row, the selected column ids
+ * ascending, then the unselected ones ascending; counts = selected per row.
+ * Replaces `pack_boolean_rows` (attention_backends/layout_ops.py:128-151).
+ * indices: [rows, keys] int32.
+ */
+int dsa_pack_rows(const uint8_t* route, int32_t rows, int32_t keys, int32_t* counts,
+                  int32_t* indices, hipStream_t stream);
+
+/*
+ * Token gather for 1-3 tensors: dst[n][b, t, h, :] = src[n][b, perm[t], h, :].
+ * Replaces `reorder_qkv` (attention_backends/layout_ops.py:86-125) with the
+ * permutation, and `SpatialTokenLayout.restore` (spatial.py:91-93) with the
+ * inverse.  Strides are in BYTES: [n*3 + (b, t, h)]; row_bytes (head_dim *
+ * element size) and strides multiples of 16.  Rows whose perm entry is out of
+ * range are left untouched.
+ */
+int dsa_permute_rows(int32_t tensors, const void* const* src, void* const* dst,
+                     const int64_t* src_strides, const int64_t* dst_strides,
+                     const int32_t* perm, int32_t batch, int32_t tokens, int32_t heads,
+                     int32_t row_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_H_ */
