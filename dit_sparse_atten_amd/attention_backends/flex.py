@@ -1,0 +1,453 @@
+"""Hybrid block-sparse backend with sampled, reusable routes (``flex_reuse``).
+
+Mirrors attention_backends/flex.py of the reference, with FlexAttention and
+BlockMask replaced by the libdsa HIP kernels and a CSR route:
+  FlexReuseConfig / validation      flex.py:43-80, 407-443
+  _top_mass_route                   flex.py:83-94      -> dsa_route_select
+  _sampled_block_mass               flex.py:205-251    -> dsa_sampled_mass
+  _pack_route / _build_block_mask   flex.py:275-355    -> dsa_pack_rows / dsa_route_to_csr
+  _flex_output                      flex.py:379-399    -> dsa_bsa_fwd
+  FlexReuseBackend state machine    flex.py:402-850    (same phases, keys, dispatch,
+                                                        prefetch stream and release)
+Step 0 returns dense output; later steps reuse, update (sampled) or dispatch
+high-keep routes to the dense kernel.  Not in this build: the exact
+(dense + LSE + second QK pass) bootstrap and refresh, and the directional
+frontier update; configurations that need them raise ``NotImplementedError``
+at construction.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from .. import ops
+from .context import routing_context
+from .dense import DenseBackend, install
+from .layout_ops import pack_boolean_rows
+from .spatial import build_spatial_layout
+
+
+@dataclass(frozen=True)
+class FlexReuseConfig:
+    block_size: int = 128
+    keep: float = 0.625
+    mass_target: float = 0.90
+    # Kept for signature compatibility; the HIP kernels need no compilation.
+    compile_kernel: bool = True
+    # 0 keeps the step-0 route static; a positive value asks for an exact
+    # dense refresh every N steps (not in this build).
+    update_interval: int = 0
+    # A positive value updates from sampled Q/K blocks every N steps.
+    sampled_update_interval: int = 0
+    route_samples: int = 2
+    sample_query_block_chunk: int = 16
+    route_persistence: float = 0.5
+    prefetch_sampled_update: bool = True
+    prefetch_sampled_bootstrap: bool = True
+    total_steps: int | None = None
+    bootstrap_mode: str = "exact"
+    # Routes at or above this keep fraction run on the dense kernel; None
+    # disables automatic per-layer/branch dispatch.
+    dense_route_threshold: float | None = None
+    release_after_final_step: bool = True
+    spatial_reorder: bool = False
+    spatial_microtile_tokens: int = 32
+    directional_update: bool = False
+    direction_min_ratio: float = 0.0
+    direction_candidate_bonus: float = 0.0
+    route_budget_scale: float = 1.0
+    route_exploration_fraction: float = 0.0
+    direction_expand_q: bool = True
+    direction_expand_k: bool = True
+    direction_expand_joint: bool = True
+    # Wan's first latent frame is a globally visible key sink.
+    first_frame_sink: bool = True
+    # Keep the first transformer layer exact on every denoising pass.
+    first_layer_dense: bool = True
+
+
+def _top_mass_route(mass, target, keep):
+    """Select K blocks independently for every (head, query-block) row."""
+    route, _ = ops.route_select(mass, target, keep)
+    return route
+
+
+def _sampled_block_mass(q, k, block_size, samples=2, scale=None, query_block_chunk=16):
+    """Estimate block mass from evenly sampled Q/K tokens per block.
+
+    One fused kernel scans every sampled key twice per query tile, so no chunk
+    of the sampled score matrix is ever materialised (``query_block_chunk`` is
+    accepted for signature compatibility).
+    """
+    if query_block_chunk <= 0:
+        raise ValueError("sample_query_block_chunk must be positive")
+    return ops.sampled_block_mass(q, k, block_size, samples, scale)
+
+
+def _pack_route(route):
+    """Pack a boolean [H,Q,K] route into counts and compact K indices."""
+    counts, indices = pack_boolean_rows(route)
+    return counts.unsqueeze(0), indices.unsqueeze(0)
+
+
+def _build_block_mask(route, tokens, block_size, counts=None):
+    """Convert a [H,Q,K] route to the CSR the attention kernel walks."""
+    if route.ndim != 3 or route.shape[-2] != route.shape[-1]:
+        raise ValueError("route must have shape [head, Q-block, K-block]")
+    if math.ceil(tokens / block_size) != route.shape[-1]:
+        raise ValueError("route does not match the token count")
+    return ops.route_to_csr(route, counts, block_size=block_size)
+
+
+def _flex_output(q, k, v, block_mask, block_size, compile_kernel=True, scale=None):
+    """Block-sparse attention of [B, T, H, D] tensors over a CSR route.
+
+    Partial last blocks are masked inside the kernel, so no padding copies are
+    made; the output is contiguous [B, T, H, D].
+    """
+    del compile_kernel
+    return ops.bsa_fwd(q, k, v, block_mask, scale=scale, block_size=block_size)
+
+
+def _route_keep(block_mask):
+    """route.float().mean() from the CSR's device nnz (one 8-byte read)."""
+    total = block_mask.route_batches * block_mask.heads * block_mask.q_blocks * block_mask.k_blocks
+    return float(np.float32(block_mask.nnz_value()) / np.float32(total))
+
+
+class FlexReuseBackend:
+    """Sampled bootstrap followed by route reuse, updates and dense dispatch."""
+
+    name = "flex_reuse"
+
+    def __init__(self, config=None):
+        self.config = config or FlexReuseConfig()
+        c = self.config
+        if c.block_size != 128:
+            raise ValueError(
+                "The minimal flex_reuse backend currently supports only 128-token blocks")
+        if c.update_interval < 0:
+            raise ValueError("update_interval must be zero or a positive integer")
+        if c.sampled_update_interval < 0:
+            raise ValueError("sampled_update_interval must be zero or a positive integer")
+        if c.update_interval and c.sampled_update_interval:
+            raise ValueError("exact and sampled route updates are mutually exclusive")
+        if not 0 < c.route_samples <= c.block_size:
+            raise ValueError("route_samples must be in [1, block_size]")
+        if c.route_persistence < 0:
+            raise ValueError("route_persistence must be non-negative")
+        if c.bootstrap_mode not in ("exact", "sampled"):
+            raise ValueError("bootstrap_mode must be 'exact' or 'sampled'")
+        if c.dense_route_threshold is not None and not 0 < c.dense_route_threshold <= 1:
+            raise ValueError("dense_route_threshold must be in (0, 1]")
+        if not 0 < c.keep <= 1:
+            raise ValueError("keep must be in (0, 1]")
+        if not 0 < c.mass_target <= 1:
+            raise ValueError("mass_target must be in (0, 1]")
+        if c.spatial_microtile_tokens <= 0:
+            raise ValueError("spatial_microtile_tokens must be positive")
+        if c.direction_min_ratio < 0:
+            raise ValueError("direction_min_ratio must be non-negative")
+        if c.direction_candidate_bonus < 0:
+            raise ValueError("direction_candidate_bonus must be non-negative")
+        if c.route_budget_scale <= 0:
+            raise ValueError("route_budget_scale must be positive")
+        if not 0 <= c.route_exploration_fraction <= 1:
+            raise ValueError("route_exploration_fraction must be in [0, 1]")
+        if c.directional_update and not c.spatial_reorder:
+            raise ValueError("directional_update requires spatial_reorder")
+        if c.route_samples > 32 or c.route_samples & (c.route_samples - 1):
+            raise ValueError("route_samples must be a power of two <= 32 on the libdsa kernels")
+        if c.bootstrap_mode == "exact" or c.update_interval:
+            raise NotImplementedError(
+                "exact route bootstrap/refresh is not part of this build; "
+                "use bootstrap_mode='sampled' (optionally with sampled_update_interval)")
+        if c.directional_update:
+            raise NotImplementedError("the directional frontier update is not part of this build")
+        self.dense = DenseBackend()
+        self.state = {}
+        self.route_streams = {}
+        self.spatial_layouts = {}
+        self.phase_counts = {
+            "dense_bootstrap": 0,
+            "sampled_bootstrap": 0,
+            "exact_refresh": 0,
+            "sampled_update": 0,
+            "sparse_reuse": 0,
+            "dense_dispatch": 0,
+            "first_layer_dense": 0,
+        }
+        self.finished_routes = []
+
+    # -- route state -----------------------------------------------------
+
+    def _activate_pending_route(self, state):
+        pending = state.pop("pending", None)
+        if pending is None:
+            return
+        torch.cuda.current_stream(pending["route"].device).wait_event(pending["ready"])
+        state.update({
+            "route": pending["route"],
+            "frontier": pending.get("frontier"),
+            "block_mask": pending["block_mask"],
+            "step": pending["source_step"],
+        })
+        self._update_dispatch(state)
+
+    def _update_dispatch(self, state):
+        threshold = self.config.dense_route_threshold
+        block_mask = state.get("block_mask")
+        keep = (_route_keep(block_mask)
+                if state.get("route") is not None and block_mask is not None else None)
+        state["keep"] = keep
+        state["frontier_fraction"] = None
+        state["dense"] = bool(threshold is not None and keep is not None and keep >= threshold)
+        if state["dense"]:
+            # A permanently dense state never reads its route again.
+            state["route"] = None
+            state["block_mask"] = None
+            state["frontier"] = None
+
+    def _is_final_step(self, step):
+        return (self.config.release_after_final_step
+                and self.config.total_steps is not None
+                and step >= self.config.total_steps - 1)
+
+    def _release_route(self, key, state):
+        self.finished_routes.append({
+            "keep": state.get("keep"),
+            "frontier_fraction": state.get("frontier_fraction"),
+            "dense": bool(state.get("dense")),
+        })
+        self.state.pop(key, None)
+
+    def _sink_blocks(self, state):
+        grid = state.get("grid")
+        if not self.config.first_frame_sink or grid is None:
+            return 0
+        return math.ceil((grid[1] * grid[2]) / self.config.block_size)
+
+    def _sampled_route(self, state, q, k, softmax_scale):
+        mass = _sampled_block_mass(
+            q, k, self.config.block_size,
+            samples=self.config.route_samples,
+            scale=softmax_scale,
+            query_block_chunk=self.config.sample_query_block_chunk,
+        )
+        previous = state.get("route")
+        use_prior = bool(self.config.route_persistence) and previous is not None
+        route, counts = ops.route_select(
+            mass, self.config.mass_target, self.config.keep,
+            previous=previous if use_prior else None,
+            persistence=self.config.route_persistence if use_prior else 0.0,
+            sink_blocks=self._sink_blocks(state))
+        return {"route": route, "frontier": None, "counts": counts}
+
+    def _add_first_frame_sink(self, state, result):
+        if not self.config.first_frame_sink:
+            return result
+        sink = self._sink_blocks(state)
+        if not sink:
+            return result
+        route = result["route"].clone()
+        route[..., :sink] = True
+        result = dict(result)
+        result["route"] = route
+        result.pop("counts", None)
+        return result
+
+    def _install_route(self, state, result, tokens):
+        route = result["route"]
+        state.update({
+            "route": route,
+            "frontier": result.get("frontier"),
+            "block_mask": _build_block_mask(route, tokens, self.config.block_size,
+                                            result.get("counts")),
+        })
+
+    def _spatial_layout(self, grid, tokens):
+        if not self.config.spatial_reorder:
+            return None
+        if grid is None or math.prod(grid) != tokens:
+            return None
+        key = (tuple(grid), self.config.block_size, self.config.spatial_microtile_tokens)
+        if key not in self.spatial_layouts:
+            self.spatial_layouts[key] = build_spatial_layout(
+                grid, self.config.block_size, self.config.spatial_microtile_tokens)
+        return self.spatial_layouts[key]
+
+    def _prefetch_sampled_route(self, state, q, k, step, softmax_scale,
+                                phase="sampled_update"):
+        # Default stream priority on purpose.
+        stream = self.route_streams.setdefault(q.device, torch.cuda.Stream(device=q.device))
+        attention_done = torch.cuda.Event()
+        attention_done.record(torch.cuda.current_stream(q.device))
+        stream.wait_event(attention_done)
+        with torch.cuda.stream(stream):
+            q.record_stream(stream)
+            k.record_stream(stream)
+            result = self._sampled_route(state, q, k, softmax_scale)
+            route = result["route"]
+            block_mask = _build_block_mask(route, q.shape[1], self.config.block_size,
+                                           result.get("counts"))
+            ready = torch.cuda.Event()
+            ready.record(stream)
+        state["pending"] = {
+            "route": route,
+            "frontier": result.get("frontier"),
+            "block_mask": block_mask,
+            "source_step": step,
+            "ready": ready,
+        }
+        self.phase_counts[phase] += 1
+
+    def profile_summary(self):
+        active = [state for state in self.state.values() if state.get("route") is not None]
+        keep = [state.get("keep") for state in active] + [
+            state["keep"] for state in self.finished_routes if state["keep"] is not None]
+        frontier = [state.get("frontier_fraction") for state in active
+                    if state.get("frontier_fraction") is not None] + [
+            state["frontier_fraction"] for state in self.finished_routes
+            if state["frontier_fraction"] is not None]
+        return {
+            "phase_counts": dict(self.phase_counts),
+            "active_routes": len(active),
+            "released_routes": len(self.finished_routes),
+            "mean_route_keep": sum(keep) / len(keep) if keep else None,
+            "mean_frontier_fraction": sum(frontier) / len(frontier) if frontier else None,
+            "dense_dispatched_routes": sum(
+                bool(state.get("dense")) for state in self.state.values())
+            + sum(state["dense"] for state in self.finished_routes),
+        }
+
+    # -- call ------------------------------------------------------------
+
+    def __call__(
+        self,
+        q,
+        k,
+        v,
+        q_lens=None,
+        k_lens=None,
+        dropout_p=0.0,
+        softmax_scale=None,
+        q_scale=None,
+        causal=False,
+        window_size=(-1, -1),
+        deterministic=False,
+        dtype=torch.bfloat16,
+        version=None,
+        **kwargs,
+    ):
+        dense_kwargs = dict(q_lens=q_lens, k_lens=k_lens, dropout_p=dropout_p,
+                            softmax_scale=softmax_scale, q_scale=q_scale, causal=causal,
+                            window_size=window_size, deterministic=deterministic,
+                            dtype=dtype, version=version, **kwargs)
+        supported = (
+            q.shape[0] == 1
+            and q.shape[1] == k.shape[1]
+            and dropout_p == 0
+            and not causal
+            and window_size == (-1, -1)
+        )
+        if not supported:
+            return self.dense(q, k, v, **dense_kwargs)
+
+        attention_id, step, branch, grid = routing_context(include_grid=True)
+        if self.config.first_layer_dense and attention_id == 0:
+            self.phase_counts["first_layer_dense"] += 1
+            return self.dense(q, k, v, **dense_kwargs)
+        layout = self._spatial_layout(grid, q.shape[1])
+        if self.config.spatial_reorder and layout is None:
+            return self.dense(q, k, v, **dense_kwargs)
+
+        output_dtype = q.dtype
+        q = q.to(dtype)
+        k = k.to(dtype)
+        v = v.to(dtype)
+        if q_scale is not None:
+            q = q * q_scale
+        if layout is not None:
+            q, k, v = layout.reorder_qkv(q, k, v)
+
+        def finish(output):
+            if layout is not None:
+                output = layout.restore(output)
+            return output.to(output_dtype)
+
+        def dense_output():
+            return self.dense(q, k, v, dropout_p=0.0, softmax_scale=softmax_scale,
+                              q_scale=None, causal=False, window_size=(-1, -1), dtype=dtype)
+
+        key = (attention_id, branch, q.shape[1], q.shape[2], q.shape[3], q.device,
+               layout.signature if layout is not None else None)
+        if step == 0 or key not in self.state:
+            # Sampled bootstrap: complete dense output, route from samples.
+            output = dense_output()
+            state = {
+                "route": None,
+                "frontier": None,
+                "block_mask": None,
+                "step": step,
+                "layout": layout,
+                "grid": grid,
+            }
+            self.state[key] = state
+            if (self.config.prefetch_sampled_bootstrap
+                    and (self.config.total_steps is None
+                         or step < self.config.total_steps - 1)):
+                self._prefetch_sampled_route(state, q, k, step, softmax_scale,
+                                             phase="sampled_bootstrap")
+            else:
+                result = self._sampled_route(state, q, k, softmax_scale)
+                self._install_route(state, result, q.shape[1])
+                self._update_dispatch(state)
+                self.phase_counts["sampled_bootstrap"] += 1
+            if self._is_final_step(step):
+                self._release_route(key, self.state[key])
+            return finish(output)
+
+        state = self.state[key]
+        self._activate_pending_route(state)
+        if state.get("dense"):
+            self.phase_counts["dense_dispatch"] += 1
+            output = dense_output()
+            if self._is_final_step(step):
+                self._release_route(key, state)
+            return finish(output)
+
+        sampled_update_due = (
+            self.config.sampled_update_interval > 0
+            and (step - state["step"]) >= self.config.sampled_update_interval
+            and (self.config.total_steps is None or step < self.config.total_steps - 1)
+        )
+        if sampled_update_due and not self.config.prefetch_sampled_update:
+            # The old route will not execute this step; drop it before the
+            # replacement is built.
+            state["block_mask"] = None
+            result = self._sampled_route(state, q, k, softmax_scale)
+            self._install_route(state, result, q.shape[1])
+            state["step"] = step
+            self._update_dispatch(state)
+            self.phase_counts["sampled_update"] += 1
+            if state.get("dense"):
+                self.phase_counts["dense_dispatch"] += 1
+                return finish(dense_output())
+
+        output = _flex_output(q, k, v, state["block_mask"], self.config.block_size,
+                              scale=softmax_scale)
+        self.phase_counts["sparse_reuse"] += 1
+        if self.config.prefetch_sampled_update and sampled_update_due:
+            state["block_mask"] = None
+            self._prefetch_sampled_route(state, q, k, step, softmax_scale)
+        if self._is_final_step(step):
+            self._release_route(key, state)
+        return finish(output)
+
+
+def install_flex_reuse(config=None):
+    return install(FlexReuseBackend(config))

@@ -75,8 +75,9 @@ def sparse_chunk(q, k, v, route_mask, tile, start, end, scale, stats=None, offse
     padded, valid = group_indices(group_mask, tile)
     selected_k = k[0, padded, group_heads[:, None]]
     selected_v = v[0, padded, group_heads[:, None]]
-    logits = np.matmul(grouped_q, selected_k.transpose(0, 2, 1)) * np.float32(scale)
-    logits = np.where(valid[:, None], logits, _F32_MIN).astype(np.float32)
+    logits = np.matmul(grouped_q, selected_k.transpose(0, 2, 1))
+    logits *= np.float32(scale)
+    np.copyto(logits, _F32_MIN, where=~valid[:, None])
     probabilities = _softmax(logits)
     output = np.matmul(probabilities, selected_v)
     output = output.reshape(query_tiles, heads, tile, -1).transpose(0, 2, 1, 3).reshape(
