@@ -49,7 +49,22 @@ def parse_args():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--only-sparse", action="store_true",
                         help="time only the sparse call (profiling runs)")
+    parser.add_argument("--copy-calibration-mib", type=int, default=0,
+                        help="run only a plain device copy of this many MiB (scales the "
+                             "FETCH_SIZE / WRITE_SIZE counters) and exit")
     return parser.parse_args()
+
+
+def copy_calibration(mib):
+    """A plain copy of known size, profiled with the same HBM counters."""
+    device = torch.device("cuda:0")
+    count = mib * 2 ** 20
+    src = torch.ones(count, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": count, "launches": 3}), flush=True)
 
 
 def clustered_inputs(device, seed=0):
@@ -162,6 +177,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration_mib:
+        copy_calibration(args.copy_calibration_mib)
+        return
 
     from dit_sparse_atten_amd import ops
 
@@ -232,7 +250,7 @@ def main():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
     result["roofline"] = {
         "bound": "mfma",
-        "kernel": "bsa_fwd_kernel<128>",
+        "kernel": "bsa_fwd_kernel (+ vt_transpose_kernel)",
         "achieved": round(achieved, 2),
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",

@@ -36,8 +36,10 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int,    # batch, q_tokens, kv_tokens, heads, head_dim
         _c_int,                                    # block_size
         _c_ptr, _c_ptr, _c_int,                    # row_ptr, col_idx, route_batches
-        _c_float, _c_ptr, _c_ptr,                  # scale, lse, stream
+        _c_float, _c_ptr,                          # scale, lse
+        _c_ptr, _c_size, _c_ptr,                   # workspace, workspace_bytes, stream
     )),
+    "dsa_bsa_workspace_bytes": (_c_size, (_c_int, _c_int, _c_int, _c_int)),
     "dsa_sampled_mass": (_c_int, (
         _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
         _c_int, _c_int, _c_int, _c_int, _c_int,    # tokens, heads, head_dim, block, samples

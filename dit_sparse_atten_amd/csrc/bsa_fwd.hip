@@ -1,4 +1,4 @@
-// Block-sparse attention forward for gfx950 (MI355X), bf16 in/out, fp32 softmax.
+// Block-sparse attention forward for gfx950 (MI355X): bf16 in/out, fp32 softmax.
 //
 // Replaces the FlexAttention call of the reference backend
 // (attention_backends/flex.py:379-399 `_flex_output`, kernel options
@@ -7,19 +7,23 @@
 // Semantics per (batch b, head h, query row t):
 //   O[b,t,h,:] = softmax_k( scale * <Q[b,t,h,:], K[b,k,h,:]> ) @ V[b,k,h,:]
 // where k ranges over the tokens of every key block listed in the CSR row of
-// (route batch, h, t / BLOCK).  Without a CSR every key block is listed (dense
+// (route batch, h, t / 128).  Without a CSR every key block is listed (dense
 // fallback).  Keys past `kv_tokens` in a partial last block are masked.
 //
-// Work decomposition: one workgroup (4 wave64s) per (b, h, query block of 128
-// rows); wave w owns query rows 32w..32w+31, one row per lane pair (l, l^32).
-// S^T = K Q^T is computed with v_mfma_f32_32x32x16_bf16 so that each lane's
-// accumulators belong to a single query row: the online-softmax max/sum stay
-// in registers and need one cross-half exchange.  P^T leaves the accumulators
-// already in the B-operand layout of O^T = V^T P^T; the V tile is transposed
-// into LDS with its keys stored in the matching order.
+// Design (per 128-row query block, one 4-wave workgroup, two per CU):
+//  * wave w owns query rows 32w..32w+31; S^T = K Q^T uses
+//    v_mfma_f32_32x32x16_bf16 so each lane's accumulators belong to one query
+//    row (row max / sum stay in registers, one cross-half exchange) and P^T
+//    leaves the accumulators already in the B-operand layout of O^T = V^T P^T;
+//  * keys stream as 64-key half-tiles, double-buffered in LDS by direct
+//    global->LDS loads issued one half-tile ahead; the two stages are distinct
+//    LDS objects so reads of one never wait on the DMA into the other;
+//  * V is first transposed into a V^T workspace whose 16-key groups store
+//    their 4-key quads as 0, 2, 1, 3 (the key order of the P^T slots), so both
+//    MFMA operands are conflict-free 16-byte LDS reads;
+//  * online softmax with a lazily moved reference max (rescale only when a
+//    score exceeds it by 2^8) and row sums from the bf16 P with dot2.
 #include "dsa_common.h"
-
-#include <stdlib.h>
 
 namespace {
 
@@ -41,766 +45,68 @@ struct BsaParams {
 };
 
 constexpr int kHeadDim = 128;
-constexpr int kRowBytes = kHeadDim * 2;  // one K row / one V^T row: 256 bytes
-
-// LDS position (16-byte units within a 256-byte row) of K chunk `c` of key row
-// `r`.  Rows are XOR-swizzled so 16 consecutive rows read at one chunk hit 16
-// distinct bank groups.
-__device__ __forceinline__ int k_swz(int r, int c) { return c ^ (r & 15); }
-
-// LDS position of logical key chunk `c` (8 keys) of V^T row `d`.  The second
-// term makes the transposing writes (rows 8 apart) conflict-free as well.
-__device__ __forceinline__ int v_swz(int d, int c) {
-  return c ^ (d & 15) ^ ((d >> 3) & 15);
-}
-
-template <int BLOCK>
-__global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p) {
-  static_assert(BLOCK == 128, "this kernel tiles 128-token blocks");
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k[BLOCK * kRowBytes];
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_v[kHeadDim * BLOCK * 2];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int g = lane >> 5;   // half-wave: selects the 8-element K-slice
-  const int qi = lane & 31;  // MFMA row/column owned by this lane
-
-  const int work = dsa::xcd_remap(blockIdx.x, gridDim.x);
-  const int qb = work % p.q_blocks;
-  const int bh = work / p.q_blocks;
-  const int h = bh % p.heads;
-  const int b = bh / p.heads;
-
-  int start = 0, end = p.kv_blocks;
-  if (p.row_ptr) {
-    const int rb = p.route_batches == 1 ? 0 : b;
-    const int64_t row = ((int64_t)rb * p.heads + h) * p.q_blocks + qb;
-    start = p.row_ptr[row];
-    end = p.row_ptr[row + 1];
-  }
-
-  // Q^T fragments (B operand of S^T = K Q^T): lane holds 8 consecutive head
-  // dims of its query row for each of the 8 K-steps of 16.
-  const int tq = qb * BLOCK + wave * 32 + qi;
-  const int tq_c = tq < p.q_tokens ? tq : p.q_tokens - 1;
-  const __bf16* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)tq_c * p.q_st;
-  dsa_bf16x8 qf[8];
-#pragma unroll
-  for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
-
-  const __bf16* kbase = p.k + b * p.k_sb + h * p.k_sh;
-  const __bf16* vbase = p.v + b * p.v_sb + h * p.v_sh;
-
-  float m_run = -INFINITY;  // running max of raw scores <q,k>
-  float l_run = 0.f;        // running sum of this half-wave's probabilities
-  dsa_f32x16 oacc[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-
-  for (int it = start; it < end; ++it) {
-    const int kb = p.row_ptr ? p.col_idx[it] : it;
-    if ((unsigned)kb >= (unsigned)p.kv_blocks) continue;  // malformed index: skip
-    const int key0 = kb * BLOCK;
-
-    __syncthreads();  // previous tile fully consumed
-
-    // K tile -> LDS, direct from global (16 B per lane); the source chunk is
-    // chosen so that the linear LDS image is the swizzled layout.
-#pragma unroll
-    for (int j = 0; j < BLOCK * 16 / 256; ++j) {
-      const int chunk_base = (wave * (BLOCK * 16 / 256) + j) * 64;
-      const int idx = chunk_base + lane;
-      const int row = idx >> 4;
-      const int c = (idx & 15) ^ (row & 15);
-      int key = key0 + row;
-      key = key < p.kv_tokens ? key : p.kv_tokens - 1;
-      const __bf16* src = kbase + (int64_t)key * p.k_st + c * 8;
-      __builtin_amdgcn_global_load_lds(
-          src, (DSA_LDS void*)(lds_k + chunk_base * 16), 16, 0, 0);
-    }
-
-    // V tile -> registers -> transposed V^T in LDS.  Thread (kg, c) owns head
-    // dims 8c..8c+7 of the 8 keys that form logical key chunk kg.
-    {
-      const int kg = tid >> 4;
-      const int c = tid & 15;
-      const int grp = kg >> 1, half = kg & 1;
-      dsa_u32x4 vr[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int key = key0 + grp * 16 + 4 * half + (i & 3) + 8 * (i >> 2);
-        key = key < p.kv_tokens ? key : p.kv_tokens - 1;
-        vr[i] = *reinterpret_cast<const dsa_u32x4*>(vbase + (int64_t)key * p.v_st + c * 8);
-      }
-#pragma unroll
-      for (int dd = 0; dd < 8; ++dd) {
-        dsa_u32x4 out;
-        const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-          out[w] = __builtin_amdgcn_perm(vr[2 * w + 1][dd >> 1], vr[2 * w][dd >> 1], sel);
-        const int d = c * 8 + dd;
-        *reinterpret_cast<dsa_u32x4*>(lds_v + d * (BLOCK * 2) + v_swz(d, kg) * 16) = out;
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    // S^T = K Q^T: 4 sub-tiles of 32 keys x 32 query rows.
-    dsa_f32x16 sacc[4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
-#pragma unroll
-    for (int dc = 0; dc < 8; ++dc) {
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const int key = kt * 32 + qi;
-        const int c = dc * 2 + g;
-        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
-            lds_k + key * kRowBytes + k_swz(key, c) * 16);
-        sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], sacc[kt], 0, 0, 0);
-      }
-    }
-
-    // Accumulator (kt, r) holds key kt*32 + 8*(r/4) + 4*g + r%4.
-    if (key0 + BLOCK > p.kv_tokens) {
-      const int valid = p.kv_tokens - key0;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= valid) sacc[kt][r] = -INFINITY;
-        }
-    }
-
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * p.scale_log2);
-    const float mb = m_use * p.scale_log2;
-
-    float rs = 0.f;
-    dsa_bf16x8 pf[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int kt = j >> 1, hf = j & 1;
-#pragma unroll
-      for (int t = 0; t < 8; t += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t], p.scale_log2, -mb));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t + 1], p.scale_log2, -mb));
-        rs += p0 + p1;
-        const dsa_f32x2 two = {p0, p1};
-        const dsa_bf16x2 pb = __builtin_convertvector(two, dsa_bf16x2);
-        pf[j][t] = pb[0];
-        pf[j][t + 1] = pb[1];
-      }
-    }
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-
-    // O^T += V^T P^T over 8 K-steps of 16 keys.
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const int d = dt * 32 + qi;
-        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
-            lds_v + d * (BLOCK * 2) + v_swz(d, 2 * j + g) * 16);
-        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[j], oacc[dt], 0, 0, 0);
-      }
-    }
-  }
-
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (tq < p.q_tokens) {
-    __bf16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const dsa_f32x2 lo = {oacc[dt][rr * 4 + 0] * inv, oacc[dt][rr * 4 + 1] * inv};
-        const dsa_f32x2 hi = {oacc[dt][rr * 4 + 2] * inv, oacc[dt][rr * 4 + 3] * inv};
-        const dsa_bf16x2 blo = __builtin_convertvector(lo, dsa_bf16x2);
-        const dsa_bf16x2 bhi = __builtin_convertvector(hi, dsa_bf16x2);
-        const dsa_bf16x4 v4 = {blo[0], blo[1], bhi[0], bhi[1]};
-        *reinterpret_cast<dsa_bf16x4*>(orow + dt * 32 + rr * 8 + g * 4) = v4;
-      }
-    if (p.lse && g == 0) {
-      p.lse[((int64_t)b * p.heads + h) * p.q_tokens + tq] =
-          l_tot > 0.f ? m_run * p.scale + logf(l_tot) : -INFINITY;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Pipelined variant: 4 waves x 32 query rows per 128-row block (2 blocks per
-// CU), keys streamed as 64-key half-tiles one step ahead of the compute: K by
-// direct global->LDS loads into a double buffer, V through registers into a
-// double-buffered transposed V^T.  One barrier per half-tile; lazy softmax
-// rescaling; row sums from the bf16 probabilities with dot2.
-// ---------------------------------------------------------------------------
-
-constexpr int kHalfKeys = 64;
-constexpr int kKStage = kHalfKeys * kRowBytes;    // 16 KB: [64 keys][128 dims]
-constexpr int kVtRow = kHalfKeys * 2;             // 128 B: one head dim, 64 keys
-constexpr int kVStage = kHeadDim * kVtRow;        // 16 KB: [128 dims][64 keys]
-constexpr float kRescaleLog2 = 8.0f;              // rescale once p could exceed 2^8
-
-// V^T half-tile: row = head dim (128 B, 8 chunks of 8 logical keys).  Even and
-// odd rows sit in different bank halves; XOR ((d >> 1) ^ (d >> 4)) & 7 makes
-// the 16 rows of a fragment read distinct and halves transposing-write clashes.
-__device__ __forceinline__ int vt_swz(int d, int c) { return c ^ (((d >> 1) ^ (d >> 4)) & 7); }
-
-__global__ void __launch_bounds__(256, 2) bsa_fwd3_kernel(BsaParams p) {
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k[2 * kKStage];
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_v[2 * kVStage];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int g = lane >> 5;
-  const int qi = lane & 31;
-
-  const int work = dsa::xcd_remap(blockIdx.x, gridDim.x);
-  const int qb = work % p.q_blocks;
-  const int bh = work / p.q_blocks;
-  const int h = bh % p.heads;
-  const int b = bh / p.heads;
-
-  int start = 0, end = p.kv_blocks;
-  if (p.row_ptr) {
-    const int rb = p.route_batches == 1 ? 0 : b;
-    const int64_t row = ((int64_t)rb * p.heads + h) * p.q_blocks + qb;
-    start = p.row_ptr[row];
-    end = p.row_ptr[row + 1];
-  }
-  const int nsub = 2 * (end - start);
-
-  const int tq = qb * 128 + wave * 32 + qi;
-  const int tq_c = tq < p.q_tokens ? tq : p.q_tokens - 1;
-  const __bf16* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)tq_c * p.q_st;
-  dsa_bf16x8 qf[8];
-#pragma unroll
-  for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
-
-  const __bf16* kbase = p.k + b * p.k_sb + h * p.k_sh;
-  const __bf16* vbase = p.v + b * p.v_sb + h * p.v_sh;
-
-  // Key block of half-tile `sub`, or -1 when the CSR entry is out of range.
-  auto block_of = [&](int sub) -> int {
-    const int it = start + (sub >> 1);
-    const int kb = p.row_ptr ? p.col_idx[it] : it;
-    return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
-  };
-  auto first_key = [&](int sub) -> int {
-    const int kb = block_of(sub);
-    return (kb < 0 ? 0 : kb) * 128 + (sub & 1) * kHalfKeys;
-  };
-
-  // V transposition duty: keys 4*vq..4*vq+3 of the half-tile, head dims 8*vc..8*vc+7.
-  const int vq = tid >> 4;
-  const int vc = tid & 15;
-  dsa_u32x4 vr[4];
-
-  auto issue = [&](int sub, int stage) {
-    const int key0 = first_key(sub);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int chunk_base = (wave * 4 + j) * 64;
-      const int idx = chunk_base + lane;
-      const int row = idx >> 4;
-      int key = key0 + row;
-      key = key < p.kv_tokens ? key : p.kv_tokens - 1;
-      const __bf16* src = kbase + (int64_t)key * p.k_st + k_swz(row, idx & 15) * 8;
-      __builtin_amdgcn_global_load_lds(
-          src, (DSA_LDS void*)(lds_k + stage * kKStage + chunk_base * 16), 16, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int key = key0 + vq * 4 + i;
-      key = key < p.kv_tokens ? key : p.kv_tokens - 1;
-      vr[i] = *reinterpret_cast<const dsa_u32x4*>(vbase + (int64_t)key * p.v_st + vc * 8);
-    }
-  };
-
-  // Logical key order inside each 16-key group swaps the two middle quads, so
-  // that V^T chunk (2j + g) holds exactly the keys of the P^T B-operand slots.
-  const int quad = vq & 3;
-  const int lkey = (vq >> 2) * 16 + (((quad & 1) << 1) | (quad >> 1)) * 4;
-  auto store_vt = [&](int stage) {
-    unsigned char* base = lds_v + stage * kVStage;
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-      const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-      dsa_u32x2 out;
-      out[0] = __builtin_amdgcn_perm(vr[1][dd >> 1], vr[0][dd >> 1], sel);
-      out[1] = __builtin_amdgcn_perm(vr[3][dd >> 1], vr[2][dd >> 1], sel);
-      const int d = vc * 8 + dd;
-      *reinterpret_cast<dsa_u32x2*>(base + d * kVtRow + vt_swz(d, lkey >> 3) * 16 +
-                                    (lkey & 7) * 2) = out;
-    }
-  };
-
-  float m_run = -INFINITY;  // reference max, log2-scaled units
-  float l_run = 0.f;        // this half-wave's partial row sum
-  dsa_f32x16 oacc[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-  const dsa_bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-
-  if (nsub > 0) issue(0, 0);
-  for (int sub = 0; sub < nsub; ++sub) {
-    const int stage = sub & 1;
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K stage and V registers landed
-    store_vt(stage);
-    __syncthreads();  // stage visible to all waves; the other stage is free
-    if (sub + 1 < nsub) issue(sub + 1, stage ^ 1);
-
-    const unsigned char* kt_lds = lds_k + stage * kKStage;
-    const unsigned char* vt_lds = lds_v + stage * kVStage;
-    const int kb = block_of(sub);
-    const int key0 = first_key(sub);
-    int valid = kb < 0 ? 0 : p.kv_tokens - key0;
-    valid = valid < kHalfKeys ? valid : kHalfKeys;
-
-    dsa_f32x16 sacc[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
-#pragma unroll
-    for (int dc = 0; dc < 8; ++dc) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int row = kt * 32 + qi;
-        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
-            kt_lds + row * kRowBytes + k_swz(row, dc * 2 + g) * 16);
-        sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], sacc[kt], 0, 0, 0);
-      }
-    }
-    if (valid < kHalfKeys) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= valid) sacc[kt][r] = -INFINITY;
-    }
-
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mx2 = mx * p.scale_log2;
-    const bool up = mx2 > m_run + kRescaleLog2;
-    if (__any(up)) {
-      const float alpha = up ? __builtin_amdgcn_exp2f(m_run - mx2) : 1.0f;
-      m_run = up ? mx2 : m_run;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-    }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-
-    dsa_bf16x8 pf[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kt = j >> 1, hf = j & 1;
-#pragma unroll
-      for (int t = 0; t < 8; t += 2) {
-        const float p0 =
-            __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t], p.scale_log2, -m_use));
-        const float p1 =
-            __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t + 1], p.scale_log2, -m_use));
-        const dsa_f32x2 two = {p0, p1};
-        const dsa_bf16x2 pb = __builtin_convertvector(two, dsa_bf16x2);
-        l_run = __builtin_amdgcn_fdot2_f32_bf16(pb, ones, l_run, false);
-        pf[j][t] = pb[0];
-        pf[j][t + 1] = pb[1];
-      }
-    }
-
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const int d = dt * 32 + qi;
-        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
-            vt_lds + d * kVtRow + vt_swz(d, 2 * j + g) * 16);
-        oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[j], oacc[dt], 0, 0, 0);
-      }
-    }
-  }
-
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (tq < p.q_tokens) {
-    __bf16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const dsa_f32x2 lo = {oacc[dt][rr * 4 + 0] * inv, oacc[dt][rr * 4 + 1] * inv};
-        const dsa_f32x2 hi = {oacc[dt][rr * 4 + 2] * inv, oacc[dt][rr * 4 + 3] * inv};
-        const dsa_bf16x2 blo = __builtin_convertvector(lo, dsa_bf16x2);
-        const dsa_bf16x2 bhi = __builtin_convertvector(hi, dsa_bf16x2);
-        const dsa_bf16x4 v4 = {blo[0], blo[1], bhi[0], bhi[1]};
-        *reinterpret_cast<dsa_bf16x4*>(orow + dt * 32 + rr * 8 + g * 4) = v4;
-      }
-    if (p.lse && g == 0) {
-      // m_run is in log2 units of scaled scores: lse = ln2 * m + ln(l).
-      p.lse[((int64_t)b * p.heads + h) * p.q_tokens + tq] =
-          l_tot > 0.f ? m_run * 0.6931471805599453f + logf(l_tot) : -INFINITY;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// v4: the v3 pipeline with uniform block indices read through scalar loads
-// (so waiting on them never drains the prefetch), per-lane load offsets
-// computed once, operand fragments staged in double-buffered groups of four,
-// and V^T rows placed so that the transposing writes use both bank halves.
-// ---------------------------------------------------------------------------
+constexpr int kRowBytes = kHeadDim * 2;        // one K row: 256 bytes
+constexpr int kHalfKeys = 64;                  // keys per pipelined half-tile
+constexpr int kKStage = kHalfKeys * kRowBytes; // 16 KB LDS stage (K or V^T)
+constexpr float kRescaleLog2 = 8.0f;           // move the max once p could exceed 2^8
 
 typedef const __attribute__((address_space(4))) int32_t* dsa_const_i32;
 
-// Physical V^T row of head dim d: rows d and d^1 swap when bit 3 of d is set,
-// so the 16 rows (8 apart) written by one transposing store straddle both
-// 128-byte bank halves.
-__device__ __forceinline__ int vt_row(int d) { return d ^ ((d >> 3) & 1); }
+// K stage [64 keys][128 dims]: 16-byte chunk XOR (row & 15), so the 32 rows a
+// fragment load reads at one chunk hit distinct banks.
+__device__ __forceinline__ int k2_swz(int r, int c) { return c ^ (r & 15); }
 
-__global__ void __launch_bounds__(256, 2) bsa_fwd4_kernel(BsaParams p) {
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k[2 * kKStage];
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_v[2 * kVStage];
+constexpr int kVtHalfRow = kHalfKeys * 2;  // 128 B: one head dim of a 64-key half-tile
 
+// V^T LDS half-tile [128 dims][64 keys]: row d occupies one 128-byte bank half
+// (even / odd d alternate); chunk XOR ((d >> 1) & 7) spreads the 16 rows read
+// per 16 lanes over distinct bank groups.
+__device__ __forceinline__ int vt9_swz(int d, int c) { return c ^ ((d >> 1) & 7); }
+
+// One workgroup per (b, h, 64-key chunk): rows of V through LDS, columns out.
+__global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restrict__ v,
+                                                           __bf16* __restrict__ vt,
+                                                           int64_t v_sb, int64_t v_st,
+                                                           int64_t v_sh, int32_t heads,
+                                                           int32_t tokens, int32_t tpad) {
+  __shared__ __bf16 tile[64][kHeadDim + 8];  // +8 keeps column reads conflict-light
+  const int chunk = blockIdx.x;              // 64-key chunk
+  const int bh = blockIdx.y;
+  const int b = bh / heads, h = bh % heads;
+  const int key0 = chunk * 64;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 5;
-  const int qi = lane & 31;
-
-  const int work = dsa::xcd_remap(blockIdx.x, gridDim.x);
-  const int qb = work % p.q_blocks;
-  const int bh = work / p.q_blocks;
-  const int h = bh % p.heads;
-  const int b = bh / p.heads;
-
-  int start = 0, end = p.kv_blocks;
-  if (p.row_ptr) {
-    const dsa_const_i32 rp = (dsa_const_i32)p.row_ptr;
-    const int rb = p.route_batches == 1 ? 0 : b;
-    const int64_t row = ((int64_t)rb * p.heads + h) * p.q_blocks + qb;
-    start = rp[row];
-    end = rp[row + 1];
-  }
-  const dsa_const_i32 cidx = (dsa_const_i32)p.col_idx;
-  const int nsub = 2 * (end - start);
-
-  const int tq = qb * 128 + wave * 32 + qi;
-  const int tq_c = tq < p.q_tokens ? tq : p.q_tokens - 1;
-  const __bf16* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)tq_c * p.q_st;
-  dsa_bf16x8 qf[8];
-#pragma unroll
-  for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
-
-  const __bf16* kbase = p.k + b * p.k_sb + h * p.k_sh;
-  const __bf16* vbase = p.v + b * p.v_sb + h * p.v_sh;
-
-  // Per-lane element offsets inside one half-tile (rows relative to its first key).
-  int krow[4], koff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int idx = (wave * 4 + j) * 64 + lane;
-    krow[j] = idx >> 4;
-    koff[j] = krow[j] * (int)p.k_st + k_swz(krow[j], idx & 15) * 8;
+    const int idx = j * 256 + tid;  // 64 rows x 16 chunks
+    const int r = idx >> 4, c = idx & 15;
+    dsa_u32x4 val = {0u, 0u, 0u, 0u};
+    if (key0 + r < tokens)
+      val = *reinterpret_cast<const dsa_u32x4*>(v + b * v_sb + h * v_sh +
+                                                (int64_t)(key0 + r) * v_st + c * 8);
+    *reinterpret_cast<dsa_u32x4*>(&tile[r][c * 8]) = val;
   }
-  const int vq = tid >> 4;
-  const int vc = tid & 15;
-  int voff[4];
+  __syncthreads();
+  __bf16* out = vt + ((int64_t)bh * kHeadDim) * tpad + key0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) voff[i] = (vq * 4 + i) * (int)p.v_st + vc * 8;
-
-  auto block_of = [&](int sub) -> int {
-    const int it = start + (sub >> 1);
-    const int kb = p.row_ptr ? cidx[it] : it;
-    return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
-  };
-
-  dsa_u32x4 vr[4];
-  auto issue = [&](int key0, int stage) {
-    const __bf16* ktile = kbase + (int64_t)key0 * p.k_st;
-    const __bf16* vtile = vbase + (int64_t)key0 * p.v_st;
-    unsigned char* kdst = lds_k + stage * kKStage + wave * 4 * 1024;
-    if (key0 + kHalfKeys <= p.kv_tokens) {
+  for (int j = 0; j < 4; ++j) {
+    const int idx = j * 256 + tid;  // 128 dims x 8 chunks of 8 slots
+    const int d = idx >> 3, c = idx & 7;
+    dsa_bf16x8 val;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_global_load_lds(ktile + koff[j], (DSA_LDS void*)(kdst + j * 1024), 16,
-                                         0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        vr[i] = *reinterpret_cast<const dsa_u32x4*>(vtile + voff[i]);
-    } else {
-      // Partial last block: clamp rows to the last token.
-      const int last = p.kv_tokens - 1 - key0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int idx = (wave * 4 + j) * 64 + lane;
-        const int r = krow[j] < last ? krow[j] : last;
-        __builtin_amdgcn_global_load_lds(ktile + (int64_t)r * p.k_st + k_swz(krow[j], idx & 15) * 8,
-                                         (DSA_LDS void*)(kdst + j * 1024), 16, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = vq * 4 + i < last ? vq * 4 + i : last;
-        vr[i] = *reinterpret_cast<const dsa_u32x4*>(vtile + (int64_t)r * p.v_st + vc * 8);
-      }
+    for (int e = 0; e < 8; ++e) {
+      const int slot = c * 8 + e;        // logical slot inside the 64-key chunk
+      const int grp16 = slot >> 4;
+      // Slot quad q holds physical quad swap(q) (the swap is its own inverse).
+      const int s16 = slot & 15, q = s16 >> 2;
+      const int phys = grp16 * 16 + ((((q & 1) << 1) | (q >> 1)) << 2) + (s16 & 3);
+      val[e] = tile[phys][d];
     }
-  };
-
-  const int quad = vq & 3;
-  const int lkey = (vq >> 2) * 16 + (((quad & 1) << 1) | (quad >> 1)) * 4;
-  auto store_vt = [&](int stage) {
-    unsigned char* base = lds_v + stage * kVStage;
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-      const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-      dsa_u32x2 out;
-      out[0] = __builtin_amdgcn_perm(vr[1][dd >> 1], vr[0][dd >> 1], sel);
-      out[1] = __builtin_amdgcn_perm(vr[3][dd >> 1], vr[2][dd >> 1], sel);
-      const int d = vc * 8 + dd;
-      *reinterpret_cast<dsa_u32x2*>(base + vt_row(d) * kVtRow + vt_swz(d, lkey >> 3) * 16 +
-                                    (lkey & 7) * 2) = out;
-    }
-  };
-
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-  dsa_f32x16 oacc[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-  const dsa_bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-
-  int kb_cur = nsub > 0 ? block_of(0) : -1;
-  if (nsub > 0) issue((kb_cur < 0 ? 0 : kb_cur) * 128, 0);
-  for (int sub = 0; sub < nsub; ++sub) {
-    const int stage = sub & 1;
-    const int kb_next = (sub + 1 < nsub) ? ((sub & 1) ? block_of(sub + 1) : kb_cur) : -1;
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this half-tile's K stage and V registers
-    store_vt(stage);
-    __syncthreads();
-    if (sub + 1 < nsub)
-      issue((kb_next < 0 ? 0 : kb_next) * 128 + ((sub + 1) & 1) * kHalfKeys, stage ^ 1);
-
-    const unsigned char* kt_lds = lds_k + stage * kKStage;
-    const unsigned char* vt_lds = lds_v + stage * kVStage;
-    const int key0 = (kb_cur < 0 ? 0 : kb_cur) * 128 + (sub & 1) * kHalfKeys;
-    int valid = kb_cur < 0 ? 0 : p.kv_tokens - key0;
-    valid = valid < kHalfKeys ? valid : kHalfKeys;
-
-    // S^T = K Q^T: 16 MFMAs, fragments staged four at a time.
-    dsa_f32x16 sacc[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
-    {
-      dsa_bf16x8 fa[4], fb[4];
-      auto load_k = [&](dsa_bf16x8* dst, int grp) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int step = grp * 4 + u;  // step = dc * 2 + kt
-          const int kt = step & 1, dc = step >> 1;
-          const int row = kt * 32 + qi;
-          dst[u] = *reinterpret_cast<const dsa_bf16x8*>(
-              kt_lds + row * kRowBytes + k_swz(row, dc * 2 + g) * 16);
-        }
-      };
-      auto mfma_k = [&](const dsa_bf16x8* src, int grp) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int step = grp * 4 + u;
-          const int kt = step & 1, dc = step >> 1;
-          sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(src[u], qf[dc], sacc[kt], 0, 0, 0);
-        }
-      };
-      load_k(fa, 0);
-      load_k(fb, 1);
-      mfma_k(fa, 0);
-      load_k(fa, 2);
-      mfma_k(fb, 1);
-      load_k(fb, 3);
-      mfma_k(fa, 2);
-      mfma_k(fb, 3);
-    }
-    if (valid < kHalfKeys) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= valid) sacc[kt][r] = -INFINITY;
-    }
-
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mx2 = mx * p.scale_log2;
-    const bool up = mx2 > m_run + kRescaleLog2;
-    if (__any(up)) {
-      const float alpha = up ? __builtin_amdgcn_exp2f(m_run - mx2) : 1.0f;
-      m_run = up ? mx2 : m_run;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-    }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-
-    dsa_bf16x8 pf[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kt = j >> 1, hf = j & 1;
-#pragma unroll
-      for (int t = 0; t < 8; t += 2) {
-        const float p0 =
-            __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t], p.scale_log2, -m_use));
-        const float p1 =
-            __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t + 1], p.scale_log2, -m_use));
-        const dsa_f32x2 two = {p0, p1};
-        const dsa_bf16x2 pb = __builtin_convertvector(two, dsa_bf16x2);
-        l_run = __builtin_amdgcn_fdot2_f32_bf16(pb, ones, l_run, false);
-        pf[j][t] = pb[0];
-        pf[j][t + 1] = pb[1];
-      }
-    }
-
-    // O^T += V^T P^T: 16 MFMAs, fragments staged four at a time.
-    {
-      dsa_bf16x8 fa[4], fb[4];
-      auto load_v = [&](dsa_bf16x8* dst, int grp) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int step = grp * 4 + u;  // step = j * 4 + dt
-          const int j = step >> 2, dt = step & 3;
-          const int d = dt * 32 + qi;
-          dst[u] = *reinterpret_cast<const dsa_bf16x8*>(
-              vt_lds + vt_row(d) * kVtRow + vt_swz(d, 2 * j + g) * 16);
-        }
-      };
-      auto mfma_v = [&](const dsa_bf16x8* src, int grp) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int step = grp * 4 + u;
-          const int j = step >> 2, dt = step & 3;
-          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(src[u], pf[j], oacc[dt], 0, 0, 0);
-        }
-      };
-      load_v(fa, 0);
-      load_v(fb, 1);
-      mfma_v(fa, 0);
-      load_v(fa, 2);
-      mfma_v(fb, 1);
-      load_v(fb, 3);
-      mfma_v(fa, 2);
-      mfma_v(fb, 3);
-    }
-    if (sub & 1) kb_cur = kb_next;
-  }
-
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (tq < p.q_tokens) {
-    __bf16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const dsa_f32x2 lo = {oacc[dt][rr * 4 + 0] * inv, oacc[dt][rr * 4 + 1] * inv};
-        const dsa_f32x2 hi = {oacc[dt][rr * 4 + 2] * inv, oacc[dt][rr * 4 + 3] * inv};
-        const dsa_bf16x2 blo = __builtin_convertvector(lo, dsa_bf16x2);
-        const dsa_bf16x2 bhi = __builtin_convertvector(hi, dsa_bf16x2);
-        const dsa_bf16x4 v4 = {blo[0], blo[1], bhi[0], bhi[1]};
-        *reinterpret_cast<dsa_bf16x4*>(orow + dt * 32 + rr * 8 + g * 4) = v4;
-      }
-    if (p.lse && g == 0) {
-      p.lse[((int64_t)b * p.heads + h) * p.q_tokens + tq] =
-          l_tot > 0.f ? m_run * 0.6931471805599453f + logf(l_tot) : -INFINITY;
-    }
+    *reinterpret_cast<dsa_bf16x8*>(out + (int64_t)d * tpad + c * 8) = val;
   }
 }
 
-// ---------------------------------------------------------------------------
-// v5: K and V half-tiles both staged by direct global->LDS loads into
-// double buffers that are distinct LDS objects (the loop is unrolled by two so
-// each stage is a compile-time buffer and reads of one stage carry no wait on
-// the DMA into the other); V^T fragments come from the transposing LDS load.
-// ---------------------------------------------------------------------------
-
-// K stage [64 keys][128 dims]: 16-byte chunk XOR (row & 15), so the 32 rows a
-// b128 fragment load reads at one chunk hit distinct banks.
-__device__ __forceinline__ int k2_swz(int r, int c) { return c ^ (r & 15); }
-// V stage [64 keys][128 dims]: chunk XOR ((row & 3) << 2); a transposing load
-// reads 4 consecutive rows x 32 bytes per 16 lanes, which this spreads over
-// all banks.
-__device__ __forceinline__ int v2_swz(int r, int c) { return c ^ ((r & 3) << 2); }
-
-typedef short dsa_s16x4 __attribute__((ext_vector_type(4)));
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i returns element (i % 4)
-// of the 64-bit rows read by lanes i/4 + 4*jj, jj = 0..3.
-__device__ __forceinline__ dsa_u32x2 lds_read_tr16(const unsigned char* addr) {
-  const dsa_s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((DSA_LDS dsa_s16x4*)(addr));
-  return __builtin_bit_cast(dsa_u32x2, v);
-}
-
-__device__ __forceinline__ dsa_bf16x8 read_vt_fragment(const unsigned char* vt, int j, int dt,
-                                                       int g, int grp, int gi) {
-  // Lane i of 16-lane group grp reads 4 consecutive head dims of one key row;
-  // the transposing load hands each lane 4 keys of one head dim.
-  const int d0 = dt * 32 + 16 * (grp & 1) + 4 * (gi & 3);
-  const int chunk = d0 >> 3;
-  const int within = (d0 & 7) * 2;
-  dsa_u32x4 a32;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int row = 16 * j + 8 * t + 4 * g + (gi >> 2);
-    const dsa_u32x2 part = lds_read_tr16(vt + row * kRowBytes + v2_swz(row, chunk) * 16 + within);
-    a32[2 * t] = part[0];
-    a32[2 * t + 1] = part[1];
-  }
-  return __builtin_bit_cast(dsa_bf16x8, a32);
-}
-
-__global__ void __launch_bounds__(256, 2) bsa_fwd5_kernel(BsaParams p) {
+__global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf16* vt,
+                                                          int32_t tpad) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
@@ -811,8 +117,6 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd5_kernel(BsaParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5;
   const int qi = lane & 31;
-  const int grp = lane >> 4;
-  const int gi = lane & 15;
 
   const int work = dsa::xcd_remap(blockIdx.x, gridDim.x);
   const int qb = work % p.q_blocks;
@@ -840,17 +144,16 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd5_kernel(BsaParams p) {
     qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
 
   const __bf16* kbase = p.k + b * p.k_sb + h * p.k_sh;
-  const __bf16* vbase = p.v + b * p.v_sb + h * p.v_sh;
-
-  // Rows (relative to the half-tile's first key) and 16-byte source chunks
-  // this lane stages; the linear LDS image is the swizzled layout.
-  int lrow[4], kchunk[4], vchunk[4];
+  const __bf16* vtbase = vt + ((int64_t)(b * p.heads + h) * kHeadDim) * tpad;
+  // Per-lane source offsets (elements) relative to the half-tile's first key.
+  int lrow[4], koff[4], voff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = (wave * 4 + j) * 64 + lane;
     lrow[j] = idx >> 4;
-    kchunk[j] = k2_swz(lrow[j], idx & 15);
-    vchunk[j] = v2_swz(lrow[j], idx & 15);
+    koff[j] = lrow[j] * (int)p.k_st + k2_swz(lrow[j], idx & 15) * 8;
+    const int d = idx >> 3;
+    voff[j] = d * tpad + vt9_swz(d, idx & 7) * 8;
   }
 
   auto block_of = [&](int sub) -> int {
@@ -860,17 +163,27 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd5_kernel(BsaParams p) {
   };
 
   auto issue = [&](int key0, unsigned char* kdst, unsigned char* vdst) {
-    int last = p.kv_tokens - 1 - key0;  // rows past the sequence end are clamped
-    last = last < kHalfKeys - 1 ? last : kHalfKeys - 1;
+    const __bf16* ktile = kbase + (int64_t)key0 * p.k_st;
+    const __bf16* vtile = vtbase + key0;
+    if (key0 + kHalfKeys <= p.kv_tokens) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = lrow[j] < last ? lrow[j] : last;
-      const int64_t key = key0 + r;
-      __builtin_amdgcn_global_load_lds(kbase + key * p.k_st + kchunk[j] * 8,
-                                       (DSA_LDS void*)(kdst + (wave * 4 + j) * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vbase + key * p.v_st + vchunk[j] * 8,
-                                       (DSA_LDS void*)(vdst + (wave * 4 + j) * 1024), 16, 0, 0);
+      for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_global_load_lds(ktile + koff[j],
+                                         (DSA_LDS void*)(kdst + (wave * 4 + j) * 1024), 16, 0, 0);
+    } else {
+      const int last = p.kv_tokens - 1 - key0;  // clamp rows past the sequence end
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int idx = (wave * 4 + j) * 64 + lane;
+        const int r = lrow[j] < last ? lrow[j] : last;
+        __builtin_amdgcn_global_load_lds(ktile + (int64_t)r * p.k_st + k2_swz(lrow[j], idx & 15) * 8,
+                                         (DSA_LDS void*)(kdst + (wave * 4 + j) * 1024), 16, 0, 0);
+      }
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_global_load_lds(vtile + voff[j],
+                                       (DSA_LDS void*)(vdst + (wave * 4 + j) * 1024), 16, 0, 0);
   };
 
   float m_run = -INFINITY;
@@ -944,14 +257,14 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd5_kernel(BsaParams p) {
     for (int j = 0; j < 4; ++j) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const dsa_bf16x8 a = read_vt_fragment(vt_lds, j, dt, g, grp, gi);
+        const int d = dt * 32 + qi;
+        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
+            vt_lds + d * kVtHalfRow + vt9_swz(d, 2 * j + g) * 16);
         oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[j], oacc[dt], 0, 0, 0);
       }
     }
   };
 
-  // One half-tile step: wait for this stage, release the other one, prefetch
-  // the next half-tile into it, compute this one.
   auto step = [&](int sub, int kb, int kb_next, const unsigned char* kc, const unsigned char* vc,
                   unsigned char* kn, unsigned char* vn) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -968,7 +281,6 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd5_kernel(BsaParams p) {
     int kb = block_of(0);
     issue((kb < 0 ? 0 : kb) * 128, lds_k0, lds_v0);
     for (int sub = 0; sub < nsub; sub += 2) {
-      // Even half-tile (stage 0) and odd half-tile (stage 1) of key block kb.
       const int kb_after = (sub + 2 < nsub) ? block_of(sub + 2) : -1;
       step(sub, kb, kb, lds_k0, lds_v0, lds_k1, lds_v1);
       step(sub + 1, kb, kb_after, lds_k1, lds_v1, lds_k0, lds_v0);
@@ -1000,14 +312,23 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd5_kernel(BsaParams p) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
+int32_t padded_tokens(int32_t kv_tokens) { return (kv_tokens + 127) / 128 * 128; }
+
 }  // namespace
+
+extern "C" size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
+                                          int32_t head_dim) {
+  if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
+  return (size_t)batch * heads * head_dim * padded_tokens(kv_tokens) * sizeof(__bf16);
+}
 
 extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
                            const int64_t* strides, int32_t batch, int32_t q_tokens,
                            int32_t kv_tokens, int32_t heads, int32_t head_dim,
                            int32_t block_size, const int32_t* row_ptr,
                            const int32_t* col_idx, int32_t route_batches, float scale,
-                           float* lse, hipStream_t stream) {
+                           float* lse, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream) {
   dsa::clear_error();
   if (!q || !k || !v || !o || !strides)
     return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: null tensor or stride pointer");
@@ -1034,10 +355,19 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
       return dsa::set_error(DSA_EINVAL,
                             "dsa_bsa_fwd: stride %d (=%lld) is not a multiple of 8 elements", i,
                             (long long)strides[i]);
+  const size_t need = dsa_bsa_workspace_bytes(batch, heads, kv_tokens, head_dim);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return dsa::set_error(DSA_EINVAL,
+                          "dsa_bsa_fwd: workspace of %zu bytes (16-byte aligned) required, got %zu",
+                          need, workspace_bytes);
   const int32_t q_blocks = (q_tokens + block_size - 1) / block_size;
   const int32_t kv_blocks = (kv_tokens + block_size - 1) / block_size;
+  const int32_t tpad = padded_tokens(kv_tokens);
   const int64_t grid = (int64_t)batch * heads * q_blocks;
-  if (grid > 0x7fffffff) return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: grid too large");
+  if (grid > 0x7fffffff || (int64_t)batch * heads > 65535)
+    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: grid too large");
+  if ((int64_t)(kHeadDim - 1) * tpad + tpad > 0x7fffffff)
+    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_bsa_fwd: kv_tokens too large");
 
   BsaParams p;
   p.q = static_cast<const __bf16*>(q);
@@ -1056,17 +386,10 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   p.route_batches = row_ptr ? route_batches : 1;
   p.scale = scale;
   p.scale_log2 = scale * 1.4426950408889634f;
-  static const int variant = [] {
-    const char* env = getenv("DSA_BSA_VARIANT");
-    return env ? atoi(env) : 5;
-  }();
-  if (variant == 1)
-    hipLaunchKernelGGL(bsa_fwd_kernel<128>, dim3((unsigned)grid), dim3(256), 0, stream, p);
-  else if (variant == 4)
-    hipLaunchKernelGGL(bsa_fwd4_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p);
-  else if (variant == 3)
-    hipLaunchKernelGGL(bsa_fwd3_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(bsa_fwd5_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p);
+  __bf16* vt = static_cast<__bf16*>(workspace);
+  hipLaunchKernelGGL(vt_transpose_kernel, dim3((unsigned)(tpad / 64), (unsigned)(batch * heads)),
+                     dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads, kv_tokens, tpad);
+  hipLaunchKernelGGL(bsa_fwd_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p,
+                     (const __bf16*)vt, tpad);
   return dsa::check_launch("dsa_bsa_fwd");
 }

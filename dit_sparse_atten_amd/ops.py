@@ -147,6 +147,9 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     strides = _lib.int64_array(
         list(q.stride()[:3]) + list(k.stride()[:3]) + list(v.stride()[:3])
         + list(out.stride()[:3]))
+    workspace_bytes = lib.dsa_bsa_workspace_bytes(batch, heads, kv_tokens, head_dim)
+    # Transposed-V scratch for this call; the caching allocator recycles it.
+    workspace = torch.empty(max(workspace_bytes, 16), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         status = lib.dsa_bsa_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), strides,
@@ -155,7 +158,7 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
             col_idx.data_ptr() if col_idx is not None else None,
             route_batches, float(scale),
             lse.data_ptr() if lse is not None else None,
-            _stream_handle(q.device))
+            workspace.data_ptr(), workspace.numel(), _stream_handle(q.device))
     _lib.check(status, "dsa_bsa_fwd")
     return (out, lse) if return_lse else out
 

@@ -47,13 +47,22 @@ const char* dsa_last_error(void);
  *                skipped; a row with no key blocks yields zeros.
  *   scale: softmax scale (d^-1/2 for softmax_scale=None).
  *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
+ *   workspace: device scratch of dsa_bsa_workspace_bytes() bytes, 16-byte
+ *                aligned, that receives the transposed V for this call; its
+ *                contents need no initialisation and are dead after the call.
  * Keys past kv_tokens in a partial last block are masked.
  */
 int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, const int64_t* strides,
                 int32_t batch, int32_t q_tokens, int32_t kv_tokens, int32_t heads,
                 int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
                 const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
-                hipStream_t stream);
+                void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes dsa_bsa_fwd needs (batch * heads * head_dim * kv_tokens
+ * rounded up to 128, in bf16); 0 for invalid sizes.  No counterpart in the
+ * reference, whose FlexAttention allocates internally. */
+size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
+                               int32_t head_dim);
 
 /*
  * Sampled block-mass estimate for one batch-1 self-attention call.

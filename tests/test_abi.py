@@ -1,0 +1,66 @@
+"""C-ABI checks that need no GPU: every function declared in include/dsa.h is
+exported by libdsa.so and bound in the ctypes table, and argument validation
+(which runs on the host before any HIP call) reports the documented errors."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from dit_sparse_atten_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "dsa.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIBRARY_PATH.exists():
+        pytest.skip("libdsa.so not built")
+    return _lib.load()
+
+
+def test_header_symbols_are_exported_and_bound(lib):
+    declared = _declared()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes binding"
+    assert set(_lib.SIGNATURES) == set(declared)
+
+
+def test_version_and_workspace_size(lib):
+    assert lib.dsa_version() == 1
+    # 2 x 12 heads x 128 dims x 32,760 tokens padded to 32,768, bf16.
+    assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == 2 * 12 * 128 * 32768 * 2
+    assert lib.dsa_bsa_workspace_bytes(0, 12, 10, 128) == 0
+
+
+def test_invalid_arguments_are_reported_before_any_launch(lib):
+    strides = _lib.int64_array([8] * 12)
+    status = lib.dsa_bsa_fwd(None, None, None, None, strides, 1, 128, 128, 1, 128, 128,
+                             None, None, 1, 0.1, None, None, 0, None)
+    assert status == _lib.DSA_EINVAL
+    assert "null" in _lib.last_error()
+    with pytest.raises(ValueError, match="null"):
+        _lib.check(status, "dsa_bsa_fwd")
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 64, 128,
+                             None, None, 1, 0.1, None, fake, 1 << 20, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 128, 128,
+                             None, None, 1, 0.1, None, fake, 16, None)
+    assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
+    status = lib.dsa_route_select(fake, None, 4, 600, 0.5, 0.95, 1, 0, fake, fake, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "512" in _lib.last_error()
+    status = lib.dsa_sampled_mass(fake, fake, _lib.int64_array([8] * 4), 1024, 2, 128, 128, 3,
+                                  0.1, fake, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "power of two" in _lib.last_error()
+    status = lib.dsa_permute_rows(4, None, None, None, None, None, 1, 1, 1, 16, None)
+    assert status == _lib.DSA_EINVAL
