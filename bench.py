@@ -217,7 +217,7 @@ def main():
     wall = time.perf_counter() - started
     total_ms = start_all.elapsed_time(end_all)
     ms_per_step = total_ms / args.steps
-    kernel_ms = sorted(per_call)[len(per_call) // 2]
+    kernel_ms = sum(per_call) / len(per_call)
     value = flops / (ms_per_step * 1e-3) / 1e12
 
     result = {
@@ -250,14 +250,17 @@ def main():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
     result["roofline"] = {
         "bound": "mfma",
-        "kernel": "bsa_fwd_kernel (+ vt_transpose_kernel)",
+        "kernel": "bsa_fwd_kernel<true> (event window also holds vt_transpose_kernel)",
         "achieved": round(achieved, 2),
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
         "traffic": traffic,
-        "launch_ms_median": round(kernel_ms, 4),
+        "launch_ms_mean": round(kernel_ms, 4),
+        "launch_ms_median": round(sorted(per_call)[len(per_call) // 2], 4),
     }
+    if traffic:
+        result["roofline"]["hbm_gbs_at_traffic"] = round(traffic / (kernel_ms * 1e-3) / 1e9, 1)
 
     if not args.only_sparse:
         def dense_call():
@@ -283,6 +286,27 @@ def main():
         mass_ms, _ = timer.time(lambda: ops.sampled_block_mass(q, k, BLOCK, 16), 10)
         updated = route_update()
         updated_keep = updated.nnz_value() / (HEADS * blocks * blocks)
+        # Morton micro-tile reorder (Q/K/V gather) and restore (O scatter) at the
+        # same shape: HBM-bound data movement, bytes = read + write of each tensor.
+        from dit_sparse_atten_amd.attention_backends.spatial import build_spatial_layout
+        layout = build_spatial_layout(GRID, BLOCK)
+        permutation, inverse, _ = layout._device_values(device)
+        head_major = [torch.empty((1, HEADS, TOKENS, HEAD_DIM), dtype=torch.bfloat16,
+                                  device=device).transpose(1, 2) for _ in range(3)]
+        restored = torch.empty_like(out)
+        reorder_ms, _ = timer.time(
+            lambda: ops.permute_tokens((q, k, v), permutation, out=head_major), 10)
+        restore_ms, _ = timer.time(
+            lambda: ops.permute_tokens((out,), inverse, out=[restored]), 10)
+        tensor_bytes = TOKENS * HEADS * HEAD_DIM * 2
+        result["layout"] = {
+            "microtile": list(layout.microtile_shape),
+            "reorder_qkv_ms": round(reorder_ms, 4),
+            "reorder_qkv_gbs": round(6 * tensor_bytes / (reorder_ms * 1e-3) / 1e9, 1),
+            "restore_ms": round(restore_ms, 4),
+            "restore_gbs": round(2 * tensor_bytes / (restore_ms * 1e-3) / 1e9, 1),
+            "hbm_peak_gbs": PEAK_HBM_GBS,
+        }
         result["dense"] = {
             "ms_per_call": round(dense_ms, 4),
             "tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),

@@ -16,8 +16,9 @@
 //    row (row max / sum stay in registers, one cross-half exchange) and P^T
 //    leaves the accumulators already in the B-operand layout of O^T = V^T P^T;
 //  * keys stream as 64-key half-tiles, double-buffered in LDS by direct
-//    global->LDS loads issued one half-tile ahead; the two stages are distinct
-//    LDS objects so reads of one never wait on the DMA into the other;
+//    buffer->LDS loads issued one half-tile ahead; the two stages are distinct
+//    LDS objects so reads of one never wait on the DMA into the other, and
+//    rows past the sequence end read as zeros (buffer range check);
 //  * V is first transposed into a V^T workspace whose 16-key groups store
 //    their 4-key quads as 0, 2, 1, 3 (the key order of the P^T slots), so both
 //    MFMA operands are conflict-free 16-byte LDS reads;
@@ -63,6 +64,35 @@ constexpr int kVtHalfRow = kHalfKeys * 2;  // 128 B: one head dim of a 64-key ha
 // per 16 lanes over distinct bank groups.
 __device__ __forceinline__ int vt9_swz(int d, int c) { return c ^ ((d >> 1) & 7); }
 
+// Raw buffer resources for the direct-to-LDS loads.  The MUBUF form
+// (buffer_load ... lds) is used rather than global_load_lds because the
+// compiler counts the latter as an LGKM event of unknown order and then waits
+// for every outstanding LDS read (lgkmcnt(0)) before each fragment use; MUBUF
+// LDS loads only count on vmcnt.  Dword 3 is the gfx9 raw-buffer format word.
+// A raw buffer (stride 0) returns zeros for offsets at or past num_records
+// (the vector offset is checked, the scalar offset is not).
+constexpr int kBufferDword3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferDword3);
+}
+
+// 16 bytes per lane into LDS at lds + 16 * lane.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds,
+                                           uint32_t voffset, uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (DSA_LDS void*)lds, 16, voffset, soffset, 0, 0);
+}
+
+// Resource covering the 64 K rows of a half-tile starting at key0; rows at or
+// past kv_tokens read as zeros (a half-tile wholly past the end has no
+// records).  The host keeps 64 rows of K within 2^31 bytes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t k_tile_rsrc(const __bf16* kbase, int64_t k_st,
+                                                             int key0, int kv_tokens) {
+  const int rows = min(kHalfKeys, kv_tokens - key0);
+  const uint32_t bytes = rows > 0 ? (uint32_t)((rows - 1) * k_st * 2 + kRowBytes) : 0u;
+  return make_rsrc(kbase + (int64_t)key0 * k_st, bytes);
+}
+
 // One workgroup per (b, h, 64-key chunk): rows of V through LDS, columns out.
 __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restrict__ v,
                                                            __bf16* __restrict__ vt,
@@ -105,6 +135,8 @@ __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restr
   }
 }
 
+// kRouted: key blocks from the CSR row (false: every key block, dense).
+template <bool kRouted>
 __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf16* vt,
                                                           int32_t tpad) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
@@ -125,7 +157,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
   const int b = bh / p.heads;
 
   int start = 0, end = p.kv_blocks;
-  if (p.row_ptr) {
+  if (kRouted) {
     const dsa_const_i32 rp = (dsa_const_i32)p.row_ptr;
     const int rb = p.route_batches == 1 ? 0 : b;
     const int64_t row = ((int64_t)rb * p.heads + h) * p.q_blocks + qb;
@@ -146,44 +178,30 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
   const __bf16* kbase = p.k + b * p.k_sb + h * p.k_sh;
   const __bf16* vtbase = vt + ((int64_t)(b * p.heads + h) * kHeadDim) * tpad;
   // Per-lane source offsets (elements) relative to the half-tile's first key.
-  int lrow[4], koff[4], voff[4];
+  int koff[4], voff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = (wave * 4 + j) * 64 + lane;
-    lrow[j] = idx >> 4;
-    koff[j] = lrow[j] * (int)p.k_st + k2_swz(lrow[j], idx & 15) * 8;
+    const int row = idx >> 4;
+    koff[j] = row * (int)p.k_st + k2_swz(row, idx & 15) * 8;
     const int d = idx >> 3;
     voff[j] = d * tpad + vt9_swz(d, idx & 7) * 8;
   }
 
   auto block_of = [&](int sub) -> int {
     const int it = start + (sub >> 1);
-    const int kb = p.row_ptr ? cidx[it] : it;
+    const int kb = kRouted ? cidx[it] : it;
     return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
   };
 
+  const __amdgpu_buffer_rsrc_t vt_rsrc = make_rsrc(vtbase, (uint32_t)(kHeadDim * tpad * 2));
   auto issue = [&](int key0, unsigned char* kdst, unsigned char* vdst) {
-    const __bf16* ktile = kbase + (int64_t)key0 * p.k_st;
-    const __bf16* vtile = vtbase + key0;
-    if (key0 + kHalfKeys <= p.kv_tokens) {
+    const __amdgpu_buffer_rsrc_t k_rsrc = k_tile_rsrc(kbase, p.k_st, key0, p.kv_tokens);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        __builtin_amdgcn_global_load_lds(ktile + koff[j],
-                                         (DSA_LDS void*)(kdst + (wave * 4 + j) * 1024), 16, 0, 0);
-    } else {
-      const int last = p.kv_tokens - 1 - key0;  // clamp rows past the sequence end
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int idx = (wave * 4 + j) * 64 + lane;
-        const int r = lrow[j] < last ? lrow[j] : last;
-        __builtin_amdgcn_global_load_lds(ktile + (int64_t)r * p.k_st + k2_swz(lrow[j], idx & 15) * 8,
-                                         (DSA_LDS void*)(kdst + (wave * 4 + j) * 1024), 16, 0, 0);
-      }
-    }
+    for (int j = 0; j < 4; ++j) lds_load16(k_rsrc, kdst + (wave * 4 + j) * 1024, koff[j] * 2, 0);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_global_load_lds(vtile + voff[j],
-                                       (DSA_LDS void*)(vdst + (wave * 4 + j) * 1024), 16, 0, 0);
+      lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, voff[j] * 2, key0 * 2);
   };
 
   float m_run = -INFINITY;
@@ -351,10 +369,14 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: tensors must be 16-byte aligned");
   for (int i = 0; i < 12; ++i)
-    if (strides[i] % 8 != 0)
+    if (strides[i] % 8 != 0 || strides[i] < 0)
       return dsa::set_error(DSA_EINVAL,
-                            "dsa_bsa_fwd: stride %d (=%lld) is not a multiple of 8 elements", i,
-                            (long long)strides[i]);
+                            "dsa_bsa_fwd: stride %d (=%lld) is not a non-negative multiple of 8 "
+                            "elements", i, (long long)strides[i]);
+  if (strides[4] * (int64_t)(2 * 64) > 0x7fffffff)
+    return dsa::set_error(DSA_EUNSUPPORTED,
+                          "dsa_bsa_fwd: key token stride %lld too large (64 rows must span < 2 GiB)",
+                          (long long)strides[4]);
   const size_t need = dsa_bsa_workspace_bytes(batch, heads, kv_tokens, head_dim);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return dsa::set_error(DSA_EINVAL,
@@ -389,7 +411,11 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   __bf16* vt = static_cast<__bf16*>(workspace);
   hipLaunchKernelGGL(vt_transpose_kernel, dim3((unsigned)(tpad / 64), (unsigned)(batch * heads)),
                      dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads, kv_tokens, tpad);
-  hipLaunchKernelGGL(bsa_fwd_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p,
-                     (const __bf16*)vt, tpad);
+  if (row_ptr)
+    hipLaunchKernelGGL(bsa_fwd_kernel<true>, dim3((unsigned)grid), dim3(256), 0, stream, p,
+                       (const __bf16*)vt, tpad);
+  else
+    hipLaunchKernelGGL(bsa_fwd_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, p,
+                       (const __bf16*)vt, tpad);
   return dsa::check_launch("dsa_bsa_fwd");
 }

@@ -5,7 +5,39 @@ TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
 checker or the reported CPU baseline.  The product (``dit_sparse_atten_amd``)
 never imports it and has no CPU fallback.
 
-Modules and the reference code each follows:
-  attention     masked block-sparse softmax attention (flex.py:379-399,
-                sparse.py:670-751), float64 closed form
+The reference is Python (PyTorch + FlexAttention + Triton), so there is no C
+or C++ reference source to compile into an ``oracle/_ref`` library; the
+restatement is numpy (fp32 / fp64 / exact integers) and plain Python loops.
+
+Modules, the reference code each follows, and what pins each function
+(tests/test_oracle_*.py; golden fixtures written by tests/golden/make_golden.py
+from the reference imported in the build container):
+
+  attention    block_sparse_attention: masked softmax closed form in fp64
+               (flex.py:379-399, sparse.py:670-751).  Pinned by: full route ==
+               torch SDPA; equality with the reference's own sparse_chunk
+               outputs on config 0 (sparse_config0.npz).
+  route        sample_indices (flex.py:221-231): known answers (offsets
+               4, 12, ..., 124; partial blocks).
+               sampled_block_mass (flex.py:205-251): reference golden
+               (sampled_mass.npz checksums), S = block => exact block mass.
+               persistence_prior (flex.py:535-541): reference golden
+               (sampled_route.npz), dyadic closed form.
+               top_mass_route (flex.py:83-94 == sparse.py:171-181): reference
+               golden (top_mass_route.npz, ties compared as value multisets
+               because torch's CPU argsort is unstable), brute force over all
+               prefixes with exact rationals, planted-mistake checks.
+               first_frame_sink (flex.py:550-566), pack_rows
+               (layout_ops.py:128-151), to_csr (flex.py:275-338), route_keep /
+               dense_dispatch (flex.py:473-493): known answers from the
+               reference's tests, stable argsort, round trips.
+  spatial      morton_code, choose_microtile, spatial_layout (spatial.py:14-183)
+               and sparse_tile_shape / tile_major_permutation (sparse.py:51-138):
+               reference golden (spatial_layout.npz, the full 57,600-token
+               permutation and neighbour table), known answers, bijection.
+  sparse_path  group_indices, sparse_chunk, dense_route, SparsePathCase
+               (sparse.py:184-233, 376-406, 670-751, 794-930): reference golden
+               on config 0 (bootstrap route, mass, outputs, one sparse step).
+
+No function of the oracle is left without such a check.
 """
