@@ -19,11 +19,15 @@
 //    buffer->LDS loads issued one half-tile ahead; the two stages are distinct
 //    LDS objects so reads of one never wait on the DMA into the other, and
 //    rows past the sequence end read as zeros (buffer range check);
-//  * V is first transposed into a V^T workspace whose 16-key groups store
+//  * V is first transposed into a V^T workspace tiled by 64-key half-tiles
+//    ([b, h][T/64][128 dims][64 keys], every half-tile 16 KB contiguous, so a
+//    stage load touches one contiguous block rather than 128 rows spread
+//    over the whole sequence); inside a half-tile the 16-key groups store
 //    their 4-key quads as 0, 2, 1, 3 (the key order of the P^T slots), so both
 //    MFMA operands are conflict-free 16-byte LDS reads;
 //  * online softmax with a lazily moved reference max (rescale only when a
-//    score exceeds it by 2^8) and row sums from the bf16 P with dot2.
+//    score exceeds it by 2^8); row sums add the fp32 P in plain VALU adds
+//    (v_dot2 would contend with the matrix core for issue).
 #include "dsa_common.h"
 
 namespace {
@@ -83,6 +87,22 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rsrc, unsigned
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (DSA_LDS void*)lds, 16, voffset, soffset, 0, 0);
 }
 
+// The same load issued through inline asm.  The compiler then does not track
+// it: its LDS-DMA alias tracking cannot tell the double-buffer stages of the
+// ping-pong kernel apart and would otherwise wait for every outstanding stage
+// load (vmcnt(0)) before the first fragment read of each phase.  Ordering is
+// carried entirely by the caller's explicit vmcnt waits and barriers; the
+// "memory" clobber keeps other memory accesses on their side of the load.
+// M0 (the LDS base) needs one wait state after the SALU write.
+__device__ __forceinline__ void lds_load16_async(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds,
+                                                 uint32_t voffset, uint32_t soffset) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(DSA_LDS void*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(m0), "v"(voffset), "s"(rsrc), "s"(soffset)
+               : "memory");
+}
+
 // Resource covering the 64 K rows of a half-tile starting at key0; rows at or
 // past kv_tokens read as zeros (a half-tile wholly past the end has no
 // records).  The host keeps 64 rows of K within 2^31 bytes.
@@ -116,7 +136,7 @@ __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restr
     *reinterpret_cast<dsa_u32x4*>(&tile[r][c * 8]) = val;
   }
   __syncthreads();
-  __bf16* out = vt + ((int64_t)bh * kHeadDim) * tpad + key0;
+  __bf16* out = vt + ((int64_t)bh * kHeadDim) * tpad + (int64_t)key0 * kHeadDim;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = j * 256 + tid;  // 128 dims x 8 chunks of 8 slots
@@ -131,7 +151,7 @@ __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restr
       const int phys = grp16 * 16 + ((((q & 1) << 1) | (q >> 1)) << 2) + (s16 & 3);
       val[e] = tile[phys][d];
     }
-    *reinterpret_cast<dsa_bf16x8*>(out + (int64_t)d * tpad + c * 8) = val;
+    *reinterpret_cast<dsa_bf16x8*>(out + d * 64 + c * 8) = val;
   }
 }
 
@@ -185,7 +205,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     const int row = idx >> 4;
     koff[j] = row * (int)p.k_st + k2_swz(row, idx & 15) * 8;
     const int d = idx >> 3;
-    voff[j] = d * tpad + vt9_swz(d, idx & 7) * 8;
+    voff[j] = d * kHalfKeys + vt9_swz(d, idx & 7) * 8;
   }
 
   auto block_of = [&](int sub) -> int {
@@ -201,7 +221,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     for (int j = 0; j < 4; ++j) lds_load16(k_rsrc, kdst + (wave * 4 + j) * 1024, koff[j] * 2, 0);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, voff[j] * 2, key0 * 2);
+      lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, voff[j] * 2, key0 * kRowBytes);
   };
 
   float m_run = -INFINITY;
@@ -211,7 +231,6 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
-  const dsa_bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 
   auto compute = [&](const unsigned char* kt_lds, const unsigned char* vt_lds, int valid) {
     dsa_f32x16 sacc[2];
@@ -255,6 +274,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     dsa_bf16x8 pf[4];
+    float sum0 = 0.f, sum1 = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kt = j >> 1, hf = j & 1;
@@ -266,11 +286,13 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
             __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t + 1], p.scale_log2, -m_use));
         const dsa_f32x2 two = {p0, p1};
         const dsa_bf16x2 pb = __builtin_convertvector(two, dsa_bf16x2);
-        l_run = __builtin_amdgcn_fdot2_f32_bf16(pb, ones, l_run, false);
+        sum0 += p0;
+        sum1 += p1;
         pf[j][t] = pb[0];
         pf[j][t + 1] = pb[1];
       }
     }
+    l_run += sum0 + sum1;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma unroll

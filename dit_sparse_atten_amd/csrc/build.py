@@ -26,7 +26,10 @@ SOURCES = (
 
 # Packed FP32 VALU forms are disabled: the device code relies on scalar and
 # float2 arithmetic only.  hipcc's host pass warns that it does not know the
-# feature; that warning is expected.
+# feature; that warning is expected.  MFMA results stay in architectural
+# VGPRs (-amdgpu-mfma-vgpr-form): at one wave per SIMD the register allocator
+# would otherwise place S accumulators in AGPRs and copy every element back
+# with v_accvgpr_read before the softmax reads it.
 HIPCC_FLAGS = (
     "--offload-arch=gfx950",
     "-O3",
@@ -34,6 +37,7 @@ HIPCC_FLAGS = (
     "-fPIC",
     "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 )
 
 
