@@ -45,10 +45,27 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int,    # tokens, heads, head_dim, block, samples
         _c_float, _c_ptr, _c_ptr,                  # scale, mass, stream
     )),
+    "dsa_block_mass": (_c_int, (
+        _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
+        _c_int, _c_int, _c_int, _c_int,            # tokens, heads, head_dim, block
+        _c_ptr, _c_i64, _c_float, _c_ptr, _c_ptr,  # lse, lse_head_stride, scale, mass, stream
+    )),
     "dsa_route_select": (_c_int, (
         _c_ptr, _c_ptr, _c_int, _c_int,            # mass, previous, rows, keys
         _c_float, _c_float, _c_int, _c_int,        # rho, target, cap, sink_blocks
         _c_ptr, _c_ptr, _c_ptr,                    # route, counts, stream
+    )),
+    "dsa_frontier_mask": (_c_int, (
+        _c_ptr, _c_int, _c_int, _c_ptr,            # route, heads, blocks, neighbors
+        _c_ptr, _c_ptr, _c_ptr,                    # frontier, count, stream
+    )),
+    "dsa_directional_update": (_c_int, (
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr,            # mass, previous, previous_frontier, neighbors
+        _c_int, _c_int, _c_int,                    # heads, blocks, cap
+        _c_float, _c_float, _c_float, _c_float,    # persistence, min_ratio, bonus, budget_scale
+        _c_int, _c_int, _c_int,                    # explore_count, expand_flags, sink_blocks
+        _c_ptr, _c_ptr, _c_ptr,                    # route, counts, candidates
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr,            # exploration, dropped, added, stream
     )),
     "dsa_route_to_csr": (_c_int, (
         _c_ptr, _c_int, _c_int,                    # route, rows, keys

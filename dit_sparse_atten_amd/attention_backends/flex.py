@@ -4,16 +4,18 @@ Mirrors attention_backends/flex.py of the reference, with FlexAttention and
 BlockMask replaced by the libdsa HIP kernels and a CSR route:
   FlexReuseConfig / validation      flex.py:43-80, 407-443
   _top_mass_route                   flex.py:83-94      -> dsa_route_select
+  _block_attention_mass             flex.py:96-202     -> dsa_block_mass
   _sampled_block_mass               flex.py:205-251    -> dsa_sampled_mass
+  _dense_bootstrap                  flex.py:254-272    -> dsa_bsa_fwd (+ LSE), dsa_block_mass
   _pack_route / _build_block_mask   flex.py:275-355    -> dsa_pack_rows / dsa_route_to_csr
   _flex_output                      flex.py:379-399    -> dsa_bsa_fwd
   FlexReuseBackend state machine    flex.py:402-850    (same phases, keys, dispatch,
                                                         prefetch stream and release)
-Step 0 returns dense output; later steps reuse, update (sampled) or dispatch
-high-keep routes to the dense kernel.  Not in this build: the exact
-(dense + LSE + second QK pass) bootstrap and refresh, and the directional
-frontier update; configurations that need them raise ``NotImplementedError``
-at construction.
+  directional update / frontier     flex.py:517-534, 544-566 -> routing.py kernels
+Step 0 returns dense output with an exact (dense + LSE + block-mass pass) or
+sampled route; later steps reuse the route, refresh it exactly or update it
+from samples (optionally frontier-directed), or dispatch high-keep routes to
+the dense kernel.
 """
 
 from __future__ import annotations
@@ -28,6 +30,7 @@ from .. import ops
 from .context import routing_context
 from .dense import DenseBackend, install
 from .layout_ops import pack_boolean_rows
+from .routing import directional_budget_update
 from .spatial import build_spatial_layout
 
 
@@ -38,8 +41,8 @@ class FlexReuseConfig:
     mass_target: float = 0.90
     # Kept for signature compatibility; the HIP kernels need no compilation.
     compile_kernel: bool = True
-    # 0 keeps the step-0 route static; a positive value asks for an exact
-    # dense refresh every N steps (not in this build).
+    # 0 keeps the step-0 route static; a positive value refreshes the route
+    # from exact dense attention every N steps.
     update_interval: int = 0
     # A positive value updates from sampled Q/K blocks every N steps.
     sampled_update_interval: int = 0
@@ -76,6 +79,18 @@ def _top_mass_route(mass, target, keep):
     return route
 
 
+def _block_attention_mass(q, k, lse, block_size, scale=None):
+    """Recover exact dense block mass from Q, K and the per-query LSE.
+
+    One HIP pass recomputes QK on the matrix cores, normalises every score
+    with the LSE of the dense forward and writes one value per 128x128 block;
+    no probability tensor is materialised and no atomics are used.
+    """
+    if q.shape[0] != 1 or q.shape[1] != k.shape[1]:
+        raise ValueError("Flex bootstrap supports batch-1 self-attention")
+    return ops.block_mass(q, k, lse, block_size, scale)
+
+
 def _sampled_block_mass(q, k, block_size, samples=2, scale=None, query_block_chunk=16):
     """Estimate block mass from evenly sampled Q/K tokens per block.
 
@@ -86,6 +101,16 @@ def _sampled_block_mass(q, k, block_size, samples=2, scale=None, query_block_chu
     if query_block_chunk <= 0:
         raise ValueError("sample_query_block_chunk must be positive")
     return ops.sampled_block_mass(q, k, block_size, samples, scale)
+
+
+def _dense_bootstrap(q, k, v, block_size, mass_target, keep, compile_kernel, scale=None):
+    """Return exact dense output and its block-quantized top-mass route."""
+    del compile_kernel
+    if q.shape[0] != 1 or q.shape[1] != k.shape[1]:
+        raise ValueError("Flex bootstrap supports batch-1 self-attention")
+    output, lse = ops.bsa_fwd(q, k, v, scale=scale, return_lse=True)
+    mass = _block_attention_mass(q, k, lse, block_size, scale=scale)
+    return output, _top_mass_route(mass, mass_target, keep)
 
 
 def _pack_route(route):
@@ -120,7 +145,7 @@ def _route_keep(block_mask):
 
 
 class FlexReuseBackend:
-    """Sampled bootstrap followed by route reuse, updates and dense dispatch."""
+    """Dense bootstrap followed by reuse with optional exact or sampled route refresh."""
 
     name = "flex_reuse"
 
@@ -162,12 +187,6 @@ class FlexReuseBackend:
             raise ValueError("directional_update requires spatial_reorder")
         if c.route_samples > 32 or c.route_samples & (c.route_samples - 1):
             raise ValueError("route_samples must be a power of two <= 32 on the libdsa kernels")
-        if c.bootstrap_mode == "exact" or c.update_interval:
-            raise NotImplementedError(
-                "exact route bootstrap/refresh is not part of this build; "
-                "use bootstrap_mode='sampled' (optionally with sampled_update_interval)")
-        if c.directional_update:
-            raise NotImplementedError("the directional frontier update is not part of this build")
         self.dense = DenseBackend()
         self.state = {}
         self.route_streams = {}
@@ -193,6 +212,7 @@ class FlexReuseBackend:
         state.update({
             "route": pending["route"],
             "frontier": pending.get("frontier"),
+            "frontier_count": pending.get("frontier_count"),
             "block_mask": pending["block_mask"],
             "step": pending["source_step"],
         })
@@ -204,13 +224,17 @@ class FlexReuseBackend:
         keep = (_route_keep(block_mask)
                 if state.get("route") is not None and block_mask is not None else None)
         state["keep"] = keep
-        state["frontier_fraction"] = None
+        frontier = state.get("frontier")
+        state["frontier_fraction"] = (
+            float(np.float32(state["frontier_count"].item()) / np.float32(frontier.numel()))
+            if frontier is not None else None)
         state["dense"] = bool(threshold is not None and keep is not None and keep >= threshold)
         if state["dense"]:
             # A permanently dense state never reads its route again.
             state["route"] = None
             state["block_mask"] = None
             state["frontier"] = None
+            state["frontier_count"] = None
 
     def _is_final_step(self, step):
         return (self.config.release_after_final_step
@@ -231,6 +255,25 @@ class FlexReuseBackend:
             return 0
         return math.ceil((grid[1] * grid[2]) / self.config.block_size)
 
+    def _with_frontier(self, state, result):
+        """Attach the frontier of the final route when a spatial layout exists."""
+        layout = state.get("layout")
+        if layout is None:
+            result["frontier"] = None
+            result["frontier_count"] = None
+            return result
+        route = result["route"]
+        result["frontier"], result["frontier_count"] = ops.frontier_mask(
+            route, layout.neighbors(route.device), return_count=True)
+        return result
+
+    def _exact_route(self, state, mass):
+        """Top-mass route of the exact mass plus the sink (flex.py:708-716, 784-792)."""
+        route, counts = ops.route_select(
+            mass, self.config.mass_target, self.config.keep,
+            sink_blocks=self._sink_blocks(state))
+        return self._with_frontier(state, {"route": route, "counts": counts})
+
     def _sampled_route(self, state, q, k, softmax_scale):
         mass = _sampled_block_mass(
             q, k, self.config.block_size,
@@ -239,13 +282,24 @@ class FlexReuseBackend:
             query_block_chunk=self.config.sample_query_block_chunk,
         )
         previous = state.get("route")
+        layout = state.get("layout")
+        if self.config.directional_update and previous is not None and layout is not None:
+            c = self.config
+            result = directional_budget_update(
+                mass, previous, layout.neighbors(q.device), keep=c.keep,
+                persistence=c.route_persistence, min_ratio=c.direction_min_ratio,
+                candidate_bonus=c.direction_candidate_bonus, budget_scale=c.route_budget_scale,
+                exploration_fraction=c.route_exploration_fraction, expand_q=c.direction_expand_q,
+                expand_k=c.direction_expand_k, expand_joint=c.direction_expand_joint,
+                previous_frontier=state.get("frontier"), sink_blocks=self._sink_blocks(state))
+            return self._with_frontier(state, result)
         use_prior = bool(self.config.route_persistence) and previous is not None
         route, counts = ops.route_select(
             mass, self.config.mass_target, self.config.keep,
             previous=previous if use_prior else None,
             persistence=self.config.route_persistence if use_prior else 0.0,
             sink_blocks=self._sink_blocks(state))
-        return {"route": route, "frontier": None, "counts": counts}
+        return self._with_frontier(state, {"route": route, "counts": counts})
 
     def _add_first_frame_sink(self, state, result):
         if not self.config.first_frame_sink:
@@ -258,13 +312,14 @@ class FlexReuseBackend:
         result = dict(result)
         result["route"] = route
         result.pop("counts", None)
-        return result
+        return self._with_frontier(state, result)
 
     def _install_route(self, state, result, tokens):
         route = result["route"]
         state.update({
             "route": route,
             "frontier": result.get("frontier"),
+            "frontier_count": result.get("frontier_count"),
             "block_mask": _build_block_mask(route, tokens, self.config.block_size,
                                             result.get("counts")),
         })
@@ -299,6 +354,7 @@ class FlexReuseBackend:
         state["pending"] = {
             "route": route,
             "frontier": result.get("frontier"),
+            "frontier_count": result.get("frontier_count"),
             "block_mask": block_mask,
             "source_step": step,
             "ready": ready,
@@ -386,8 +442,6 @@ class FlexReuseBackend:
         key = (attention_id, branch, q.shape[1], q.shape[2], q.shape[3], q.device,
                layout.signature if layout is not None else None)
         if step == 0 or key not in self.state:
-            # Sampled bootstrap: complete dense output, route from samples.
-            output = dense_output()
             state = {
                 "route": None,
                 "frontier": None,
@@ -397,12 +451,23 @@ class FlexReuseBackend:
                 "grid": grid,
             }
             self.state[key] = state
-            if (self.config.prefetch_sampled_bootstrap
+            if self.config.bootstrap_mode == "exact":
+                # Dense output with its LSE, then one exact block-mass pass.
+                output, lse = ops.bsa_fwd(q, k, v, scale=softmax_scale, return_lse=True)
+                mass = _block_attention_mass(q, k, lse, self.config.block_size,
+                                             scale=softmax_scale)
+                self._install_route(state, self._exact_route(state, mass), q.shape[1])
+                self._update_dispatch(state)
+                self.phase_counts["dense_bootstrap"] += 1
+            # Sampled bootstrap: complete dense output, route from samples.
+            elif (self.config.prefetch_sampled_bootstrap
                     and (self.config.total_steps is None
                          or step < self.config.total_steps - 1)):
+                output = dense_output()
                 self._prefetch_sampled_route(state, q, k, step, softmax_scale,
                                              phase="sampled_bootstrap")
             else:
+                output = dense_output()
                 result = self._sampled_route(state, q, k, softmax_scale)
                 self._install_route(state, result, q.shape[1])
                 self._update_dispatch(state)
@@ -418,6 +483,18 @@ class FlexReuseBackend:
             output = dense_output()
             if self._is_final_step(step):
                 self._release_route(key, state)
+            return finish(output)
+
+        if (self.config.update_interval > 0
+                and (step - state["step"]) >= self.config.update_interval
+                and not self._is_final_step(step)):
+            output, lse = ops.bsa_fwd(q, k, v, scale=softmax_scale, return_lse=True)
+            mass = _block_attention_mass(q, k, lse, self.config.block_size, scale=softmax_scale)
+            state["block_mask"] = None
+            self._install_route(state, self._exact_route(state, mass), q.shape[1])
+            state["step"] = step
+            self._update_dispatch(state)
+            self.phase_counts["exact_refresh"] += 1
             return finish(output)
 
         sampled_update_due = (

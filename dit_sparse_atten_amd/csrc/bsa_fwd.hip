@@ -28,7 +28,7 @@
 //  * online softmax with a lazily moved reference max (rescale only when a
 //    score exceeds it by 2^8); row sums add the fp32 P in plain VALU adds
 //    (v_dot2 would contend with the matrix core for issue).
-#include "dsa_common.h"
+#include "bsa_tiles.h"
 
 namespace {
 
@@ -49,17 +49,17 @@ struct BsaParams {
   float scale_log2;  // scale * log2(e)
 };
 
-constexpr int kHeadDim = 128;
-constexpr int kRowBytes = kHeadDim * 2;        // one K row: 256 bytes
-constexpr int kHalfKeys = 64;                  // keys per pipelined half-tile
-constexpr int kKStage = kHalfKeys * kRowBytes; // 16 KB LDS stage (K or V^T)
-constexpr float kRescaleLog2 = 8.0f;           // move the max once p could exceed 2^8
+using dsa::kHeadDim;
+using dsa::kRowBytes;
+using dsa::kHalfKeys;
+using dsa::kKStage;
+using dsa::k2_swz;
+using dsa::k_tile_rsrc;
+using dsa::lds_load16;
+using dsa::make_rsrc;
+typedef dsa::const_i32 dsa_const_i32;
 
-typedef const __attribute__((address_space(4))) int32_t* dsa_const_i32;
-
-// K stage [64 keys][128 dims]: 16-byte chunk XOR (row & 15), so the 32 rows a
-// fragment load reads at one chunk hit distinct banks.
-__device__ __forceinline__ int k2_swz(int r, int c) { return c ^ (r & 15); }
+constexpr float kRescaleLog2 = 8.0f;  // move the max once p could exceed 2^8
 
 constexpr int kVtHalfRow = kHalfKeys * 2;  // 128 B: one head dim of a 64-key half-tile
 
@@ -67,51 +67,6 @@ constexpr int kVtHalfRow = kHalfKeys * 2;  // 128 B: one head dim of a 64-key ha
 // (even / odd d alternate); chunk XOR ((d >> 1) & 7) spreads the 16 rows read
 // per 16 lanes over distinct bank groups.
 __device__ __forceinline__ int vt9_swz(int d, int c) { return c ^ ((d >> 1) & 7); }
-
-// Raw buffer resources for the direct-to-LDS loads.  The MUBUF form
-// (buffer_load ... lds) is used rather than global_load_lds because the
-// compiler counts the latter as an LGKM event of unknown order and then waits
-// for every outstanding LDS read (lgkmcnt(0)) before each fragment use; MUBUF
-// LDS loads only count on vmcnt.  Dword 3 is the gfx9 raw-buffer format word.
-// A raw buffer (stride 0) returns zeros for offsets at or past num_records
-// (the vector offset is checked, the scalar offset is not).
-constexpr int kBufferDword3 = 0x00020000;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferDword3);
-}
-
-// 16 bytes per lane into LDS at lds + 16 * lane.
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds,
-                                           uint32_t voffset, uint32_t soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (DSA_LDS void*)lds, 16, voffset, soffset, 0, 0);
-}
-
-// The same load issued through inline asm.  The compiler then does not track
-// it: its LDS-DMA alias tracking cannot tell the double-buffer stages of the
-// ping-pong kernel apart and would otherwise wait for every outstanding stage
-// load (vmcnt(0)) before the first fragment read of each phase.  Ordering is
-// carried entirely by the caller's explicit vmcnt waits and barriers; the
-// "memory" clobber keeps other memory accesses on their side of the load.
-// M0 (the LDS base) needs one wait state after the SALU write.
-__device__ __forceinline__ void lds_load16_async(__amdgpu_buffer_rsrc_t rsrc, unsigned char* lds,
-                                                 uint32_t voffset, uint32_t soffset) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(DSA_LDS void*)lds);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(m0), "v"(voffset), "s"(rsrc), "s"(soffset)
-               : "memory");
-}
-
-// Resource covering the 64 K rows of a half-tile starting at key0; rows at or
-// past kv_tokens read as zeros (a half-tile wholly past the end has no
-// records).  The host keeps 64 rows of K within 2^31 bytes.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t k_tile_rsrc(const __bf16* kbase, int64_t k_st,
-                                                             int key0, int kv_tokens) {
-  const int rows = min(kHalfKeys, kv_tokens - key0);
-  const uint32_t bytes = rows > 0 ? (uint32_t)((rows - 1) * k_st * 2 + kRowBytes) : 0u;
-  return make_rsrc(kbase + (int64_t)key0 * k_st, bytes);
-}
 
 // One workgroup per (b, h, 64-key chunk): rows of V through LDS, columns out.
 __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restrict__ v,
@@ -135,7 +90,7 @@ __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restr
                                                 (int64_t)(key0 + r) * v_st + c * 8);
     *reinterpret_cast<dsa_u32x4*>(&tile[r][c * 8]) = val;
   }
-  __syncthreads();
+  dsa::lds_barrier();
   __bf16* out = vt + ((int64_t)bh * kHeadDim) * tpad + (int64_t)key0 * kHeadDim;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {

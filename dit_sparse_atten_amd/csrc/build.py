@@ -20,7 +20,9 @@ LIBRARY = PACKAGE / "libdsa.so"
 SOURCES = (
     "dsa_api.hip",
     "bsa_fwd.hip",
+    "block_mass.hip",
     "route.hip",
+    "routing.hip",
     "permute.hip",
 )
 

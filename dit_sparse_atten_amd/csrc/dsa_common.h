@@ -48,4 +48,17 @@ __device__ __forceinline__ int xcd_remap(int wg, int total) {
   return xcd * per + (xcd < rem ? xcd : rem) + slot;
 }
 
+// Workgroup barrier after which every wave sees the LDS writes (and reads)
+// that any wave issued before it.  __syncthreads alone orders LDS through the
+// hardware LDS queue only, and a ds_write issued just before the barrier has
+// been seen to land after another wave's ds_read issued just after it (under
+// concurrent buffer->LDS traffic), so each wave first retires its own LDS
+// operations (lgkmcnt(0)).  kWithVmem also retires vector memory operations
+// (vmcnt(0)), which includes this wave's buffer->LDS loads.
+template <bool kWithVmem = false>
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(kWithVmem ? 0x0070 : 0xC07F);  // [vmcnt(0)] lgkmcnt(0)
+  __syncthreads();
+}
+
 }  // namespace dsa

@@ -15,9 +15,14 @@
 // fp32(fp32(sum) * fp32(target)); prior m' = fp32(m + fp32(rho * fp32(sum/K)));
 // order = value descending, key index ascending; count = #{prefix < threshold}
 // + 1, clamped to the cap; then the sink columns are OR-ed in.
-#include "dsa_common.h"
+#include "route_common.h"
 
 namespace {
+
+using dsa::fixed_to_f32;
+using dsa::to_fixed;
+using dsa::wave_sum_i32;
+using dsa::wave_sum_i64;
 
 constexpr int kHeadDim = 128;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -192,29 +197,6 @@ struct SelectParams {
   float rho, target;
 };
 
-constexpr double kFixedScale = 4503599627370496.0;  // 2^52
-constexpr float kInvFixed = 2.220446049250313e-16f; // 2^-52
-
-__device__ __forceinline__ int64_t to_fixed(float v) {
-  return (int64_t)__builtin_floor((double)v * kFixedScale);
-}
-
-__device__ __forceinline__ float fixed_to_f32(int64_t x) {
-  return (float)x * kInvFixed;  // i64 -> f32 rounds to nearest even
-}
-
-__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
-  return v;
-}
-
-__device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
-  return v;
-}
-
 __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
   __shared__ uint8_t flags[4][512];
   const int lane = threadIdx.x & 63;
@@ -252,45 +234,14 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
   total = wave_sum_i64(total);
   const float threshold = fixed_to_f32(total) * p.target;
 
-  // Bitonic sort, descending, of key = value bits << 32 | (511 - index).
+  // Descending sort of key = value bits << 32 | (511 - index).
   uint64_t key[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int e = lane * 8 + j;
     key[j] = e < K ? ((uint64_t)__float_as_uint(v[j]) << 32) | (uint32_t)(511 - e) : 0ull;
   }
-#pragma unroll
-  for (int size = 2; size <= 512; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride >= 8) {
-        const int lane_mask = stride >> 3;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int e = lane * 8 + j;
-          const uint64_t other = __shfl_xor((unsigned long long)key[j], lane_mask);
-          const bool desc = (e & size) == 0;
-          const bool lower = (e & stride) == 0;
-          const uint64_t hi = key[j] > other ? key[j] : other;
-          const uint64_t lo = key[j] > other ? other : key[j];
-          key[j] = (desc == lower) ? hi : lo;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (j & stride) continue;
-          const int jp = j | stride;
-          const int e = lane * 8 + j;
-          const bool desc = (e & size) == 0;
-          const uint64_t a = key[j], b = key[jp];
-          const uint64_t hi = a > b ? a : b;
-          const uint64_t lo = a > b ? b : a;
-          key[j] = desc ? hi : lo;
-          key[jp] = desc ? lo : hi;
-        }
-      }
-    }
-  }
+  dsa::sort512_desc(key, lane);
 
   // Exact prefix sums in sorted order.
   int64_t pre[8];
@@ -370,12 +321,12 @@ __global__ void __launch_bounds__(1024) scan_counts_kernel(const int32_t* counts
   int64_t local = 0;
   for (int i = begin; i < end; ++i) local += counts[i];
   partial[t] = local;
-  __syncthreads();
+  dsa::lds_barrier();
   for (int offset = 1; offset < 1024; offset <<= 1) {
     const int64_t add = t >= offset ? partial[t - offset] : 0;
-    __syncthreads();
+    dsa::lds_barrier();
     partial[t] += add;
-    __syncthreads();
+    dsa::lds_barrier();
   }
   int64_t run = partial[t] - local;
   for (int i = begin; i < end; ++i) {

@@ -1,0 +1,75 @@
+// Row arithmetic shared by the route kernels (gfx950): exact fixed-point row
+// sums and a one-wave 512-key bitonic sort.
+//
+// A row value m >= 0 is represented as the integer floor(m * 2^52), so row and
+// prefix sums are exact and independent of summation order; a sum is rounded
+// once to fp32.  The CPU oracle uses the same arithmetic, which makes routes
+// bit-exact given the same fp32 inputs.
+#pragma once
+
+#include "dsa_common.h"
+
+namespace dsa {
+
+constexpr double kFixedScale = 4503599627370496.0;  // 2^52
+constexpr float kInvFixed = 2.220446049250313e-16f; // 2^-52
+
+__device__ __forceinline__ int64_t to_fixed(float v) {
+  return (int64_t)__builtin_floor((double)v * kFixedScale);
+}
+
+__device__ __forceinline__ float fixed_to_f32(int64_t x) {
+  return (float)x * kInvFixed;  // i64 -> f32 rounds to nearest even
+}
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// Sorts the 512 keys of one wave (element e = lane * 8 + j in key[j]) into
+// descending order, in place: a bitonic network, with partners eight or more
+// elements apart exchanged across lanes and closer ones inside a lane.
+__device__ __forceinline__ void sort512_desc(uint64_t key[8], int lane) {
+#pragma unroll
+  for (int size = 2; size <= 512; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= 8) {
+        const int lane_mask = stride >> 3;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int e = lane * 8 + j;
+          const uint64_t other = __shfl_xor((unsigned long long)key[j], lane_mask);
+          const bool desc = (e & size) == 0;
+          const bool lower = (e & stride) == 0;
+          const uint64_t hi = key[j] > other ? key[j] : other;
+          const uint64_t lo = key[j] > other ? other : key[j];
+          key[j] = (desc == lower) ? hi : lo;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (j & stride) continue;
+          const int jp = j | stride;
+          const int e = lane * 8 + j;
+          const bool desc = (e & size) == 0;
+          const uint64_t a = key[j], b = key[jp];
+          const uint64_t hi = a > b ? a : b;
+          const uint64_t lo = a > b ? b : a;
+          key[j] = desc ? hi : lo;
+          key[jp] = desc ? lo : hi;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace dsa

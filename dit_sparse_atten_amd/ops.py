@@ -197,6 +197,48 @@ def sampled_block_mass(q, k, block_size, samples=2, scale=None):
     return mass
 
 
+def block_mass(q, k, lse, block_size=128, scale=None):
+    """Exact block attention mass [heads, blocks, blocks] fp32 of a batch-1 call.
+
+    Same contract as the reference's ``_block_attention_mass``
+    (attention_backends/flex.py:158-202): ``lse`` is the natural-log
+    normaliser of every query row ([1, H, T] or [H, T], as ``bsa_fwd(...,
+    return_lse=True)`` returns it) and mass[h, qb, kb] sums
+    exp(scale * q.k - lse) over the tokens of the two blocks.
+    """
+    lib = _lib.load()
+    if q.shape[0] != 1 or q.shape[1] != k.shape[1]:
+        raise ValueError("Flex bootstrap supports batch-1 self-attention")
+    if block_size != 128:
+        raise ValueError("The exact mass kernel currently requires block_size=128")
+    q = _kernel_view("q", q)
+    k = _kernel_view("k", k)
+    _, tokens, heads, head_dim = q.shape
+    _require_cuda("lse", lse)
+    if lse.dtype != torch.float32:
+        raise ValueError("lse must be float32")
+    if lse.ndim == 3:
+        if lse.shape[0] != 1:
+            raise ValueError("lse must have shape [1, heads, tokens] or [heads, tokens]")
+        lse = lse[0]
+    if tuple(lse.shape) != (heads, tokens):
+        raise ValueError("lse must have shape [1, heads, tokens] or [heads, tokens]")
+    if lse.stride(1) != 1:
+        lse = lse.contiguous()
+    if scale is None:
+        scale = head_dim ** -0.5
+    blocks = math.ceil(tokens / block_size)
+    mass = torch.empty((heads, blocks, blocks), dtype=torch.float32, device=q.device)
+    strides = _lib.int64_array([q.stride(1), q.stride(2), k.stride(1), k.stride(2)])
+    with torch.cuda.device(q.device):
+        status = lib.dsa_block_mass(
+            q.data_ptr(), k.data_ptr(), strides, tokens, heads, head_dim, block_size,
+            lse.data_ptr(), lse.stride(0), float(scale), mass.data_ptr(),
+            _stream_handle(q.device))
+    _lib.check(status, "dsa_block_mass")
+    return mass
+
+
 def route_select(mass, target, keep, previous=None, persistence=0.0, sink_blocks=0):
     """Prior + top-mass selection + sink on the GPU.
 
@@ -231,6 +273,89 @@ def route_select(mass, target, keep, previous=None, persistence=0.0, sink_blocks
             int(sink_blocks), route.data_ptr(), counts.data_ptr(), _stream_handle(mass.device))
     _lib.check(status, "dsa_route_select")
     return route, counts
+
+
+def _neighbor_table(neighbors, blocks, device):
+    _require_cuda("neighbors", neighbors)
+    if tuple(neighbors.shape) != (blocks, 4):
+        raise ValueError("neighbors must have shape [blocks, 4]")
+    if neighbors.device != device:
+        raise ValueError("neighbors must live on the route device")
+    return neighbors.to(torch.int32).contiguous()
+
+
+def frontier_mask(route, neighbors, return_count=False):
+    """Selected route cells with an unselected valid neighbour along the query
+    or key axis (attention_backends/routing.py:35-41).  route: bool [H, B, B];
+    neighbors: int [B, 4] (-1 = none).  With ``return_count`` also returns the
+    number of frontier cells as a device int64 tensor."""
+    lib = _lib.load()
+    route = _require_bool_route(route)
+    if route.ndim != 3 or route.shape[1] != route.shape[2]:
+        raise ValueError("route must have shape [heads, blocks, blocks]")
+    heads, blocks, _ = route.shape
+    neighbors = _neighbor_table(neighbors, blocks, route.device)
+    frontier = torch.empty_like(route)
+    count = torch.empty(1, dtype=torch.int64, device=route.device) if return_count else None
+    with torch.cuda.device(route.device):
+        status = lib.dsa_frontier_mask(
+            route.data_ptr(), heads, blocks, neighbors.data_ptr(), frontier.data_ptr(),
+            count.data_ptr() if count is not None else None, _stream_handle(route.device))
+    _lib.check(status, "dsa_frontier_mask")
+    return (frontier, count) if return_count else frontier
+
+
+def directional_update(mass, previous, neighbors, *, keep, persistence=0.5, min_ratio=0.0,
+                       candidate_bonus=0.0, budget_scale=1.0, exploration_fraction=0.0,
+                       expand_q=True, expand_k=True, expand_joint=True,
+                       previous_frontier=None, sink_blocks=0):
+    """Frontier-aware directional route update on the GPU.
+
+    Same contract as the reference's ``directional_budget_update``
+    (attention_backends/routing.py:92-168), followed by the first
+    ``sink_blocks`` columns (flex.py:544-546).  Returns a dict with route
+    (after the sink), counts (int32 [H, B], sink included), candidates,
+    exploration, dropped and added (the last two before the sink, as the
+    reference reports them).
+    """
+    lib = _lib.load()
+    _require_cuda("mass", mass)
+    if mass.dtype != torch.float32:
+        raise ValueError("mass must be float32")
+    previous = _require_bool_route(previous)
+    if previous.shape != mass.shape:
+        raise ValueError("previous route and mass must have identical shapes")
+    if mass.ndim != 3 or mass.shape[1] != mass.shape[2]:
+        raise ValueError("mass must have shape [heads, blocks, blocks]")
+    if budget_scale <= 0:
+        raise ValueError("budget_scale must be positive")
+    if not 0 <= exploration_fraction <= 1:
+        raise ValueError("exploration_fraction must be in [0, 1]")
+    heads, blocks, _ = mass.shape
+    mass = mass.contiguous()
+    neighbors = _neighbor_table(neighbors, blocks, mass.device)
+    if previous_frontier is not None:
+        previous_frontier = _require_bool_route(previous_frontier)
+        if previous_frontier.shape != mass.shape:
+            raise ValueError("previous_frontier must match the route shape")
+    cap = max(1, math.ceil(blocks * keep))
+    explore = max(1, math.ceil(blocks * exploration_fraction)) if exploration_fraction else 0
+    flags = (1 if expand_q else 0) | (2 if expand_k else 0) | (4 if expand_joint else 0)
+    outputs = {name: torch.empty(mass.shape, dtype=torch.bool, device=mass.device)
+               for name in ("route", "candidates", "exploration", "dropped", "added")}
+    counts = torch.empty((heads, blocks), dtype=torch.int32, device=mass.device)
+    with torch.cuda.device(mass.device):
+        status = lib.dsa_directional_update(
+            mass.data_ptr(), previous.data_ptr(),
+            previous_frontier.data_ptr() if previous_frontier is not None else None,
+            neighbors.data_ptr(), heads, blocks, cap, float(persistence), float(min_ratio),
+            float(candidate_bonus), float(budget_scale), explore, flags, int(sink_blocks),
+            outputs["route"].data_ptr(), counts.data_ptr(), outputs["candidates"].data_ptr(),
+            outputs["exploration"].data_ptr(), outputs["dropped"].data_ptr(),
+            outputs["added"].data_ptr(), _stream_handle(mass.device))
+    _lib.check(status, "dsa_directional_update")
+    outputs["counts"] = counts
+    return outputs
 
 
 def route_to_csr(route, counts=None, block_size=128):

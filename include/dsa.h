@@ -78,6 +78,21 @@ int dsa_sampled_mass(const void* q, const void* k, const int64_t* strides, int32
                      float scale, float* mass, hipStream_t stream);
 
 /*
+ * Exact block attention mass of one batch-1 self-attention call.
+ * Replaces `_block_attention_mass` and its Triton `_exact_block_mass_kernel`
+ * (attention_backends/flex.py:96-202): mass[h, qb, kb] = sum over the valid
+ * query tokens t of block qb and key tokens s of block kb of
+ * exp(scale * <q_t, k_s> - lse[h, t]).  lse: [heads, tokens] fp32 natural-log
+ * normaliser of the same Q/K and scale (dsa_bsa_fwd's lse output), head
+ * stride lse_head_stride >= tokens.  strides[4]: q (t, h), k (t, h) in
+ * elements.  head_dim 128, block_size 128.  mass: [heads, blocks, blocks],
+ * every entry written (no initialisation needed); deterministic.
+ */
+int dsa_block_mass(const void* q, const void* k, const int64_t* strides, int32_t tokens,
+                   int32_t heads, int32_t head_dim, int32_t block_size, const float* lse,
+                   int64_t lse_head_stride, float scale, float* mass, hipStream_t stream);
+
+/*
  * Persistence prior + top-mass selection + first-frame sink, per row.
  * Replaces the prior of `_sampled_route` (flex.py:535-541), `_top_mass_route`
  * (flex.py:83-94, == sparse.py:171-181 `_row_mask`) and `_add_first_frame_sink`
@@ -89,6 +104,43 @@ int dsa_sampled_mass(const void* q, const void* k, const int64_t* strides, int32
 int dsa_route_select(const float* mass, const uint8_t* previous, int32_t rows, int32_t keys,
                      float rho, float target, int32_t cap, int32_t sink_blocks, uint8_t* route,
                      int32_t* counts, hipStream_t stream);
+
+/*
+ * Frontier of a route: selected cells (h, q, k) with an unselected valid
+ * neighbour along the query axis (route[h, nb[q][d], k]) or the key axis
+ * (route[h, q, nb[k][d]]).  Replaces `frontier_mask`
+ * (attention_backends/routing.py:10-41).  route, frontier: [heads, blocks,
+ * blocks] bytes; neighbors: [blocks, 4] int32 (-1 = none), blocks <= 512.
+ * count (optional, device) receives the number of frontier cells.
+ */
+int dsa_frontier_mask(const uint8_t* route, int32_t heads, int32_t blocks,
+                      const int32_t* neighbors, uint8_t* frontier, unsigned long long* count,
+                      hipStream_t stream);
+
+/*
+ * Frontier-aware directional route update with a per-row budget.
+ * Replaces `directional_budget_update` (attention_backends/routing.py:92-168,
+ * with `_sparse_best_targets` 53-80 and `_select_fixed_budget` 83-89) and the
+ * first-frame sink that flex.py:544-546 applies to its result.
+ *   mass: [heads, blocks, blocks] fp32, non-negative; previous: route bytes;
+ *   previous_frontier: bytes or NULL (then the frontier of previous);
+ *   neighbors: [blocks, 4] int32, blocks <= 512; cap = max(1, ceil(blocks *
+ *   keep)); explore_count = 0 or max(1, ceil(blocks * exploration_fraction));
+ *   expand_flags: 1 query axis, 2 key axis, 4 joint.
+ * Outputs (bytes, [heads, blocks, blocks]): route (selection, then the first
+ * sink_blocks columns set), candidates (required, 16-byte aligned; also the
+ * scatter scratch), and optionally exploration, dropped and added (before
+ * the sink, as the reference's result dict); counts [heads, blocks] = set
+ * entries per route row.
+ */
+int dsa_directional_update(const float* mass, const uint8_t* previous,
+                           const uint8_t* previous_frontier, const int32_t* neighbors,
+                           int32_t heads, int32_t blocks, int32_t cap, float persistence,
+                           float min_ratio, float candidate_bonus, float budget_scale,
+                           int32_t explore_count, int32_t expand_flags, int32_t sink_blocks,
+                           uint8_t* route, int32_t* counts, uint8_t* candidates,
+                           uint8_t* exploration, uint8_t* dropped, uint8_t* added,
+                           hipStream_t stream);
 
 /*
  * Boolean route rows -> CSR (ascending key blocks per row).

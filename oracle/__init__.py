@@ -31,6 +31,16 @@ from the reference imported in the build container):
                (layout_ops.py:128-151), to_csr (flex.py:275-338), route_keep /
                dense_dispatch (flex.py:473-493): known answers from the
                reference's tests, stable argsort, round trips.
+  exact        dense_lse, exact_block_mass(_rows), exact_route (flex.py:96-106,
+               158-202, 254-272): the reference's own identities (full sampling
+               S = block equals exact / block, test_flex_backend.py:43-53;
+               explicit padded softmax, test_flex_backend.py:62-76), rows summing
+               to the valid query count, planted mistakes.
+  routing      frontier_mask, best_targets, select_fixed_budget,
+               directional_budget_update (routing.py:10-168): reference golden
+               (routing.npz: two frontiers and three directional updates on the
+               720p neighbour table, bit-exact), the reference's known answers
+               (test_directional_routing.py), invariants, planted mistakes.
   spatial      morton_code, choose_microtile, spatial_layout (spatial.py:14-183)
                and sparse_tile_shape / tile_major_permutation (sparse.py:51-138):
                reference golden (spatial_layout.npz, the full 57,600-token

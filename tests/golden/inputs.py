@@ -40,3 +40,19 @@ def clustered_qkv(tokens, heads, head_dim=128, group=64, seed=0, permutation=Non
     q = 0.5 * q_noise + q_centroid[:, group_of]
     k = 0.5 * k_noise + k_centroid[:, group_of]
     return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def route_mass(heads, blocks, seed):
+    """Heavy-tailed non-negative block mass [heads, blocks, blocks] float32:
+    u^4 for u ~ U[0, 1).  Only elementwise fp32 products of the generator's
+    output, so every machine reproduces it bit for bit."""
+    generator = torch.Generator().manual_seed(seed)
+    u = torch.rand((heads, blocks, blocks), generator=generator)
+    u2 = u * u
+    return u2 * u2
+
+
+def random_route(heads, blocks, seed, keep=0.625):
+    """Bernoulli(keep) boolean route [heads, blocks, blocks]."""
+    generator = torch.Generator().manual_seed(seed)
+    return torch.rand((heads, blocks, blocks), generator=generator) < keep

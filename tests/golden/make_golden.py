@@ -8,6 +8,9 @@ run here:
   * FlexReuseBackend._sampled_route   persistence prior + selection
   * spatial.build_spatial_layout      Morton order and majority-vote neighbours
   * sparse.MatrixSparseBackend  config-0 bootstrap route, mass and outputs
+  * routing.frontier_mask / directional_budget_update   on the 720p block
+    neighbour table (the known answers of test_directional_routing.py cover
+    one line-shaped case only)
 This script runs in the build container only (it reads /root/reference);
 tests, smoke() and bench.py read the .npz files it writes and never the
 reference.  Regenerate with:  python tests/golden/make_golden.py
@@ -26,15 +29,15 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parents[1]))
 REFERENCE = Path(os.environ.get("DSA_REFERENCE", "/root/reference"))
 
-from tests.golden.inputs import clustered_qkv  # noqa: E402
+from tests.golden.inputs import clustered_qkv, random_route, route_mass  # noqa: E402
 
 
 def _reference_modules():
     if not REFERENCE.exists():
         raise SystemExit(f"reference not found at {REFERENCE}")
     sys.path.insert(0, str(REFERENCE))
-    from attention_backends import context, flex, sparse, spatial  # noqa: PLC0415
-    return context, flex, sparse, spatial
+    from attention_backends import context, flex, routing, sparse, spatial  # noqa: PLC0415
+    return context, flex, routing, sparse, spatial
 
 
 def _save(name, **arrays):
@@ -153,14 +156,49 @@ def sparse_config0_fixture(context, sparse):
           out0=out0[0, :256, heads_kept].numpy(), out1=out1[0, :256, heads_kept].numpy())
 
 
+ROUTING_CASES = {
+    # name: (mass seed, previous seed, previous keep, explicit previous frontier, kwargs)
+    "default": (11, 12, 0.625, False, dict(keep=0.625)),
+    "tuned": (13, 14, 0.55, True, dict(
+        keep=0.625, persistence=0.5, min_ratio=0.5, candidate_bonus=0.25, budget_scale=0.8,
+        exploration_fraction=0.02, expand_joint=False)),
+    "q_only": (15, 16, 0.4, False, dict(
+        keep=0.5, persistence=0.0, budget_scale=1.3, expand_k=False, expand_joint=False)),
+}
+
+
+def routing_fixture(routing, spatial):
+    """frontier_mask and directional_budget_update on the 16x45x80 layout's
+    450-block neighbour table (one head; inputs regenerated from seeds)."""
+    layout = spatial.build_spatial_layout((16, 45, 80), 128, 32)
+    neighbors = layout.neighbors_cpu
+    arrays = {"neighbors": neighbors.numpy()}
+    for name, seed, keep in (("frontier_p625", 21, 0.625), ("frontier_p90", 22, 0.9)):
+        route = random_route(1, 450, seed, keep)
+        arrays[f"{name}__params"] = np.array([seed, keep])
+        arrays[f"{name}__frontier"] = np.packbits(routing.frontier_mask(route, neighbors).numpy())
+    for name, (mass_seed, prev_seed, prev_keep, explicit, kwargs) in ROUTING_CASES.items():
+        mass = route_mass(1, 450, mass_seed)
+        previous = random_route(1, 450, prev_seed, prev_keep)
+        frontier = routing.frontier_mask(previous, neighbors) if explicit else None
+        result = routing.directional_budget_update(
+            mass, previous, neighbors, previous_frontier=frontier, **kwargs)
+        arrays[f"{name}__checksum"] = np.array([mass.double().sum().item(),
+                                                float(previous.sum().item())])
+        for key in ("route", "frontier", "candidates", "exploration"):
+            arrays[f"{name}__{key}"] = np.packbits(result[key].numpy())
+    _save("routing", **arrays)
+
+
 def main():
     torch.set_num_threads(4)
-    context, flex, sparse, spatial = _reference_modules()
+    context, flex, routing, sparse, spatial = _reference_modules()
     top_mass_fixture(flex)
     sampled_mass_fixture(flex)
     sampled_route_fixture(flex)
     spatial_fixture(spatial)
     sparse_config0_fixture(context, sparse)
+    routing_fixture(routing, spatial)
 
 
 if __name__ == "__main__":

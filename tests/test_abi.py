@@ -64,3 +64,31 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
     assert status == _lib.DSA_EUNSUPPORTED and "power of two" in _lib.last_error()
     status = lib.dsa_permute_rows(4, None, None, None, None, None, 1, 1, 1, 16, None)
     assert status == _lib.DSA_EINVAL
+
+
+def test_exact_and_routing_entry_points_validate_first(lib):
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    strides = _lib.int64_array([8] * 4)
+    status = lib.dsa_block_mass(fake, fake, strides, 256, 2, 64, 128, fake, 256, 0.1, fake, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
+    status = lib.dsa_block_mass(fake, fake, strides, 256, 2, 128, 128, fake, 100, 0.1, fake,
+                                None)
+    assert status == _lib.DSA_EINVAL and "lse" in _lib.last_error()
+    status = lib.dsa_block_mass(fake, fake, strides, 256, 2, 128, 128, fake, 256, -1.0, fake,
+                                None)
+    assert status == _lib.DSA_EINVAL and "scale" in _lib.last_error()
+    status = lib.dsa_frontier_mask(fake, 2, 600, fake, fake, None, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "512" in _lib.last_error()
+    status = lib.dsa_frontier_mask(fake, 2, 16, None, fake, None, None)
+    assert status == _lib.DSA_EINVAL and "neighbors" in _lib.last_error()
+    aligned = ctypes.c_void_p(4096)
+    status = lib.dsa_directional_update(fake, fake, None, fake, 2, 16, 0, 0.5, 0.0, 0.0, 1.0,
+                                        0, 7, 0, fake, fake, aligned, None, None, None, None)
+    assert status == _lib.DSA_EINVAL and "cap" in _lib.last_error()
+    status = lib.dsa_directional_update(fake, fake, None, fake, 2, 16, 8, 0.5, 0.0, 0.0, 0.0,
+                                        0, 7, 0, fake, fake, aligned, None, None, None, None)
+    assert status == _lib.DSA_EINVAL and "budget_scale" in _lib.last_error()
+    status = lib.dsa_directional_update(fake, fake, None, fake, 2, 16, 8, 0.5, 0.0, 0.0, 1.0,
+                                        0, 7, 0, fake, fake, ctypes.c_void_p(4097), None, None,
+                                        None, None)
+    assert status == _lib.DSA_EINVAL and "aligned" in _lib.last_error()
