@@ -261,6 +261,21 @@ def main():
     }
     if traffic:
         result["roofline"]["hbm_gbs_at_traffic"] = round(traffic / (kernel_ms * 1e-3) / 1e9, 1)
+    if not args.only_sparse:
+        # What the matrix cores sustain on this box for random bf16 data under
+        # its power limit: the vendor GEMM (hipBLASLt through torch.mm), 16384^3.
+        gemm_n = 16384
+        generator = torch.Generator(device=device).manual_seed(5)
+        ga = torch.randn(gemm_n, gemm_n, device=device, generator=generator).bfloat16()
+        gb = torch.randn(gemm_n, gemm_n, device=device, generator=generator).bfloat16()
+        gc = torch.empty_like(ga)
+        torch.mm(ga, gb, out=gc)
+        torch.cuda.synchronize()
+        gemm_ms, _ = timer.time(lambda: torch.mm(ga, gb, out=gc), 5)
+        gemm_tflops = 2.0 * gemm_n ** 3 / (gemm_ms * 1e-3) / 1e12
+        result["roofline"]["measured_bf16_gemm_tflops"] = round(gemm_tflops, 1)
+        result["roofline"]["frac_of_measured_gemm"] = round(achieved / gemm_tflops, 4)
+        del ga, gb, gc
 
     if not args.only_sparse:
         def dense_call():

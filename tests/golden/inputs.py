@@ -56,3 +56,45 @@ def random_route(heads, blocks, seed, keep=0.625):
     """Bernoulli(keep) boolean route [heads, blocks, blocks]."""
     generator = torch.Generator().manual_seed(seed)
     return torch.rand((heads, blocks, blocks), generator=generator) < keep
+
+
+def wan_rope_angles(grid, head_dim=128, theta=10000.0):
+    """Rotation angles [tokens, head_dim // 2] of a 3D RoPE over the (F, H, W)
+    latent grid, flattened frame-major: head dims split into a time part of
+    head_dim - 2 * 2 * (head_dim // 6) and two spatial parts of
+    2 * (head_dim // 6) each (44 / 42 / 42 at d = 128); each part rotates its
+    consecutive (even, odd) pairs by position * theta^(-2j / part)."""
+    frames, height, width = grid
+    spatial = 2 * (head_dim // 6)
+    parts = (head_dim - 2 * spatial, spatial, spatial)
+    positions = torch.stack(torch.meshgrid(
+        torch.arange(frames), torch.arange(height), torch.arange(width), indexing="ij"),
+        dim=-1).reshape(-1, 3).to(torch.float64)
+    angles = []
+    for axis, part in enumerate(parts):
+        freqs = theta ** (-torch.arange(0, part, 2, dtype=torch.float64) / part)
+        angles.append(positions[:, axis:axis + 1] * freqs[None])
+    return torch.cat(angles, dim=-1)
+
+
+def apply_rope(x, angles):
+    """Rotate the (even, odd) pairs of x [B, T, H, D] by angles [T, D/2];
+    computed in float64 and returned in x's dtype."""
+    x64 = x.to(torch.float64)
+    cos = torch.cos(angles)[None, :, None, :]
+    sin = torch.sin(angles)[None, :, None, :]
+    even, odd = x64[..., 0::2], x64[..., 1::2]
+    out = torch.empty_like(x64)
+    out[..., 0::2] = even * cos - odd * sin
+    out[..., 1::2] = even * sin + odd * cos
+    return out.to(x.dtype)
+
+
+def rope_qkv(grid, batch, heads, head_dim=128, seed=0, dtype=torch.bfloat16):
+    """BASELINE config 1 inputs: Q/K/V ~ N(0,1) [B, T, H, D], 3D RoPE on Q and K."""
+    tokens = grid[0] * grid[1] * grid[2]
+    generator = torch.Generator().manual_seed(seed)
+    shape = (batch, tokens, heads, head_dim)
+    q, k, v = (torch.randn(shape, generator=generator) for _ in range(3))
+    angles = wan_rope_angles(grid, head_dim)
+    return apply_rope(q, angles).to(dtype), apply_rope(k, angles).to(dtype), v.to(dtype)

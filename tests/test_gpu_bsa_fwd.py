@@ -90,3 +90,55 @@ def test_strided_bhsd_views_and_lse(cuda_device):
     _, expected_lse = block_sparse_attention(
         q.float().numpy(), k.float().numpy(), v.float().numpy(), None, 128)
     np.testing.assert_allclose(lse.cpu().numpy(), expected_lse, atol=1e-3, rtol=1e-4)
+
+
+def _gpu_metrics(actual, expected):
+    """max-abs and cosine of two same-shape device tensors, in float32 on the GPU."""
+    a, e = actual.float().reshape(-1), expected.float().reshape(-1)
+    return {"max_absolute_error": float((a - e).abs().max()),
+            "cosine_similarity": float(torch.dot(a, e) / (a.norm() * e.norm()))}
+
+
+def test_config1_dense_rope_against_sdpa_and_fp32(cuda_device):
+    """the dense path at the Wan2.1-1.3B shape, B=2 (CFG
+    pair), 12 heads, grid 21x30x52 = 32,760 tokens, Q/K with 3D RoPE, handed
+    over as [B,T,H,D] views of BHSD storage.  Every row is compared with
+    PyTorch SDPA (flash or memory-efficient kernel, never the math path), and
+    sampled rows with a float32 matmul reference."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from dit_sparse_atten_amd.attention_backends.dense import DenseBackend
+    from tests.golden.inputs import rope_qkv
+
+    grid = (21, 30, 52)
+    q, k, v = rope_qkv(grid, batch=2, heads=12, seed=1)
+    qh, kh, vh = (x.transpose(1, 2).contiguous().to(cuda_device) for x in (q, k, v))
+    out = DenseBackend()(qh.transpose(1, 2), kh.transpose(1, 2), vh.transpose(1, 2))
+    torch.cuda.synchronize()
+    assert out.shape == (2, 32760, 12, 128) and out.dtype == torch.bfloat16
+
+    sdpa = None
+    for backend in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            with sdpa_kernel([backend]):
+                sdpa = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh)
+            break
+        except RuntimeError:
+            continue
+    if sdpa is not None:
+        torch.cuda.synchronize()
+        metrics = _gpu_metrics(out, sdpa.transpose(1, 2))
+        assert metrics["max_absolute_error"] <= MAX_ABS, metrics
+        assert metrics["cosine_similarity"] >= MIN_COSINE, metrics
+
+    generator = torch.Generator().manual_seed(2)
+    rows = torch.randint(0, 32760, (256,), generator=generator).to(cuda_device)
+    for b in range(2):
+        for h in (0, 5, 11):
+            qs = qh[b, h, rows].float().contiguous()
+            kt = kh[b, h].float().t().contiguous()
+            probs = torch.softmax(qs @ kt * 128 ** -0.5, dim=-1)
+            expected = probs @ vh[b, h].float().contiguous()
+            metrics = _gpu_metrics(out[b, rows, h], expected)
+            assert metrics["max_absolute_error"] <= MAX_ABS, (b, h, metrics)
+            assert metrics["cosine_similarity"] >= MIN_COSINE, (b, h, metrics)
