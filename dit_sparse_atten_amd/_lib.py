@@ -40,6 +40,7 @@ SIGNATURES = {
         _c_ptr, _c_size, _c_ptr,                   # workspace, workspace_bytes, stream
     )),
     "dsa_bsa_workspace_bytes": (_c_size, (_c_int, _c_int, _c_int, _c_int)),
+    "dsa_bsa_workspace_bytes_block": (_c_size, (_c_int, _c_int, _c_int, _c_int, _c_int)),
     "dsa_sampled_mass": (_c_int, (
         _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
         _c_int, _c_int, _c_int, _c_int, _c_int,    # tokens, heads, head_dim, block, samples
@@ -49,6 +50,13 @@ SIGNATURES = {
         _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
         _c_int, _c_int, _c_int, _c_int,            # tokens, heads, head_dim, block
         _c_ptr, _c_i64, _c_float, _c_ptr, _c_ptr,  # lse, lse_head_stride, scale, mass, stream
+    )),
+    "dsa_tile_stats": (_c_int, (
+        _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
+        _c_int, _c_int, _c_int, _c_int, _c_int,    # tokens, heads, head_dim, tile_h, tile_w
+        _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_float,  # lse, lse_head_stride, row_ptr, col_idx, scale
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # mass, mass_f16, centroids q_y q_x k_y k_x
+        _c_ptr,                                    # stream
     )),
     "dsa_route_select": (_c_int, (
         _c_ptr, _c_ptr, _c_int, _c_int,            # mass, previous, rows, keys
@@ -66,6 +74,16 @@ SIGNATURES = {
         _c_int, _c_int, _c_int,                    # explore_count, expand_flags, sink_blocks
         _c_ptr, _c_ptr, _c_ptr,                    # route, counts, candidates
         _c_ptr, _c_ptr, _c_ptr, _c_ptr,            # exploration, dropped, added, stream
+    )),
+    "dsa_drop_low_mass": (_c_int, (
+        _c_ptr, _c_ptr, _c_int, _c_int, _c_int,    # mask, mass, mass_is_f16, heads, tiles
+        _c_float, _c_int, _c_ptr, _c_ptr, _c_ptr,  # drop_factor, sink, scratch, out, counts
+        _c_ptr,                                    # stream
+    )),
+    "dsa_expand_route": (_c_int, (
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # mask, mass, centroids q_y q_x k_y k_x
+        _c_int, _c_int, _c_int, _c_int, _c_int,    # heads, frames, blocks_h, blocks_w, policy
+        _c_float, _c_float, _c_ptr, _c_ptr, _c_ptr,  # threshold, huge, scratch, out, stream
     )),
     "dsa_route_to_csr": (_c_int, (
         _c_ptr, _c_int, _c_int,                    # route, rows, keys

@@ -45,6 +45,7 @@ struct BsaParams {
   const int32_t* row_ptr;  // null: every key block (dense)
   const int32_t* col_idx;
   int32_t batch, heads, q_tokens, kv_tokens, q_blocks, kv_blocks, route_batches;
+  int32_t block;     // tokens per query block and per key block (1..128)
   float scale;       // softmax scale applied to <q, k>
   float scale_log2;  // scale * log2(e)
 };
@@ -69,29 +70,37 @@ constexpr int kVtHalfRow = kHalfKeys * 2;  // 128 B: one head dim of a 64-key ha
 __device__ __forceinline__ int vt9_swz(int d, int c) { return c ^ ((d >> 1) & 7); }
 
 // One workgroup per (b, h, 64-key chunk): rows of V through LDS, columns out.
+// Chunk c holds half-tile (c % nh) of key block (c / nh): keys
+// block * (c / nh) + 64 * (c % nh) + r for r < 64, zero past the block's end
+// or the sequence end (nh = 1 for blocks of at most 64 keys, else 2; with
+// 128-key blocks the chunks are simply consecutive 64-key ranges).
 __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restrict__ v,
                                                            __bf16* __restrict__ vt,
                                                            int64_t v_sb, int64_t v_st,
                                                            int64_t v_sh, int32_t heads,
-                                                           int32_t tokens, int32_t tpad) {
+                                                           int32_t tokens, int32_t block,
+                                                           int32_t nh, int32_t vt_keys) {
   __shared__ __bf16 tile[64][kHeadDim + 8];  // +8 keeps column reads conflict-light
-  const int chunk = blockIdx.x;              // 64-key chunk
+  const int chunk = blockIdx.x;
   const int bh = blockIdx.y;
   const int b = bh / heads, h = bh % heads;
-  const int key0 = chunk * 64;
+  const int half = chunk % nh;
+  const int key0 = (chunk / nh) * block + half * 64;
+  int rows = min(64, block - half * 64);
+  rows = min(rows, tokens - key0);
   const int tid = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = j * 256 + tid;  // 64 rows x 16 chunks
     const int r = idx >> 4, c = idx & 15;
     dsa_u32x4 val = {0u, 0u, 0u, 0u};
-    if (key0 + r < tokens)
+    if (r < rows)
       val = *reinterpret_cast<const dsa_u32x4*>(v + b * v_sb + h * v_sh +
                                                 (int64_t)(key0 + r) * v_st + c * 8);
     *reinterpret_cast<dsa_u32x4*>(&tile[r][c * 8]) = val;
   }
   dsa::lds_barrier();
-  __bf16* out = vt + ((int64_t)bh * kHeadDim) * tpad + (int64_t)key0 * kHeadDim;
+  __bf16* out = vt + ((int64_t)bh * kHeadDim) * vt_keys + (int64_t)chunk * 64 * kHeadDim;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = j * 256 + tid;  // 128 dims x 8 chunks of 8 slots
@@ -111,9 +120,10 @@ __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restr
 }
 
 // kRouted: key blocks from the CSR row (false: every key block, dense).
-template <bool kRouted>
+// kNh: 64-key half-tiles per key block (2 for blocks of 65..128 keys, else 1).
+template <bool kRouted, int kNh>
 __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf16* vt,
-                                                          int32_t tpad) {
+                                                          int32_t vt_keys) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
@@ -140,9 +150,15 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     end = rp[row + 1];
   }
   const dsa_const_i32 cidx = (dsa_const_i32)p.col_idx;
-  const int nsub = 2 * (end - start);
+  const int nblk = end - start;
 
-  const int tq = qb * 128 + wave * 32 + qi;
+  // Rows past the block (blocks shorter than 128) or the sequence are
+  // computed on a clamped row and never stored; waves wholly past the block
+  // only stage their share of K/V.
+  const int local_row = wave * 32 + qi;
+  const int tq = qb * p.block + local_row;
+  const bool row_ok = local_row < p.block && tq < p.q_tokens;
+  const bool wave_active = wave * 32 < p.block;
   const int tq_c = tq < p.q_tokens ? tq : p.q_tokens - 1;
   const __bf16* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)tq_c * p.q_st;
   dsa_bf16x8 qf[8];
@@ -151,7 +167,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
 
   const __bf16* kbase = p.k + b * p.k_sb + h * p.k_sh;
-  const __bf16* vtbase = vt + ((int64_t)(b * p.heads + h) * kHeadDim) * tpad;
+  const __bf16* vtbase = vt + ((int64_t)(b * p.heads + h) * kHeadDim) * vt_keys;
   // Per-lane source offsets (elements) relative to the half-tile's first key.
   int koff[4], voff[4];
 #pragma unroll
@@ -163,20 +179,32 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     voff[j] = d * kHalfKeys + vt9_swz(d, idx & 7) * 8;
   }
 
-  auto block_of = [&](int sub) -> int {
-    const int it = start + (sub >> 1);
+  auto block_of = [&](int j) -> int {
+    const int it = start + j;
     const int kb = kRouted ? cidx[it] : it;
     return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
   };
 
-  const __amdgpu_buffer_rsrc_t vt_rsrc = make_rsrc(vtbase, (uint32_t)(kHeadDim * tpad * 2));
-  auto issue = [&](int key0, unsigned char* kdst, unsigned char* vdst) {
+  const __amdgpu_buffer_rsrc_t vt_rsrc = make_rsrc(vtbase, (uint32_t)(kHeadDim * vt_keys * 2));
+  // Stages half-tile `half` of key block kb (an invalid block stages block 0,
+  // which is then fully masked).
+  auto issue = [&](int kb, int half, unsigned char* kdst, unsigned char* vdst) {
+    const int kbc = kb < 0 ? 0 : kb;
+    const int key0 = kbc * p.block + half * kHalfKeys;
     const __amdgpu_buffer_rsrc_t k_rsrc = k_tile_rsrc(kbase, p.k_st, key0, p.kv_tokens);
 #pragma unroll
     for (int j = 0; j < 4; ++j) lds_load16(k_rsrc, kdst + (wave * 4 + j) * 1024, koff[j] * 2, 0);
+    const uint32_t vsoff = (uint32_t)(kbc * kNh + half) * (uint32_t)kKStage;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, voff[j] * 2, key0 * kRowBytes);
+      lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, voff[j] * 2, vsoff);
+  };
+  // Valid keys of half-tile `half` of block kb (0 for an invalid block).
+  auto valid_of = [&](int kb, int half) -> int {
+    if (kb < 0) return 0;
+    const int key0 = kb * p.block + half * kHalfKeys;
+    int valid = min(kHalfKeys, p.block - half * kHalfKeys);
+    return min(valid, p.kv_tokens - key0);
   };
 
   float m_run = -INFINITY;
@@ -260,32 +288,41 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     }
   };
 
-  auto step = [&](int sub, int kb, int kb_next, const unsigned char* kc, const unsigned char* vc,
-                  unsigned char* kn, unsigned char* vn) {
+  // One pipelined step: wait for the current stage, prefetch the next
+  // half-tile (next_kb == -2: none), then compute on the current one.
+  auto step = [&](int kb, int half, int next_kb, int next_half, const unsigned char* kc,
+                  const unsigned char* vc, unsigned char* kn, unsigned char* vn) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    if (sub + 1 < nsub)
-      issue((kb_next < 0 ? 0 : kb_next) * 128 + ((sub + 1) & 1) * kHalfKeys, kn, vn);
-    const int key0 = (kb < 0 ? 0 : kb) * 128 + (sub & 1) * kHalfKeys;
-    int valid = kb < 0 ? 0 : p.kv_tokens - key0;
-    valid = valid < kHalfKeys ? valid : kHalfKeys;
-    compute(kc, vc, valid);
+    if (next_kb != -2) issue(next_kb, next_half, kn, vn);
+    if (wave_active) compute(kc, vc, valid_of(kb, half));
   };
 
-  if (nsub > 0) {
+  if (nblk > 0) {
     int kb = block_of(0);
-    issue((kb < 0 ? 0 : kb) * 128, lds_k0, lds_v0);
-    for (int sub = 0; sub < nsub; sub += 2) {
-      const int kb_after = (sub + 2 < nsub) ? block_of(sub + 2) : -1;
-      step(sub, kb, kb, lds_k0, lds_v0, lds_k1, lds_v1);
-      step(sub + 1, kb, kb_after, lds_k1, lds_v1, lds_k0, lds_v0);
-      kb = kb_after;
+    issue(kb, 0, lds_k0, lds_v0);
+    if (kNh == 2) {
+      for (int j = 0; j < nblk; ++j) {
+        const int kb_after = j + 1 < nblk ? block_of(j + 1) : -2;
+        step(kb, 0, kb, 1, lds_k0, lds_v0, lds_k1, lds_v1);
+        step(kb, 1, kb_after, 0, lds_k1, lds_v1, lds_k0, lds_v0);
+        kb = kb_after;
+      }
+    } else {
+      for (int j = 0; j < nblk; j += 2) {
+        const int kb1 = j + 1 < nblk ? block_of(j + 1) : -2;
+        step(kb, 0, kb1, 0, lds_k0, lds_v0, lds_k1, lds_v1);
+        if (kb1 == -2) break;
+        const int kb2 = j + 2 < nblk ? block_of(j + 2) : -2;
+        step(kb1, 0, kb2, 0, lds_k1, lds_v1, lds_k0, lds_v0);
+        kb = kb2;
+      }
     }
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (tq < p.q_tokens) {
+  if (row_ok) {
     __bf16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -307,14 +344,27 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-int32_t padded_tokens(int32_t kv_tokens) { return (kv_tokens + 127) / 128 * 128; }
+// Half-tiles per key block, and keys of the per-(b, h) V^T workspace.
+int32_t halves_per_block(int32_t block) { return block > kHalfKeys ? 2 : 1; }
+
+int64_t vt_keys_for(int32_t kv_tokens, int32_t block) {
+  const int64_t blocks = (kv_tokens + block - 1) / block;
+  return blocks * halves_per_block(block) * kHalfKeys;
+}
 
 }  // namespace
 
+extern "C" size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads,
+                                                int32_t kv_tokens, int32_t head_dim,
+                                                int32_t block_size) {
+  if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
+  if (block_size <= 0 || block_size > 128) return 0;
+  return (size_t)batch * heads * head_dim * vt_keys_for(kv_tokens, block_size) * sizeof(__bf16);
+}
+
 extern "C" size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
                                           int32_t head_dim) {
-  if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
-  return (size_t)batch * heads * head_dim * padded_tokens(kv_tokens) * sizeof(__bf16);
+  return dsa_bsa_workspace_bytes_block(batch, heads, kv_tokens, head_dim, 128);
 }
 
 extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
@@ -332,9 +382,9 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   if (head_dim != kHeadDim)
     return dsa::set_error(DSA_EUNSUPPORTED, "dsa_bsa_fwd: head_dim %d unsupported (128 only)",
                           head_dim);
-  if (block_size != 128)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_bsa_fwd: block_size %d unsupported (128)",
-                          block_size);
+  if (block_size <= 0 || block_size > 128)
+    return dsa::set_error(DSA_EUNSUPPORTED,
+                          "dsa_bsa_fwd: block_size %d unsupported (1..128)", block_size);
   if ((row_ptr == nullptr) != (col_idx == nullptr))
     return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: row_ptr and col_idx must both be set or null");
   if (row_ptr && route_batches != 1 && route_batches != batch)
@@ -354,19 +404,22 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
     return dsa::set_error(DSA_EUNSUPPORTED,
                           "dsa_bsa_fwd: key token stride %lld too large (64 rows must span < 2 GiB)",
                           (long long)strides[4]);
-  const size_t need = dsa_bsa_workspace_bytes(batch, heads, kv_tokens, head_dim);
+  const size_t need = dsa_bsa_workspace_bytes_block(batch, heads, kv_tokens, head_dim,
+                                                    block_size);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return dsa::set_error(DSA_EINVAL,
                           "dsa_bsa_fwd: workspace of %zu bytes (16-byte aligned) required, got %zu",
                           need, workspace_bytes);
   const int32_t q_blocks = (q_tokens + block_size - 1) / block_size;
   const int32_t kv_blocks = (kv_tokens + block_size - 1) / block_size;
-  const int32_t tpad = padded_tokens(kv_tokens);
+  const int32_t nh = halves_per_block(block_size);
+  const int64_t vt_keys64 = vt_keys_for(kv_tokens, block_size);
   const int64_t grid = (int64_t)batch * heads * q_blocks;
   if (grid > 0x7fffffff || (int64_t)batch * heads > 65535)
     return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: grid too large");
-  if ((int64_t)(kHeadDim - 1) * tpad + tpad > 0x7fffffff)
+  if ((int64_t)kHeadDim * vt_keys64 * 2 > 0x7fffffff)
     return dsa::set_error(DSA_EUNSUPPORTED, "dsa_bsa_fwd: kv_tokens too large");
+  const int32_t vt_keys = (int32_t)vt_keys64;
 
   BsaParams p;
   p.q = static_cast<const __bf16*>(q);
@@ -383,16 +436,22 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   p.batch = batch; p.heads = heads; p.q_tokens = q_tokens; p.kv_tokens = kv_tokens;
   p.q_blocks = q_blocks; p.kv_blocks = kv_blocks;
   p.route_batches = row_ptr ? route_batches : 1;
+  p.block = block_size;
   p.scale = scale;
   p.scale_log2 = scale * 1.4426950408889634f;
   __bf16* vt = static_cast<__bf16*>(workspace);
-  hipLaunchKernelGGL(vt_transpose_kernel, dim3((unsigned)(tpad / 64), (unsigned)(batch * heads)),
-                     dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads, kv_tokens, tpad);
-  if (row_ptr)
-    hipLaunchKernelGGL(bsa_fwd_kernel<true>, dim3((unsigned)grid), dim3(256), 0, stream, p,
-                       (const __bf16*)vt, tpad);
+  hipLaunchKernelGGL(vt_transpose_kernel, dim3((unsigned)(vt_keys / 64), (unsigned)(batch * heads)),
+                     dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads, kv_tokens,
+                     block_size, nh, vt_keys);
+  const dim3 blocks((unsigned)grid), threads(256);
+  const __bf16* vtc = vt;
+  if (row_ptr && nh == 2)
+    hipLaunchKernelGGL((bsa_fwd_kernel<true, 2>), blocks, threads, 0, stream, p, vtc, vt_keys);
+  else if (row_ptr)
+    hipLaunchKernelGGL((bsa_fwd_kernel<true, 1>), blocks, threads, 0, stream, p, vtc, vt_keys);
+  else if (nh == 2)
+    hipLaunchKernelGGL((bsa_fwd_kernel<false, 2>), blocks, threads, 0, stream, p, vtc, vt_keys);
   else
-    hipLaunchKernelGGL(bsa_fwd_kernel<false>, dim3((unsigned)grid), dim3(256), 0, stream, p,
-                       (const __bf16*)vt, tpad);
+    hipLaunchKernelGGL((bsa_fwd_kernel<false, 1>), blocks, threads, 0, stream, p, vtc, vt_keys);
   return dsa::check_launch("dsa_bsa_fwd");
 }

@@ -21,8 +21,10 @@ SOURCES = (
     "dsa_api.hip",
     "bsa_fwd.hip",
     "block_mass.hip",
+    "tile_stats.hip",
     "route.hip",
     "routing.hip",
+    "tile_route.hip",
     "permute.hip",
 )
 

@@ -185,7 +185,8 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Top-mass selection: one wave per (head, query-block) row, K <= 512.
+// Top-mass selection: one wave per (head, query-block) row, K <= 64 * kPer
+// (512 or 1024).
 // ---------------------------------------------------------------------------
 
 struct SelectParams {
@@ -197,8 +198,10 @@ struct SelectParams {
   float rho, target;
 };
 
+template <int kPer>
 __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
-  __shared__ uint8_t flags[4][512];
+  constexpr int kN = 64 * kPer;
+  __shared__ uint8_t flags[4][kN];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + wave;
@@ -206,48 +209,48 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
   const int K = p.keys;
   const float* mrow = p.mass + (int64_t)row * K;
 
-  // Element e = lane * 8 + j.
-  float v[8];
+  // Element e = lane * kPer + j.
+  float v[kPer];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = lane * 8 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
     float x = e < K ? mrow[e] : 0.f;
     v[j] = x > 0.f ? x : 0.f;  // rows are probabilities: clamp -0.0 and noise
   }
   if (p.previous) {
     int64_t s = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s += to_fixed(v[j]);
+    for (int j = 0; j < kPer; ++j) s += to_fixed(v[j]);
     s = wave_sum_i64(s);
     const float mean = fixed_to_f32(s) / (float)K;
     const float prior = p.rho * mean;
     const uint8_t* prow = p.previous + (int64_t)row * K;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane * 8 + j;
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane * kPer + j;
       if (e < K && prow[e]) v[j] = v[j] + prior;
     }
   }
   int64_t total = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) total += to_fixed(v[j]);
+  for (int j = 0; j < kPer; ++j) total += to_fixed(v[j]);
   total = wave_sum_i64(total);
   const float threshold = fixed_to_f32(total) * p.target;
 
-  // Descending sort of key = value bits << 32 | (511 - index).
-  uint64_t key[8];
+  // Descending sort of key = value bits << 32 | (kN - 1 - index).
+  uint64_t key[kPer];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = lane * 8 + j;
-    key[j] = e < K ? ((uint64_t)__float_as_uint(v[j]) << 32) | (uint32_t)(511 - e) : 0ull;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
+    key[j] = e < K ? ((uint64_t)__float_as_uint(v[j]) << 32) | (uint32_t)(kN - 1 - e) : 0ull;
   }
-  dsa::sort512_desc(key, lane);
+  dsa::sort_desc<kPer>(key, lane);
 
   // Exact prefix sums in sorted order.
-  int64_t pre[8];
+  int64_t pre[kPer];
   int64_t run = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < kPer; ++j) {
     run += to_fixed(__uint_as_float((uint32_t)(key[j] >> 32)));
     pre[j] = run;
   }
@@ -260,8 +263,8 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
   const int64_t offset = scan - run;
   int below = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = lane * 8 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
     if (e < K && fixed_to_f32(pre[j] + offset) < threshold) ++below;
   }
   int count = wave_sum_i32(below) + 1;
@@ -269,21 +272,21 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
 
   uint8_t* f = flags[wave];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) f[lane * 8 + j] = 0;
+  for (int j = 0; j < kPer; ++j) f[lane * kPer + j] = 0;
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int pos = lane * 8 + j;
-    if (pos < count) f[511 - (int)(key[j] & 0xffffffffu)] = 1;
+  for (int j = 0; j < kPer; ++j) {
+    const int pos = lane * kPer + j;
+    if (pos < count) f[kN - 1 - (int)(key[j] & 0xffffffffu)] = 1;
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   int selected = 0;
   uint8_t* rout = p.route + (int64_t)row * K;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = lane * 8 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
     if (e < K) {
       const uint8_t on = (f[e] || e < p.sink) ? 1 : 0;
       rout[e] = on;
@@ -447,8 +450,8 @@ extern "C" int dsa_route_select(const float* mass, const uint8_t* previous, int3
   dsa::clear_error();
   if (!mass || !route || !counts) return dsa::set_error(DSA_EINVAL, "dsa_route_select: null pointer");
   if (rows <= 0 || keys <= 0) return dsa::set_error(DSA_EINVAL, "dsa_route_select: empty route");
-  if (keys > 512)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_route_select: at most 512 key blocks (got %d)",
+  if (keys > 1024)
+    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_route_select: at most 1024 key blocks (got %d)",
                           keys);
   if (!(target > 0.f && target <= 1.f))
     return dsa::set_error(DSA_EINVAL, "mass_target must be in (0, 1]");
@@ -465,8 +468,11 @@ extern "C" int dsa_route_select(const float* mass, const uint8_t* previous, int3
   p.sink = sink_blocks < 0 ? 0 : sink_blocks;
   p.rho = rho;
   p.target = target;
-  hipLaunchKernelGGL(route_select_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream,
-                     p);
+  const dim3 groups((unsigned)((rows + 3) / 4)), threads(256);
+  if (keys <= 512)
+    hipLaunchKernelGGL(route_select_kernel<8>, groups, threads, 0, stream, p);
+  else
+    hipLaunchKernelGGL(route_select_kernel<16>, groups, threads, 0, stream, p);
   return dsa::check_launch("dsa_route_select");
 }
 

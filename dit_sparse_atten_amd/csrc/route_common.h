@@ -1,5 +1,5 @@
 // Row arithmetic shared by the route kernels (gfx950): exact fixed-point row
-// sums and a one-wave 512-key bitonic sort.
+// sums and a one-wave bitonic sort of up to 1024 keys.
 //
 // A row value m >= 0 is represented as the integer floor(m * 2^52), so row and
 // prefix sums are exact and independent of summation order; a sum is rounded
@@ -34,19 +34,22 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
   return v;
 }
 
-// Sorts the 512 keys of one wave (element e = lane * 8 + j in key[j]) into
-// descending order, in place: a bitonic network, with partners eight or more
-// elements apart exchanged across lanes and closer ones inside a lane.
-__device__ __forceinline__ void sort512_desc(uint64_t key[8], int lane) {
+// Sorts the 64 * kPer keys of one wave (element e = lane * kPer + j in
+// key[j]) into descending order, in place: a bitonic network, with partners
+// kPer or more elements apart exchanged across lanes and closer ones inside a
+// lane.
+template <int kPer>
+__device__ __forceinline__ void sort_desc(uint64_t key[kPer], int lane) {
+  constexpr int kN = 64 * kPer;
 #pragma unroll
-  for (int size = 2; size <= 512; size <<= 1) {
+  for (int size = 2; size <= kN; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride >= 8) {
-        const int lane_mask = stride >> 3;
+      if (stride >= kPer) {
+        const int lane_mask = stride / kPer;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int e = lane * 8 + j;
+        for (int j = 0; j < kPer; ++j) {
+          const int e = lane * kPer + j;
           const uint64_t other = __shfl_xor((unsigned long long)key[j], lane_mask);
           const bool desc = (e & size) == 0;
           const bool lower = (e & stride) == 0;
@@ -56,10 +59,10 @@ __device__ __forceinline__ void sort512_desc(uint64_t key[8], int lane) {
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < kPer; ++j) {
           if (j & stride) continue;
           const int jp = j | stride;
-          const int e = lane * 8 + j;
+          const int e = lane * kPer + j;
           const bool desc = (e & size) == 0;
           const uint64_t a = key[j], b = key[jp];
           const uint64_t hi = a > b ? a : b;
@@ -71,5 +74,7 @@ __device__ __forceinline__ void sort512_desc(uint64_t key[8], int lane) {
     }
   }
 }
+
+__device__ __forceinline__ void sort512_desc(uint64_t key[8], int lane) { sort_desc<8>(key, lane); }
 
 }  // namespace dsa

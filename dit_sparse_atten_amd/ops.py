@@ -99,6 +99,10 @@ def csr_from_route(route, block_size=128):
 def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_size=128):
     """Block-sparse (or, with ``csr=None``, dense) attention forward on the GPU.
 
+    ``block_size`` (1..128) is the number of consecutive tokens per query
+    block and per key block that the route addresses: 128 for ``flex_reuse``,
+    the spatial tile size for the matrix-sparse backend.
+
     q: [B,Tq,H,128], k/v: [B,Tk,H,128] bf16 on a HIP device, any strides with a
     contiguous head dim.  Returns O [B,Tq,H,128] bf16 (contiguous unless
     ``out`` is given) and, with ``return_lse``, the natural-log LSE [B,H,Tq] fp32.
@@ -147,7 +151,10 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     strides = _lib.int64_array(
         list(q.stride()[:3]) + list(k.stride()[:3]) + list(v.stride()[:3])
         + list(out.stride()[:3]))
-    workspace_bytes = lib.dsa_bsa_workspace_bytes(batch, heads, kv_tokens, head_dim)
+    if not 1 <= block_size <= 128:
+        raise ValueError(f"block_size {block_size} unsupported (1..128)")
+    workspace_bytes = lib.dsa_bsa_workspace_bytes_block(batch, heads, kv_tokens, head_dim,
+                                                        block_size)
     # Transposed-V scratch for this call; the caching allocator recycles it.
     workspace = torch.empty(max(workspace_bytes, 16), dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
@@ -237,6 +244,65 @@ def block_mass(q, k, lse, block_size=128, scale=None):
             _stream_handle(q.device))
     _lib.check(status, "dsa_block_mass")
     return mass
+
+
+def tile_stats(q, k, lse, tile_shape, csr=None, scale=None, centroids=True):
+    """Spatial-tile attention statistics of tile-major q/k [1, T, H, 128].
+
+    Same quantities as the reference's matrix-sparse statistics
+    (attention_backends/sparse.py:184-233 with ``csr=None``, 718-750 with the
+    CSR of the attended tiles): ``lse`` is the natural-log normaliser of that
+    attention ([1, H, T] or [H, T]).  Returns a dict of [H, tiles, tiles]
+    tensors: ``mass`` (fp32, mass / tokens), ``mass_f16`` and, with
+    ``centroids``, ``centroid_q_y``, ``centroid_q_x``, ``centroid_k_y``,
+    ``centroid_k_x`` (fp16).
+    """
+    lib = _lib.load()
+    if q.shape[0] != 1 or q.shape[1] != k.shape[1]:
+        raise ValueError("tile statistics support batch-1 self-attention")
+    q = _kernel_view("q", q)
+    k = _kernel_view("k", k)
+    _, tokens, heads, head_dim = q.shape
+    tile_h, tile_w = (int(x) for x in tile_shape)
+    tile = tile_h * tile_w
+    if tile <= 0 or tokens % tile:
+        raise ValueError("the tile shape must divide the token count")
+    tiles = tokens // tile
+    _require_cuda("lse", lse)
+    if lse.dtype != torch.float32:
+        raise ValueError("lse must be float32")
+    if lse.ndim == 3:
+        lse = lse[0]
+    if tuple(lse.shape) != (heads, tokens):
+        raise ValueError("lse must have shape [1, heads, tokens] or [heads, tokens]")
+    if lse.stride(1) != 1:
+        lse = lse.contiguous()
+    if scale is None:
+        scale = head_dim ** -0.5
+    row_ptr = col_idx = None
+    if csr is not None:
+        if (csr.route_batches, csr.heads, csr.q_blocks, csr.k_blocks) != (1, heads, tiles, tiles):
+            raise ValueError("route shape does not match the tile layout")
+        row_ptr, col_idx = csr.row_ptr, csr.col_idx
+    shape = (heads, tiles, tiles)
+    out = {"mass": torch.empty(shape, dtype=torch.float32, device=q.device),
+           "mass_f16": torch.empty(shape, dtype=torch.float16, device=q.device)}
+    names = ("centroid_q_y", "centroid_q_x", "centroid_k_y", "centroid_k_x")
+    if centroids:
+        for name in names:
+            out[name] = torch.empty(shape, dtype=torch.float16, device=q.device)
+    strides = _lib.int64_array([q.stride(1), q.stride(2), k.stride(1), k.stride(2)])
+    with torch.cuda.device(q.device):
+        status = lib.dsa_tile_stats(
+            q.data_ptr(), k.data_ptr(), strides, tokens, heads, head_dim, tile_h, tile_w,
+            lse.data_ptr(), lse.stride(0),
+            row_ptr.data_ptr() if row_ptr is not None else None,
+            col_idx.data_ptr() if col_idx is not None else None, float(scale),
+            out["mass"].data_ptr(), out["mass_f16"].data_ptr(),
+            *[out[name].data_ptr() if name in out else None for name in names],
+            _stream_handle(q.device))
+    _lib.check(status, "dsa_tile_stats")
+    return out
 
 
 def route_select(mass, target, keep, previous=None, persistence=0.0, sink_blocks=0):
@@ -356,6 +422,69 @@ def directional_update(mass, previous, neighbors, *, keep, persistence=0.5, min_
     _lib.check(status, "dsa_directional_update")
     outputs["counts"] = counts
     return outputs
+
+
+def drop_low_mass(mask, mass, drop_factor, sink_tiles=0):
+    """Next route of the matrix-sparse backend (attention_backends/sparse.py:
+    327-348, then the first ``sink_tiles`` columns): returns (route bool, counts
+    int32).  ``mass`` is fp16 (the stored route mass) or fp32."""
+    lib = _lib.load()
+    mask = _require_bool_route(mask)
+    _require_cuda("mass", mass)
+    if mask.ndim != 3 or mask.shape[1] != mask.shape[2] or mass.shape != mask.shape:
+        raise ValueError("mask and mass must have shape [heads, tiles, tiles]")
+    if mass.dtype not in (torch.float16, torch.float32):
+        raise ValueError("mass must be float16 or float32")
+    heads, tiles, _ = mask.shape
+    mass = mass.contiguous()
+    out = torch.empty_like(mask)
+    counts = torch.empty((heads, tiles), dtype=torch.int32, device=mask.device)
+    scratch = torch.empty(2 * heads, dtype=torch.float32, device=mask.device)
+    with torch.cuda.device(mask.device):
+        status = lib.dsa_drop_low_mass(
+            mask.data_ptr(), mass.data_ptr(), int(mass.dtype == torch.float16), heads, tiles,
+            float(drop_factor), int(sink_tiles), scratch.data_ptr(), out.data_ptr(),
+            counts.data_ptr(), _stream_handle(mask.device))
+    _lib.check(status, "dsa_drop_low_mass")
+    return out, counts
+
+
+EXPAND_POLICIES = {"all": 1, "directional": 2}
+
+
+def expand_route(mask, grid_tiles, policy, mass=None, centroids=None, centroid_threshold=0.15,
+                 huge_factor=2.0):
+    """Predicted next mask (attention_backends/sparse.py:350-373) for policy
+    "all" or "directional".  ``grid_tiles`` = (frames, blocks_h, blocks_w);
+    ``mass`` and ``centroids`` (q_y, q_x, k_y, k_x) are fp16 [H, tiles, tiles]."""
+    lib = _lib.load()
+    if policy not in EXPAND_POLICIES:
+        raise ValueError(f"unknown expansion policy {policy!r}")
+    mask = _require_bool_route(mask)
+    heads, tiles, _ = mask.shape
+    frames, blocks_h, blocks_w = (int(x) for x in grid_tiles)
+    if frames * blocks_h * blocks_w != tiles:
+        raise ValueError("the tile grid does not match the route")
+    pointers = [None] * 5
+    scratch = None
+    if policy == "directional":
+        tensors = [mass, *centroids]
+        for tensor in tensors:
+            _require_cuda("mass/centroid", tensor)
+            if tensor.dtype != torch.float16 or tensor.shape != mask.shape:
+                raise ValueError("directional expansion needs fp16 mass and centroids")
+        tensors = [tensor.contiguous() for tensor in tensors]
+        pointers = [tensor.data_ptr() for tensor in tensors]
+        scratch = torch.empty(2 * heads, dtype=torch.float32, device=mask.device)
+    out = torch.empty_like(mask)
+    with torch.cuda.device(mask.device):
+        status = lib.dsa_expand_route(
+            mask.data_ptr(), *pointers, heads, frames, blocks_h, blocks_w,
+            EXPAND_POLICIES[policy], float(centroid_threshold), float(huge_factor),
+            scratch.data_ptr() if scratch is not None else None, out.data_ptr(),
+            _stream_handle(mask.device))
+    _lib.check(status, "dsa_expand_route")
+    return out
 
 
 def route_to_csr(route, counts=None, block_size=128):

@@ -39,7 +39,9 @@ const char* dsa_last_error(void);
  * SDPA (attention_backends/dense.py:14-48).
  *   strides[12]: q (b,t,h), k (b,t,h), v (b,t,h), o (b,t,h), in elements,
  *                each a multiple of 8; pointers 16-byte aligned.
- *   head_dim: 128.  block_size: 128.
+ *   head_dim: 128.  block_size: 1..128 tokens per query block and per key
+ *                block (128 for the flex_reuse route; the spatial tile size of
+ *                the matrix-sparse backend, sparse.py:51-103, 670-751).
  *   row_ptr/col_idx: CSR over rows ((rb * heads + h) * q_blocks + qb), rb <
  *                route_batches (1 = shared by all batch items, else = batch);
  *                col_idx lists key blocks (ascending order not required).
@@ -47,7 +49,7 @@ const char* dsa_last_error(void);
  *                skipped; a row with no key blocks yields zeros.
  *   scale: softmax scale (d^-1/2 for softmax_scale=None).
  *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
- *   workspace: device scratch of dsa_bsa_workspace_bytes() bytes, 16-byte
+ *   workspace: device scratch of dsa_bsa_workspace_bytes_block() bytes, 16-byte
  *                aligned, that receives the transposed V for this call; its
  *                contents need no initialisation and are dead after the call.
  * Keys past kv_tokens in a partial last block are masked.
@@ -58,11 +60,16 @@ int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, const int6
                 const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* Workspace bytes dsa_bsa_fwd needs (batch * heads * head_dim * kv_tokens
- * rounded up to 128, in bf16); 0 for invalid sizes.  No counterpart in the
- * reference, whose FlexAttention allocates internally. */
+/* Workspace bytes dsa_bsa_fwd needs with 128-token blocks (batch * heads *
+ * head_dim * kv_tokens rounded up to 128, in bf16); 0 for invalid sizes.  No
+ * counterpart in the reference, whose FlexAttention allocates internally. */
 size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
                                int32_t head_dim);
+
+/* The same for any block_size in 1..128: batch * heads * head_dim * 64 *
+ * (key blocks * (block_size > 64 ? 2 : 1)) bf16 values; 0 for invalid sizes. */
+size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_tokens,
+                                     int32_t head_dim, int32_t block_size);
 
 /*
  * Sampled block-mass estimate for one batch-1 self-attention call.
@@ -93,12 +100,33 @@ int dsa_block_mass(const void* q, const void* k, const int64_t* strides, int32_t
                    int64_t lse_head_stride, float scale, float* mass, hipStream_t stream);
 
 /*
+ * Spatial-tile attention statistics of one batch-1 self-attention call over
+ * tile-major tokens (tile_h * tile_w <= 128 tokens per tile, tokens a whole
+ * number of tiles, at most 1024 tiles).  Replaces the statistics of the
+ * matrix-sparse backend: `_dense_route` (attention_backends/sparse.py:184-233)
+ * with row_ptr == col_idx == NULL, `sparse_chunk` (sparse.py:718-750) with the
+ * CSR of the tiles each (head, query tile) row attended, and the
+ * normalisations of sparse.py:859-864, 908-922.  lse: [heads, tokens]
+ * natural-log normaliser of that same attention (dsa_bsa_fwd with
+ * block_size = tile_h * tile_w).  Outputs [heads, tiles, tiles]: mass (fp32,
+ * mass / tokens, required), mass_f16 (the same in fp16) and the four
+ * centroids moment / max(mass, 1e-12) in fp16 (each optional).  Cells a CSR
+ * row does not list are written as zeros; a row must not repeat a tile.
+ */
+int dsa_tile_stats(const void* q, const void* k, const int64_t* strides, int32_t tokens,
+                   int32_t heads, int32_t head_dim, int32_t tile_h, int32_t tile_w,
+                   const float* lse, int64_t lse_head_stride, const int32_t* row_ptr,
+                   const int32_t* col_idx, float scale, float* mass, void* mass_f16,
+                   void* centroid_q_y, void* centroid_q_x, void* centroid_k_y,
+                   void* centroid_k_x, hipStream_t stream);
+
+/*
  * Persistence prior + top-mass selection + first-frame sink, per row.
  * Replaces the prior of `_sampled_route` (flex.py:535-541), `_top_mass_route`
  * (flex.py:83-94, == sparse.py:171-181 `_row_mask`) and `_add_first_frame_sink`
  * (flex.py:550-566).  mass: [rows, keys] fp32, non-negative; previous: [rows,
  * keys] bytes or NULL (no prior); cap = max(1, ceil(keys * keep)); the first
- * sink_blocks columns are set after the cap.  keys <= 512.  Outputs route
+ * sink_blocks columns are set after the cap.  keys <= 1024.  Outputs route
  * [rows, keys] bytes and counts [rows] (selected blocks per row, sink included).
  */
 int dsa_route_select(const float* mass, const uint8_t* previous, int32_t rows, int32_t keys,
@@ -141,6 +169,38 @@ int dsa_directional_update(const float* mass, const uint8_t* previous,
                            uint8_t* route, int32_t* counts, uint8_t* candidates,
                            uint8_t* exploration, uint8_t* dropped, uint8_t* added,
                            hipStream_t stream);
+
+/*
+ * Next-step route of the matrix-sparse backend: drop low-mass tiles, keep one
+ * tile in any row the drop emptied, then set the first sink_tiles columns.
+ * Replaces `_drop_low_mass` + `_preserve_one_per_row`
+ * (attention_backends/sparse.py:327-348) and the sink of sparse.py:883-884.
+ *   mask, out: [heads, tiles, tiles] bytes; mass: the same shape, fp16
+ *   (mass_is_f16 = 1, the reference's stored route mass) or fp32 (0);
+ *   drop_factor > 0; head_scratch: device float[2 * heads];
+ *   counts: [heads, tiles] entries set per output row.
+ */
+int dsa_drop_low_mass(const uint8_t* mask, const void* mass, int32_t mass_is_f16, int32_t heads,
+                      int32_t tiles, float drop_factor, int32_t sink_tiles, float* head_scratch,
+                      uint8_t* out, int32_t* counts, hipStream_t stream);
+
+/*
+ * Predicted next-step mask of the matrix-sparse backend.  Replaces `_expand`
+ * (attention_backends/sparse.py:350-373) for policy 1 ("all": eight coupled
+ * query/key spatial neighbours of every routed tile, `_spatial_neighbors`
+ * 258-276) and policy 2 ("directional": the eight neighbours of tiles whose
+ * mass is at least huge_factor times the head's mean selected mass, and up to
+ * three one-step moves of the others along their fp16 centroid directions,
+ * `_apply_directional_steps` 285-324).  Tiles are numbered frame-major over
+ * frames x blocks_h x blocks_w; mask, out: [heads, tiles, tiles] bytes;
+ * mass_f16 and the centroids: fp16 of the same shape (directional only);
+ * head_scratch: device float[2 * heads] (directional only).
+ */
+int dsa_expand_route(const uint8_t* mask, const void* mass_f16, const void* centroid_q_y,
+                     const void* centroid_q_x, const void* centroid_k_y,
+                     const void* centroid_k_x, int32_t heads, int32_t frames, int32_t blocks_h,
+                     int32_t blocks_w, int32_t policy, float centroid_threshold,
+                     float huge_factor, float* head_scratch, uint8_t* out, hipStream_t stream);
 
 /*
  * Boolean route rows -> CSR (ascending key blocks per row).

@@ -8,6 +8,8 @@ run here:
   * FlexReuseBackend._sampled_route   persistence prior + selection
   * spatial.build_spatial_layout      Morton order and majority-vote neighbours
   * sparse.MatrixSparseBackend  config-0 bootstrap route, mass and outputs
+  * sparse.MatrixSparseBackend  four steps per policy (reuse / all / directional):
+    masks, fp16 mass and centroids, outputs (drop, expansion and statistics)
   * routing.frontier_mask / directional_budget_update   on the 720p block
     neighbour table (the known answers of test_directional_routing.py cover
     one line-shaped case only)
@@ -190,6 +192,47 @@ def routing_fixture(routing, spatial):
     _save("routing", **arrays)
 
 
+MATRIX_SPARSE_CASES = {
+    # name: (grid, heads, policy)
+    "g4x16x16_reuse": ((4, 16, 16), 4, "reuse"),
+    "g4x16x16_all": ((4, 16, 16), 4, "all"),
+    "g4x16x16_directional": ((4, 16, 16), 4, "directional"),
+    "g2x24x32_directional": ((2, 24, 32), 3, "directional"),
+    "g2x24x32_all": ((2, 24, 32), 3, "all"),
+}
+
+
+def matrix_sparse_fixture(context, sparse):
+    """MatrixSparseBackend through steps 0..3 (fresh clustered inputs per
+    step): the route state after every step and an output sample."""
+    arrays = {}
+    for name, (grid, heads, policy) in MATRIX_SPARSE_CASES.items():
+        tokens = grid[0] * grid[1] * grid[2]
+        backend = sparse.MatrixSparseBackend(sparse.SparseConfig(
+            tile=64, keep=0.625, mass_target=0.95, policy=policy, prefetch_route=False))
+        layout = sparse._spatial_layout(grid, 64, tokens)
+        order = layout.to_tile_major(torch.arange(tokens).view(1, tokens, 1, 1)).flatten()
+        arrays[f"{name}__params"] = np.array([*grid, heads, layout.tile_h, layout.tile_w])
+        context.reset_runtime_state()
+        context._STATE.attention_id = 1
+        context._STATE.cfg_branch = 0
+        context._STATE.grid_size = grid
+        for step in range(4):
+            q, k, v = clustered_qkv(tokens, heads, 128, group=64, seed=40 + step,
+                                    permutation=order)
+            context._STATE.denoising_step = step
+            with torch.no_grad():
+                out = backend(q, k, v, dtype=torch.float32)
+            state = next(iter(backend.state.values()))
+            arrays[f"{name}__step{step}_mask"] = np.packbits(state["mask"].numpy())
+            arrays[f"{name}__step{step}_mass"] = state["mass"].numpy()
+            for key in ("centroid_q_y", "centroid_q_x", "centroid_k_y", "centroid_k_x"):
+                arrays[f"{name}__step{step}_{key}"] = state[key].numpy()
+            # Output sample: the first 32 tokens (original order), heads 0-1, fp16.
+            arrays[f"{name}__step{step}_out"] = out[0, :32, :2].to(torch.float16).numpy()
+    _save("matrix_sparse", **arrays)
+
+
 def main():
     torch.set_num_threads(4)
     context, flex, routing, sparse, spatial = _reference_modules()
@@ -199,6 +242,7 @@ def main():
     spatial_fixture(spatial)
     sparse_config0_fixture(context, sparse)
     routing_fixture(routing, spatial)
+    matrix_sparse_fixture(context, sparse)
 
 
 if __name__ == "__main__":

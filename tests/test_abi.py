@@ -57,8 +57,8 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 128, 128,
                              None, None, 1, 0.1, None, fake, 16, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
-    status = lib.dsa_route_select(fake, None, 4, 600, 0.5, 0.95, 1, 0, fake, fake, None)
-    assert status == _lib.DSA_EUNSUPPORTED and "512" in _lib.last_error()
+    status = lib.dsa_route_select(fake, None, 4, 1100, 0.5, 0.95, 1, 0, fake, fake, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "1024" in _lib.last_error()
     status = lib.dsa_sampled_mass(fake, fake, _lib.int64_array([8] * 4), 1024, 2, 128, 128, 3,
                                   0.1, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "power of two" in _lib.last_error()
@@ -92,3 +92,17 @@ def test_exact_and_routing_entry_points_validate_first(lib):
                                         0, 7, 0, fake, fake, ctypes.c_void_p(4097), None, None,
                                         None, None)
     assert status == _lib.DSA_EINVAL and "aligned" in _lib.last_error()
+
+
+def test_tile_stats_validates_first(lib):
+    fake = ctypes.c_void_p(16)
+    strides = _lib.int64_array([8] * 4)
+    status = lib.dsa_tile_stats(fake, fake, strides, 1024, 2, 128, 12, 12, fake, 1024, None,
+                                None, 0.1, fake, None, None, None, None, None, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "128" in _lib.last_error()
+    status = lib.dsa_tile_stats(fake, fake, strides, 1000, 2, 128, 8, 8, fake, 1000, None,
+                                None, 0.1, fake, None, None, None, None, None, None)
+    assert status == _lib.DSA_EINVAL and "whole" in _lib.last_error()
+    status = lib.dsa_tile_stats(fake, fake, strides, 1024, 2, 128, 8, 8, fake, 1024, fake,
+                                None, 0.1, fake, None, None, None, None, None, None)
+    assert status == _lib.DSA_EINVAL

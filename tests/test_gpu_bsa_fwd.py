@@ -142,3 +142,36 @@ def test_config1_dense_rope_against_sdpa_and_fp32(cuda_device):
             metrics = _gpu_metrics(out[b, rows, h], expected)
             assert metrics["max_absolute_error"] <= MAX_ABS, (b, h, metrics)
             assert metrics["cosine_similarity"] >= MIN_COSINE, (b, h, metrics)
+
+
+@pytest.mark.parametrize("block,tokens", [(8, 200), (40, 600), (64, 1024), (65, 650),
+                                          (72, 1440), (72, 1400), (100, 777), (128, 1000)])
+def test_tile_blocks_match_oracle(cuda_device, block, tokens):
+    """Blocks of 1..128 tokens (the matrix-sparse backend's spatial tiles,
+    sparse.py:670-751): one 64-key half-tile per block up to 64 keys, two
+    above, partial last blocks, rows past a short block never stored."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    q, k, v = _inputs(1, tokens, 2, seed=block)
+    blocks = math.ceil(tokens / block)
+    generator = torch.Generator().manual_seed(block)
+    route = torch.rand(2, blocks, blocks, generator=generator) < 0.5
+    route[..., 0] = True
+    csr = csr_from_route(route.to(cuda_device), block_size=block)
+    out, lse = bsa_fwd(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device), csr,
+                       return_lse=True, block_size=block)
+    torch.cuda.synchronize()
+    _check(out, q, k, v, route, block=block)
+    _, expected_lse = block_sparse_attention(
+        q.float().numpy(), k.float().numpy(), v.float().numpy(), route.numpy(), block)
+    np.testing.assert_allclose(lse.cpu().numpy(), expected_lse, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("block", [24, 72, 128])
+def test_dense_result_independent_of_block(cuda_device, block):
+    """Without a route every key is attended whatever the block size."""
+    from dit_sparse_atten_amd.ops import bsa_fwd
+    q, k, v = _inputs(1, 700, 2, seed=3)
+    qd, kd, vd = (t.to(cuda_device) for t in (q, k, v))
+    out = bsa_fwd(qd, kd, vd, block_size=block)
+    torch.cuda.synchronize()
+    _check(out, q, k, v, None)

@@ -1,0 +1,215 @@
+"""GPU parity of the matrix-sparse (``sparse``) backend pieces against the oracle
+(oracle/sparse_path.py, itself equal to the reference's sparse.py on the
+golden cases): tile statistics within fp32 tolerance of its numpy restatement
+on the same bf16 inputs, routes bit-exact given the same mass,
+outputs within max-abs 2e-2 / cosine 0.9995."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import route as R
+from oracle import sparse_path as S
+from tests.golden.inputs import clustered_qkv, random_route, route_mass
+
+pytestmark = pytest.mark.gpu
+
+STAT_ATOL = 2e-5     # normalised mass (values ~ 1 / tiles^2 .. 1 / tiles)
+CENTROID_ATOL = 2e-3  # fp16 centroids in [-1, 1]
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from dit_sparse_atten_amd import ops as module
+    return module
+
+
+def _tile_major_inputs(grid, heads, seed, tile=64):
+    case = S.SparsePathCase(grid, tile=tile)
+    tokens = grid[0] * grid[1] * grid[2]
+    q, k, v = clustered_qkv(tokens, heads, 128, group=case.tile, seed=seed,
+                            permutation=torch.as_tensor(case.permutation, dtype=torch.long),
+                            dtype=torch.bfloat16)
+    # Tile-major order on both sides.
+    perm = torch.as_tensor(case.permutation, dtype=torch.long)
+    return case, q[:, perm], k[:, perm], v[:, perm]
+
+
+def _oracle_stats(case, q, k, v, route=None):
+    """Oracle statistics (fp32 numpy) of tile-major bf16 inputs."""
+    qf, kf, vf = (x.float().numpy() for x in (q, k, v))
+    tokens, heads = qf.shape[1:3]
+    tiles = tokens // case.tile
+    stats = S.empty_stats(heads, tiles)
+    offsets = S.spatial_offsets(case.tile_shape, tiles)
+    scale = 128 ** -0.5
+    if route is None:
+        _, _, out = S.dense_route(qf, kf, vf, case.tile, 256, 0.95, 0.625, scale, stats, offsets)
+    else:
+        out = np.empty_like(qf)
+        for start in range(0, tokens, case.tile * 4):
+            end = min(start + case.tile * 4, tokens)
+            out[:, start:end] = S.sparse_chunk(qf, kf, vf, route, case.tile, start, end, scale,
+                                               stats, offsets)
+    den = np.maximum(stats["mass"], np.float32(1e-12))
+    expected = {"mass": (stats["mass"] / np.float32(tokens)).astype(np.float32)}
+    for name in ("q_y", "q_x", "k_y", "k_x"):
+        expected[f"centroid_{name}"] = (stats[name] / den).astype(np.float32)
+    return expected, out
+
+
+def _compare_stats(got, expected):
+    np.testing.assert_allclose(got["mass"].cpu().numpy(), expected["mass"], atol=STAT_ATOL,
+                               rtol=2e-3)
+    np.testing.assert_allclose(got["mass_f16"].float().cpu().numpy(), expected["mass"],
+                               atol=STAT_ATOL, rtol=2e-3)
+    for name in ("q_y", "q_x", "k_y", "k_x"):
+        key = f"centroid_{name}"
+        np.testing.assert_allclose(got[key].float().cpu().numpy(), expected[key],
+                                   atol=CENTROID_ATOL, err_msg=key)
+
+
+@pytest.mark.parametrize("grid", [(4, 16, 16), (2, 18, 32), (2, 24, 32)])
+def test_dense_tile_stats_match_oracle(ops, cuda_device, grid):
+    """Tiles of 8x8 (64 tokens) and 9x8 (72 tokens: two half-tiles per tile)."""
+    case, q, k, v = _tile_major_inputs(grid, 3, seed=sum(grid))
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    _, lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
+    got = ops.tile_stats(qd, kd, lse, case.tile_shape)
+    torch.cuda.synchronize()
+    expected, _ = _oracle_stats(case, q, k, v)
+    _compare_stats(got, expected)
+    # Every query row of the dense softmax sums to one: rows of mass sum to tile / tokens.
+    np.testing.assert_allclose(got["mass"].sum(-1).cpu().numpy(),
+                               case.tile / q.shape[1], rtol=1e-4)
+
+
+@pytest.mark.parametrize("grid", [(4, 16, 16), (2, 18, 32)])
+def test_routed_tile_attention_and_stats_match_oracle(ops, cuda_device, grid):
+    case, q, k, v = _tile_major_inputs(grid, 2, seed=7)
+    tiles = q.shape[1] // case.tile
+    route = random_route(2, tiles, seed=3, keep=0.5).numpy()
+    route[..., 0] = True
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=case.tile)
+    out, lse = ops.bsa_fwd(qd, kd, vd, csr, return_lse=True, block_size=case.tile)
+    got = ops.tile_stats(qd, kd, lse, case.tile_shape, csr=csr)
+    torch.cuda.synchronize()
+    expected, expected_out = _oracle_stats(case, q, k, v, route)
+    _compare_stats(got, expected)
+    metrics = A.summarize(out.float().cpu().numpy(), expected_out)
+    assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
+    assert (got["mass"].cpu().numpy()[~route] == 0).all()
+
+
+def test_route_select_up_to_1024_tiles(ops, cuda_device):
+    """The 720p tile route has 800 key tiles per row (one-wave 1024-key sort)."""
+    rng = np.random.default_rng(5)
+    for keys in (513, 800, 1024):
+        mass = rng.dirichlet(np.full(keys, 0.3), size=(3, 40)).astype(np.float32)
+        route, counts = ops.route_select(torch.from_numpy(mass).to(cuda_device), 0.95, 0.625,
+                                         sink_blocks=100)
+        torch.cuda.synchronize()
+        expected = R.top_mass_route(mass, 0.95, 0.625)
+        expected[..., :100] = True
+        np.testing.assert_array_equal(route.cpu().numpy(), expected)
+        np.testing.assert_array_equal(counts.cpu().numpy(), expected.sum(-1))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("heads,tiles,drop", [(4, 16, 0.1), (8, 800, 0.1), (4, 100, 1.5)])
+def test_drop_low_mass_bit_exact(ops, cuda_device, dtype, heads, tiles, drop):
+    mass = (route_mass(heads, tiles, seed=tiles) / tiles).to(dtype)
+    mask = random_route(heads, tiles, seed=tiles + 1, keep=0.6).numpy()
+    mask[0, 3] = False  # an empty row stays empty
+    out, counts = ops.drop_low_mass(torch.from_numpy(mask).to(cuda_device),
+                                    mass.to(cuda_device), drop, sink_tiles=4)
+    torch.cuda.synchronize()
+    mnp = mass.numpy() if dtype == torch.float16 else mass.float().numpy()
+    expected = S.drop_low_mass(mask, mnp, drop)
+    expected[..., :4] = True
+    np.testing.assert_array_equal(out.cpu().numpy(), expected)
+    np.testing.assert_array_equal(counts.cpu().numpy(), expected.sum(-1))
+
+
+@pytest.mark.parametrize("policy", ["all", "directional"])
+@pytest.mark.parametrize("grid_tiles", [(4, 2, 2), (2, 3, 4), (16, 5, 10)])
+def test_expand_route_bit_exact(ops, cuda_device, policy, grid_tiles):
+    heads = 3
+    tiles = math.prod(grid_tiles)
+    mask = random_route(heads, tiles, seed=tiles, keep=0.3).numpy()
+    rng = np.random.default_rng(tiles)
+    state = {"mask": mask,
+             "mass": (rng.random((heads, tiles, tiles)) ** 4 / tiles).astype(np.float16)}
+    for name in ("q_y", "q_x", "k_y", "k_x"):
+        state[f"centroid_{name}"] = rng.uniform(-0.6, 0.6, (heads, tiles, tiles)).astype(
+            np.float16)
+    centroids = [torch.from_numpy(state[f"centroid_{n}"]).to(cuda_device)
+                 for n in ("q_y", "q_x", "k_y", "k_x")]
+    out = ops.expand_route(torch.from_numpy(mask).to(cuda_device), grid_tiles, policy,
+                           mass=torch.from_numpy(state["mass"]).to(cuda_device),
+                           centroids=centroids)
+    torch.cuda.synchronize()
+    expected = S.expand(state, policy, grid_tiles)
+    np.testing.assert_array_equal(out.cpu().numpy(), expected)
+
+
+@pytest.mark.parametrize("policy", ["reuse", "all", "directional"])
+def test_backend_steps_match_oracle(ops, cuda_device, policy):
+    """Four steps of MatrixSparseBackend on a 9x8-tile grid.  At every step the
+    output matches the oracle's attention over the route the backend used, and
+    the stored mask equals the oracle's selection (step 0) or drop + sink
+    (later steps) of the same mass, recomputed with the same kernels; the
+    route used is the oracle's expansion of the previous stored state."""
+    from dit_sparse_atten_amd.attention_backends import context
+    from dit_sparse_atten_amd.attention_backends.sparse import MatrixSparseBackend, SparseConfig
+    grid, heads = (2, 18, 32), 3
+    case = S.SparsePathCase(grid, tile=64)
+    tokens = grid[0] * grid[1] * grid[2]
+    perm = torch.as_tensor(case.permutation, dtype=torch.long)
+    sink = case.block_h * case.block_w
+    grid_tiles = (grid[0], case.block_h, case.block_w)
+    backend = MatrixSparseBackend(SparseConfig(tile=64, keep=0.625, mass_target=0.95,
+                                               policy=policy))
+    context.reset_runtime_state()
+    try:
+        previous = None
+        for step in range(4):
+            q, k, v = clustered_qkv(tokens, heads, 128, group=64, seed=60 + step,
+                                    permutation=perm, dtype=torch.bfloat16)
+            context.set_routing_context(attention_id=2, step=step, branch=0, grid=grid)
+            out = backend(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device))
+            torch.cuda.synchronize()
+            state = {key: val.cpu().numpy() for key, val in
+                     next(iter(backend.state.values())).items() if torch.is_tensor(val)}
+            # Tile-major inputs, as the backend sees them.
+            qt, kt, vt = (x[:, perm].to(cuda_device) for x in (q, k, v))
+            route_used = None if previous is None else S.expand(previous, policy, grid_tiles)
+            expected_out, _ = A.block_sparse_attention(
+                *(x.float().cpu().numpy() for x in (qt, kt, vt)), route_used, case.tile)
+            restored = np.empty_like(expected_out)
+            restored[:, perm.numpy()] = expected_out
+            metrics = A.summarize(out.float().cpu().numpy(), restored)
+            assert metrics["max_absolute_error"] <= 2e-2, (step, metrics)
+            assert metrics["cosine_similarity"] >= 0.9995, (step, metrics)
+            if route_used is None:
+                _, lse = ops.bsa_fwd(qt, kt, vt, return_lse=True)
+                mass = ops.tile_stats(qt, kt, lse, case.tile_shape)["mass"].cpu().numpy()
+                expected_mask = R.top_mass_route(mass, 0.95, 0.625)
+            elif policy == "reuse":
+                expected_mask = S.drop_low_mass(route_used, previous["mass"], 0.1)
+            else:
+                csr = ops.route_to_csr(torch.from_numpy(route_used).to(cuda_device),
+                                       block_size=case.tile)
+                _, lse = ops.bsa_fwd(qt, kt, vt, csr, return_lse=True, block_size=case.tile)
+                mass = ops.tile_stats(qt, kt, lse, case.tile_shape, csr=csr)["mass"]
+                expected_mask = S.drop_low_mass(route_used, mass.cpu().numpy(), 0.1)
+            expected_mask = np.array(expected_mask, copy=True)
+            expected_mask[..., :sink] = True
+            np.testing.assert_array_equal(state["mask"], expected_mask, err_msg=f"step {step}")
+            previous = state
+    finally:
+        context.reset_runtime_state()
