@@ -366,6 +366,56 @@ def main():
             "reference_block_mass_ms": 749.2, "reference_route_selection_ms": 31.4,
             "reference_source": "results/flex_lse_57k_summary.json (keep .5, target .9)",
         }
+        # Matrix-sparse backend (sparse.py) at the same shape: 9x8 = 72-token
+        # spatial tiles of the 16x45x80 grid (800 tiles), Bernoulli(keep) tile
+        # routes plus the 50-tile first-frame sink, tile-major inputs.
+        from dit_sparse_atten_amd.attention_backends.sparse import _spatial_layout
+        tile_layout = _spatial_layout(GRID, 64, TOKENS)
+        tile = tile_layout.tile_tokens
+        tiles = tile_layout.tile_count
+        tile_sink = tile_layout.block_h * tile_layout.block_w
+        tgen = torch.Generator(device=device).manual_seed(7)
+        tile_route = torch.rand((HEADS, tiles, tiles), device=device, generator=tgen) < KEEP
+        tile_route[..., :tile_sink] = True
+        tile_csr = ops.route_to_csr(tile_route, block_size=tile)
+        tile_nnz = tile_csr.nnz_value()
+        qt, kt, vt = tile_layout.to_tile_major(q, k, v)
+        tile_out = torch.empty_like(out)
+
+        def tile_attention():
+            ops.bsa_fwd(qt, kt, vt, tile_csr, out=tile_out, block_size=tile)
+
+        def tile_step_directional():
+            _, tlse = ops.bsa_fwd(qt, kt, vt, tile_csr, out=tile_out, return_lse=True,
+                                  block_size=tile)
+            tstats = ops.tile_stats(qt, kt, tlse, (tile_layout.tile_h, tile_layout.tile_w),
+                                    csr=tile_csr)
+            ops.drop_low_mass(tile_route, tstats["mass"], 0.1, tile_sink)
+
+        def tile_bootstrap():
+            _, tlse = ops.bsa_fwd(qt, kt, vt, out=tile_out, return_lse=True)
+            tstats = ops.tile_stats(qt, kt, tlse, (tile_layout.tile_h, tile_layout.tile_w))
+            ops.route_select(tstats["mass"], 0.9, KEEP, sink_blocks=tile_sink)
+
+        tile_attention()
+        tile_step_directional()
+        torch.cuda.synchronize()
+        tile_ms, _ = timer.time(tile_attention, 5)
+        tile_step_ms, _ = timer.time(tile_step_directional, 3)
+        tile_boot_ms, _ = timer.time(tile_bootstrap, 2)
+        tile_flops = 4.0 * HEAD_DIM * tile * tile * tile_nnz
+        result["matrix_sparse"] = {
+            "tile_shape": [tile_layout.tile_h, tile_layout.tile_w],
+            "tiles": tiles,
+            "realized_keep": round(tile_nnz / (HEADS * tiles * tiles), 6),
+            "attention_ms": round(tile_ms, 4),
+            "attention_eff_tflops": round(tile_flops / (tile_ms * 1e-3) / 1e12, 2),
+            "directional_step_ms": round(tile_step_ms, 4),
+            "bootstrap_ms": round(tile_boot_ms, 4),
+            "reference_pytorch_sparse_ms": 8396.6, "reference_triton_sparse_ms": 4038.5,
+            "reference_source": ("results/sparse_attention_profile.json (57,600 tokens, "
+                                 "40 heads, 6x10 tiles, keep .625)"),
+        }
         result["reference_published"] = {
             "device": "PPU-ZW810E (reference's own run)",
             "sparse_flex_ms": 703.6, "sparse_eff_tflops": 60.5,
