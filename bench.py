@@ -47,6 +47,8 @@ def parse_args():
     parser.add_argument("--cpu-sample-rows", type=int, default=64,
                         help="(head, query-block) rows timed for the CPU baseline")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-e2e", action="store_true",
+                        help="skip the end-to-end denoising loop (BASELINE config 4)")
     parser.add_argument("--only-sparse", action="store_true",
                         help="time only the sparse call (profiling runs)")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -165,6 +167,74 @@ def cpu_baseline(q, k, v, route, rows):
                    f"{flops / 1e9:.1f} GFLOP in {seconds:.2f} s; cpu {cpu_model or platform.machine()}"),
         "ms_per_call_extrapolated": seconds / flops * kept_flops(int(route.sum())) * 1e3,
     }
+
+
+def e2e_loop(device):
+    """random-init Wan2.1-1.3B-shaped DiT, 5 steps at
+    1280x720x61 (57,600 tokens), CFG pair, 512 x 4096 text embeddings; the
+    dense backend against the flex_reuse hybrid of the reference's timed run
+    (sampled bootstrap with prefetch, sampled update every 2 steps without
+    prefetch, 16 samples, persistence .5, target .95, keep .625, 1x16 Morton
+    micro-tiles, dense dispatch at keep >= .58) and the same hybrid without
+    dense dispatch.  Each model call is bracketed by HIP events."""
+    from dit_sparse_atten_amd.attention_backends import context
+    from dit_sparse_atten_amd.attention_backends.dense import DenseBackend
+    from dit_sparse_atten_amd.attention_backends.flex import FlexReuseBackend, FlexReuseConfig
+    from dit_sparse_atten_amd.wan_dit import WanDiT, denoise
+
+    model = WanDiT(device=device, seed=11)
+    gen = torch.Generator(device=device).manual_seed(12)
+    latents = torch.randn(1, 16, 16, 90, 160, device=device, generator=gen).bfloat16()
+    text_cond = torch.randn(1, 512, 4096, device=device, generator=gen).bfloat16()
+    text_uncond = torch.randn(1, 512, 4096, device=device, generator=gen).bfloat16()
+
+    def hybrid(threshold):
+        return FlexReuseBackend(FlexReuseConfig(
+            bootstrap_mode="sampled", prefetch_sampled_bootstrap=True,
+            sampled_update_interval=2, prefetch_sampled_update=False, route_samples=16,
+            route_persistence=0.5, mass_target=0.95, keep=0.625,
+            dense_route_threshold=threshold, total_steps=5, spatial_reorder=True))
+
+    context.reset_runtime_state()
+    model(latents, 999.0, model.embed_text(text_cond), DenseBackend())  # warm-up
+    torch.cuda.synchronize()
+    runs = {}
+    for name, backend in (("dense", DenseBackend()), ("flex_hybrid_0.58", hybrid(0.58)),
+                          ("flex_no_dense_dispatch", hybrid(None))):
+        context.reset_runtime_state()
+        marks = []
+
+        def on_call(step, branch, phase):
+            event = torch.cuda.Event(enable_timing=True)
+            event.record()
+            marks.append(event)
+
+        denoise(model, backend, latents, text_cond, text_uncond, steps=5, on_call=on_call)
+        torch.cuda.synchronize()
+        calls = [marks[i].elapsed_time(marks[i + 1]) for i in range(0, len(marks), 2)]
+        entry = {"model_forward_ms": round(sum(calls), 1),
+                 "forward_ms_per_call": [round(t, 1) for t in calls]}
+        if hasattr(backend, "profile_summary"):
+            summary = backend.profile_summary()
+            entry["phase_counts"] = summary["phase_counts"]
+            keep = summary["mean_route_keep"]
+            entry["mean_route_keep"] = None if keep is None else round(float(keep), 4)
+            entry["dense_dispatched_routes"] = summary["dense_dispatched_routes"]
+        runs[name] = entry
+        print(f"e2e {name}: {entry['model_forward_ms']} ms", file=sys.stderr, flush=True)
+    dense_ms = runs["dense"]["model_forward_ms"]
+    for entry in runs.values():
+        entry["speedup_vs_dense"] = round(dense_ms / entry["model_forward_ms"], 3)
+    context.reset_runtime_state()
+    return {"workload": "Wan2.1-1.3B shape (30 layers, dim 1536, 12 heads, d=128), random "
+                        "init, latents 16x16x90x160 -> 57,600 tokens, 5 steps x CFG pair, "
+                        "text 512x4096",
+            "runs": runs,
+            "reference_published": {
+                "device": "PPU-ZW810E (reference's own run, Wan2.1-14B, 40 layers)",
+                "dense_model_forward_s": 406.6, "flex_hybrid_0.58_model_forward_s": 386.9,
+                "source": "results/final_{dense,flex_hybrid058_update2_release}_57k_5step_"
+                          "timing.json"}}
 
 
 def main():
@@ -422,6 +492,9 @@ def main():
             "dense_sdpa_ms": 677.6, "route_update_ms": 79.3,
             "source": "results/flex_route_profile_target95_keep625.json",
         }
+
+    if not args.no_e2e and not args.only_sparse:
+        result["e2e"] = e2e_loop(device)
 
     if not args.no_cpu_baseline and not args.only_sparse:
         result["cpu_baseline"] = cpu_baseline(q, k, v, route, args.cpu_sample_rows)

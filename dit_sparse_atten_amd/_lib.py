@@ -99,6 +99,21 @@ SIGNATURES = {
         _c_ptr, _c_int, _c_int, _c_int, _c_int,                  # perm, batch, tokens, heads, row_bytes
         _c_ptr,                                                  # stream
     )),
+    "dsa_layernorm_modulate": (_c_int, (
+        _c_ptr, _c_i64, _c_int, _c_int,            # x, x_stride, rows, dim
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr,            # weight, bias, shift, scale
+        _c_int, _c_float, _c_ptr, _c_i64, _c_ptr,  # rows_per_group, eps, out, out_stride, stream
+    )),
+    "dsa_rmsnorm_rope": (_c_int, (
+        _c_ptr, _c_i64, _c_int, _c_int, _c_int,    # x, x_stride, rows, dim, head_dim
+        _c_ptr, _c_ptr, _c_int, _c_float,          # weight, cos_sin, tokens, eps
+        _c_ptr, _c_i64, _c_ptr,                    # out, out_stride, stream
+    )),
+    "dsa_gated_residual": (_c_int, (
+        _c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr,    # x, x_stride, y, y_stride, gate
+        _c_int, _c_int, _c_int, _c_ptr, _c_i64,    # rows, dim, rows_per_group, out, out_stride
+        _c_ptr,                                    # stream
+    )),
 }
 
 _lock = threading.Lock()

@@ -421,6 +421,20 @@ class FlexReuseBackend:
         if self.config.spatial_reorder and layout is None:
             return self.dense(q, k, v, **dense_kwargs)
 
+        key = (attention_id, branch, q.shape[1], q.shape[2], q.shape[3], q.device,
+               layout.signature if layout is not None else None)
+        state = self.state.get(key) if step != 0 else None
+        if state is not None:
+            self._activate_pending_route(state)
+            if state.get("dense"):
+                # Dense attention commutes with the token permutation, so a
+                # dense-dispatched state skips the reorder and restore that the
+                # reference performs first (flex.py:690-700, 766-775).
+                self.phase_counts["dense_dispatch"] += 1
+                if self._is_final_step(step):
+                    self._release_route(key, state)
+                return self.dense(q, k, v, **dense_kwargs)
+
         output_dtype = q.dtype
         q = q.to(dtype)
         k = k.to(dtype)
@@ -439,9 +453,7 @@ class FlexReuseBackend:
             return self.dense(q, k, v, dropout_p=0.0, softmax_scale=softmax_scale,
                               q_scale=None, causal=False, window_size=(-1, -1), dtype=dtype)
 
-        key = (attention_id, branch, q.shape[1], q.shape[2], q.shape[3], q.device,
-               layout.signature if layout is not None else None)
-        if step == 0 or key not in self.state:
+        if state is None:
             state = {
                 "route": None,
                 "frontier": None,
@@ -474,15 +486,6 @@ class FlexReuseBackend:
                 self.phase_counts["sampled_bootstrap"] += 1
             if self._is_final_step(step):
                 self._release_route(key, self.state[key])
-            return finish(output)
-
-        state = self.state[key]
-        self._activate_pending_route(state)
-        if state.get("dense"):
-            self.phase_counts["dense_dispatch"] += 1
-            output = dense_output()
-            if self._is_final_step(step):
-                self._release_route(key, state)
             return finish(output)
 
         if (self.config.update_interval > 0

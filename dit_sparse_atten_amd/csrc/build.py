@@ -26,6 +26,7 @@ SOURCES = (
     "routing.hip",
     "tile_route.hip",
     "permute.hip",
+    "dit_ops.hip",
 )
 
 # Packed FP32 VALU forms are disabled: the device code relies on scalar and

@@ -589,3 +589,88 @@ def permute_tokens(tensors, permutation, out=None, head_major=False):
             _stream_handle(first.device))
     _lib.check(status, "dsa_permute_rows")
     return out
+
+
+# ---------------------------------------------------------------------------
+# Wan DiT block elementwise work (end-to-end loop)
+# ---------------------------------------------------------------------------
+
+def _rows_view(name, x):
+    _require_cuda(name, x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    dim = x.shape[-1]
+    rows = x.numel() // dim
+    flat = x.reshape(rows, dim) if x.is_contiguous() else x.contiguous().reshape(rows, dim)
+    return flat
+
+
+def _f32_or_none(name, t, device):
+    if t is None:
+        return None
+    _require_cuda(name, t)
+    if t.dtype != torch.float32:
+        raise ValueError(f"{name} must be float32")
+    if t.device != device:
+        raise ValueError(f"{name} must live on the tensor's device")
+    return t.contiguous()
+
+
+def layernorm_modulate(x, shift=None, scale=None, weight=None, bias=None, eps=1e-6, out=None):
+    """LN(x) [* weight + bias] [* (1 + scale) + shift] over the last axis of a
+    bf16 [B, T, C] tensor; shift/scale fp32 [B, C] (one vector per batch item)."""
+    lib = _lib.load()
+    flat = _rows_view("x", x)
+    rows, dim = flat.shape
+    weight, bias, shift, scale = (_f32_or_none(n, t, x.device) for n, t in (
+        ("weight", weight), ("bias", bias), ("shift", shift), ("scale", scale)))
+    per_group = rows // (scale.numel() // dim) if scale is not None else rows
+    out = torch.empty_like(flat) if out is None else out.reshape(rows, dim)
+    with torch.cuda.device(x.device):
+        status = lib.dsa_layernorm_modulate(
+            flat.data_ptr(), flat.stride(0), rows, dim,
+            *[t.data_ptr() if t is not None else None for t in (weight, bias, shift, scale)],
+            per_group, float(eps), out.data_ptr(), out.stride(0), _stream_handle(x.device))
+    _lib.check(status, "dsa_layernorm_modulate")
+    return out.reshape(x.shape)
+
+
+def rmsnorm_rope(x, weight, head_dim=128, cos_sin=None, eps=1e-6, out=None):
+    """rope(RMSNorm(x) * weight) over the last axis of bf16 [B, T, C]; cos_sin
+    fp32 [T, head_dim / 2, 2] or None (no rotation)."""
+    lib = _lib.load()
+    flat = _rows_view("x", x)
+    rows, dim = flat.shape
+    weight = _f32_or_none("weight", weight, x.device)
+    cos_sin = _f32_or_none("cos_sin", cos_sin, x.device)
+    tokens = x.shape[-2] if x.ndim >= 2 else rows
+    out = torch.empty_like(flat) if out is None else out.reshape(rows, dim)
+    with torch.cuda.device(x.device):
+        status = lib.dsa_rmsnorm_rope(
+            flat.data_ptr(), flat.stride(0), rows, dim, head_dim, weight.data_ptr(),
+            cos_sin.data_ptr() if cos_sin is not None else None, tokens, float(eps),
+            out.data_ptr(), out.stride(0), _stream_handle(x.device))
+    _lib.check(status, "dsa_rmsnorm_rope")
+    return out.reshape(x.shape)
+
+
+def gated_residual(x, y, gate=None, out=None):
+    """x + gate * y over bf16 [B, T, C]; gate fp32 [B, C] or None (1)."""
+    lib = _lib.load()
+    fx = _rows_view("x", x)
+    fy = _rows_view("y", y)
+    if fx.shape != fy.shape:
+        raise ValueError("x and y must have the same shape")
+    rows, dim = fx.shape
+    gate = _f32_or_none("gate", gate, x.device)
+    per_group = rows // (gate.numel() // dim) if gate is not None else rows
+    out = torch.empty_like(fx) if out is None else out.reshape(rows, dim)
+    with torch.cuda.device(x.device):
+        status = lib.dsa_gated_residual(
+            fx.data_ptr(), fx.stride(0), fy.data_ptr(), fy.stride(0),
+            gate.data_ptr() if gate is not None else None, rows, dim, per_group,
+            out.data_ptr(), out.stride(0), _stream_handle(x.device))
+    _lib.check(status, "dsa_gated_residual")
+    return out.reshape(x.shape)

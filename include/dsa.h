@@ -236,6 +236,33 @@ int dsa_permute_rows(int32_t tensors, const void* const* src, void* const* dst,
                      const int32_t* perm, int32_t batch, int32_t tokens, int32_t heads,
                      int32_t row_bytes, hipStream_t stream);
 
+/*
+ * Non-GEMM work of the Wan DiT block around the attention call, for the
+ * end-to-end denoising loop (the reference runs it through Diffusers'
+ * WanTransformerBlock, wan_diffusers.py:75-191).  Rows are bf16 [rows, dim]
+ * (dim a multiple of 8, <= 8192; row strides in elements; 16-byte aligned);
+ * arithmetic in fp32; in-place use (out == x) is allowed.
+ *
+ * dsa_layernorm_modulate: out = LN(x) [* weight + bias] [* (1 + scale) + shift]
+ *   (LayerNorm without or with affine; shift/scale fp32 [groups, dim], row r
+ *   using group r / rows_per_group) - norm1/norm3 + modulation and norm2.
+ * dsa_rmsnorm_rope: out = rope(x * rsqrt(mean(x^2) + eps) * weight) - the
+ *   q/k RMSNorm, then (cos_sin != NULL, fp32 [tokens, head_dim / 2, 2]) the
+ *   rotation of every head's consecutive (even, odd) pairs for token r % tokens.
+ * dsa_gated_residual: out = x + gate * y (gate fp32 [groups, dim] or NULL = 1).
+ */
+int dsa_layernorm_modulate(const void* x, int64_t x_stride, int32_t rows, int32_t dim,
+                           const float* weight, const float* bias, const float* shift,
+                           const float* scale, int32_t rows_per_group, float eps, void* out,
+                           int64_t out_stride, hipStream_t stream);
+int dsa_rmsnorm_rope(const void* x, int64_t x_stride, int32_t rows, int32_t dim,
+                     int32_t head_dim, const float* weight, const float* cos_sin,
+                     int32_t tokens, float eps, void* out, int64_t out_stride,
+                     hipStream_t stream);
+int dsa_gated_residual(const void* x, int64_t x_stride, const void* y, int64_t y_stride,
+                       const float* gate, int32_t rows, int32_t dim, int32_t rows_per_group,
+                       void* out, int64_t out_stride, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

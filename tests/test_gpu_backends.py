@@ -97,6 +97,38 @@ def test_sampled_update_can_switch_route_to_dense(backends, cuda_device, monkeyp
     assert backend.phase_counts["dense_dispatch"] == 1
 
 
+def test_dense_dispatched_state_skips_reorder(backends, cuda_device, monkeypatch):
+    """A dense-dispatched (layer, branch) with a spatial layout runs dense
+    attention on the caller's token order: same output as the dense oracle,
+    no reorder or restore, released on the final step."""
+    flex, context = backends
+    grid = (2, 16, 32)
+    tokens = math.prod(grid)
+    q, k, v = clustered_qkv(tokens, 2, 128, group=64, seed=21, dtype=torch.bfloat16)
+    backend = flex.FlexReuseBackend(flex.FlexReuseConfig(
+        bootstrap_mode="sampled", dense_route_threshold=0.58, total_steps=4,
+        spatial_reorder=True))
+    layout = backend._spatial_layout(grid, tokens)
+    key = (2, 1, tokens, 2, 128, cuda_device, layout.signature)
+
+    def no_permute(*args, **kwargs):
+        raise AssertionError("a dense-dispatched state must not permute tokens")
+
+    monkeypatch.setattr(type(layout), "reorder_qkv", no_permute)
+    monkeypatch.setattr(type(layout), "restore", no_permute)
+    for step in (2, 3):
+        backend.state[key] = {"route": None, "block_mask": None, "step": 1, "dense": True,
+                              "keep": 0.7, "grid": grid, "layout": layout}
+        context.set_routing_context(attention_id=2, step=step, branch=1, grid=grid)
+        output = backend(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device))
+        expected, _ = A.block_sparse_attention(*(x.float().numpy() for x in (q, k, v)),
+                                               None, 128)
+        _assert_close(output.float().cpu().numpy(), expected)
+        assert backend.phase_counts["dense_dispatch"] == step - 1
+    assert key not in backend.state
+    assert backend.finished_routes == [{"keep": 0.7, "frontier_fraction": None, "dense": True}]
+
+
 def test_sampled_route_is_bit_exact_to_oracle_selection(backends, cuda_device):
     """The backend's route equals the oracle's prior+top-mass+sink on the same mass."""
     flex, context = backends
