@@ -198,6 +198,33 @@ def e2e_loop(device):
     context.reset_runtime_state()
     model(latents, 999.0, model.embed_text(text_cond), DenseBackend())  # warm-up
     torch.cuda.synchronize()
+
+    # The DiT's elementwise kernels at the loop's shape (57,600 x 1536 bf16):
+    # algorithmic bytes = read x (+ y) + write out, 2 B per element.
+    from dit_sparse_atten_amd import ops
+    timer = EventTimer()
+    c = model.config
+    x = torch.randn(1, 57600, c.dim, device=device, generator=gen).bfloat16()
+    y = torch.randn_like(x)
+    out = torch.empty_like(x)
+    mod = torch.randn(6, c.dim, device=device, generator=gen)
+    cos_sin = model._cos_sin((16, 45, 80))
+    blk = model.blocks[0]
+    elem = x.numel() * 2
+    kernels = {
+        "layernorm_modulate": (lambda: ops.layernorm_modulate(
+            x, shift=mod[0:1], scale=mod[1:2], out=out), 2 * elem),
+        "rmsnorm_rope": (lambda: ops.rmsnorm_rope(
+            x, blk["norm_q"], c.head_dim, cos_sin, out=out), 2 * elem + cos_sin.numel() * 4),
+        "gated_residual": (lambda: ops.gated_residual(x, y, gate=mod[2:3], out=out), 3 * elem),
+    }
+    dit_ops = {}
+    for name, (function, nbytes) in kernels.items():
+        function()
+        ms, _ = timer.time(function, 10)
+        dit_ops[name] = {"ms": round(ms, 4), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3)}
+    del x, y, out
     runs = {}
     for name, backend in (("dense", DenseBackend()), ("flex_hybrid_0.58", hybrid(0.58)),
                           ("flex_no_dense_dispatch", hybrid(None))):
@@ -230,6 +257,7 @@ def e2e_loop(device):
                         "init, latents 16x16x90x160 -> 57,600 tokens, 5 steps x CFG pair, "
                         "text 512x4096",
             "runs": runs,
+            "dit_kernels_57600x1536": dit_ops,
             "reference_published": {
                 "device": "PPU-ZW810E (reference's own run, Wan2.1-14B, 40 layers)",
                 "dense_model_forward_s": 406.6, "flex_hybrid_0.58_model_forward_s": 386.9,

@@ -615,7 +615,31 @@ def _f32_or_none(name, t, device):
         raise ValueError(f"{name} must be float32")
     if t.device != device:
         raise ValueError(f"{name} must live on the tensor's device")
-    return t.contiguous()
+    t = t.contiguous()
+    # The kernels read parameter vectors with 16-byte loads.
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _out_rows(out, x, rows, dim):
+    """A [rows, dim] view of the caller's output tensor (or a new one)."""
+    if out is None:
+        return torch.empty((rows, dim), dtype=torch.bfloat16, device=x.device)
+    if out.dtype != torch.bfloat16 or out.device != x.device or out.shape != x.shape:
+        raise ValueError("out must be a bfloat16 tensor of x's shape on x's device")
+    try:
+        return out.view(rows, dim)
+    except RuntimeError as exc:
+        raise ValueError("out must be viewable as [rows, dim] rows") from exc
+
+
+def _row_groups(name, t, rows, dim):
+    """Rows per group of a per-group fp32 parameter [groups, dim]."""
+    if t.numel() % dim or t.shape[-1] != dim:
+        raise ValueError(f"{name} must be [groups, {dim}]")
+    groups = t.numel() // dim
+    if rows % groups:
+        raise ValueError(f"{name} has {groups} groups, which do not divide {rows} rows")
+    return rows // groups
 
 
 def layernorm_modulate(x, shift=None, scale=None, weight=None, bias=None, eps=1e-6, out=None):
@@ -626,15 +650,21 @@ def layernorm_modulate(x, shift=None, scale=None, weight=None, bias=None, eps=1e
     rows, dim = flat.shape
     weight, bias, shift, scale = (_f32_or_none(n, t, x.device) for n, t in (
         ("weight", weight), ("bias", bias), ("shift", shift), ("scale", scale)))
-    per_group = rows // (scale.numel() // dim) if scale is not None else rows
-    out = torch.empty_like(flat) if out is None else out.reshape(rows, dim)
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is not None and t.numel() != dim:
+            raise ValueError(f"{name} must hold {dim} values")
+    per_group = _row_groups("scale", scale, rows, dim) if scale is not None else rows
+    if shift is not None and (scale is None or shift.shape != scale.shape):
+        raise ValueError("shift needs a scale of the same shape")
+    rows_out = _out_rows(out, x, rows, dim)
     with torch.cuda.device(x.device):
         status = lib.dsa_layernorm_modulate(
             flat.data_ptr(), flat.stride(0), rows, dim,
             *[t.data_ptr() if t is not None else None for t in (weight, bias, shift, scale)],
-            per_group, float(eps), out.data_ptr(), out.stride(0), _stream_handle(x.device))
+            per_group, float(eps), rows_out.data_ptr(), rows_out.stride(0),
+            _stream_handle(x.device))
     _lib.check(status, "dsa_layernorm_modulate")
-    return out.reshape(x.shape)
+    return out if out is not None else rows_out.view(x.shape)
 
 
 def rmsnorm_rope(x, weight, head_dim=128, cos_sin=None, eps=1e-6, out=None):
@@ -646,14 +676,18 @@ def rmsnorm_rope(x, weight, head_dim=128, cos_sin=None, eps=1e-6, out=None):
     weight = _f32_or_none("weight", weight, x.device)
     cos_sin = _f32_or_none("cos_sin", cos_sin, x.device)
     tokens = x.shape[-2] if x.ndim >= 2 else rows
-    out = torch.empty_like(flat) if out is None else out.reshape(rows, dim)
+    if weight.numel() != dim:
+        raise ValueError(f"weight must hold {dim} values")
+    if cos_sin is not None and cos_sin.numel() != tokens * head_dim:
+        raise ValueError(f"cos_sin must be [{tokens}, {head_dim // 2}, 2]")
+    rows_out = _out_rows(out, x, rows, dim)
     with torch.cuda.device(x.device):
         status = lib.dsa_rmsnorm_rope(
             flat.data_ptr(), flat.stride(0), rows, dim, head_dim, weight.data_ptr(),
             cos_sin.data_ptr() if cos_sin is not None else None, tokens, float(eps),
-            out.data_ptr(), out.stride(0), _stream_handle(x.device))
+            rows_out.data_ptr(), rows_out.stride(0), _stream_handle(x.device))
     _lib.check(status, "dsa_rmsnorm_rope")
-    return out.reshape(x.shape)
+    return out if out is not None else rows_out.view(x.shape)
 
 
 def gated_residual(x, y, gate=None, out=None):
@@ -665,12 +699,12 @@ def gated_residual(x, y, gate=None, out=None):
         raise ValueError("x and y must have the same shape")
     rows, dim = fx.shape
     gate = _f32_or_none("gate", gate, x.device)
-    per_group = rows // (gate.numel() // dim) if gate is not None else rows
-    out = torch.empty_like(fx) if out is None else out.reshape(rows, dim)
+    per_group = _row_groups("gate", gate, rows, dim) if gate is not None else rows
+    rows_out = _out_rows(out, x, rows, dim)
     with torch.cuda.device(x.device):
         status = lib.dsa_gated_residual(
             fx.data_ptr(), fx.stride(0), fy.data_ptr(), fy.stride(0),
             gate.data_ptr() if gate is not None else None, rows, dim, per_group,
-            out.data_ptr(), out.stride(0), _stream_handle(x.device))
+            rows_out.data_ptr(), rows_out.stride(0), _stream_handle(x.device))
     _lib.check(status, "dsa_gated_residual")
-    return out.reshape(x.shape)
+    return out if out is not None else rows_out.view(x.shape)

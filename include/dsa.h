@@ -241,7 +241,8 @@ int dsa_permute_rows(int32_t tensors, const void* const* src, void* const* dst,
  * end-to-end denoising loop (the reference runs it through Diffusers'
  * WanTransformerBlock, wan_diffusers.py:75-191).  Rows are bf16 [rows, dim]
  * (dim a multiple of 8, <= 8192; row strides in elements; 16-byte aligned);
- * arithmetic in fp32; in-place use (out == x) is allowed.
+ * fp32 parameter vectors 16-byte aligned; arithmetic in fp32; in-place use
+ * (out == x) is allowed.  One wave per row, 16 rows per workgroup.
  *
  * dsa_layernorm_modulate: out = LN(x) [* weight + bias] [* (1 + scale) + shift]
  *   (LayerNorm without or with affine; shift/scale fp32 [groups, dim], row r

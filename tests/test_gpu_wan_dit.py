@@ -71,6 +71,41 @@ def test_gated_residual_matches_torch(ops, cuda_device):
     torch.testing.assert_close(z.float(), x.float() + y.float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dim", [8, 520, 1536, 5120, 8192])
+def test_row_kernels_every_chunk_count_in_place(ops, cuda_device, dim):
+    """Each chunk-count instantiation (dim / 512 rounded up: 1, 2, 3, 16 with
+    bounds), a row count that leaves the last workgroup partial, two groups,
+    and in-place output."""
+    gen = torch.Generator(device=cuda_device).manual_seed(dim)
+    rows_per_group, groups, head_dim = 37, 2, 8
+    x = torch.randn(groups, rows_per_group, dim, device=cuda_device, generator=gen).bfloat16()
+    y = torch.randn_like(x)
+    shift, scale, gate = (torch.randn(groups, dim, device=cuda_device, generator=gen) * 0.1
+                          for _ in range(3))
+    weight = 1 + torch.randn(dim, device=cuda_device, generator=gen) * 0.1
+    angles = torch.rand(rows_per_group, head_dim // 2, device=cuda_device, generator=gen) * 6
+    cos_sin = torch.stack([angles.cos(), angles.sin()], dim=-1).contiguous()
+
+    ln = F.layer_norm(x.float(), (dim,), eps=1e-6) * (1 + scale[:, None]) + shift[:, None]
+    z = x.clone()
+    ops.layernorm_modulate(z, shift=shift, scale=scale, out=z)
+    torch.testing.assert_close(z.float(), ln, atol=2e-2, rtol=1e-2)
+
+    xf = x.float()
+    normed = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * weight
+    pairs = normed.view(groups, rows_per_group, dim // head_dim, head_dim // 2, 2)
+    c, s = cos_sin[None, :, None, :, 0], cos_sin[None, :, None, :, 1]
+    rotated = torch.stack([pairs[..., 0] * c - pairs[..., 1] * s,
+                           pairs[..., 0] * s + pairs[..., 1] * c], dim=-1).reshape(x.shape)
+    z = x.clone()
+    ops.rmsnorm_rope(z, weight, head_dim, cos_sin, out=z)
+    torch.testing.assert_close(z.float(), rotated, atol=2e-2, rtol=1e-2)
+
+    z = x.clone()
+    ops.gated_residual(z, y, gate, out=z)
+    torch.testing.assert_close(z.float(), xf + gate[:, None] * y.float(), atol=2e-2, rtol=1e-2)
+
+
 def _small_config():
     from dit_sparse_atten_amd.wan_dit import WanDiTConfig
     return WanDiTConfig(layers=2, dim=256, heads=2, ffn_dim=512, text_dim=64, freq_dim=32)
