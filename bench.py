@@ -49,6 +49,9 @@ def parse_args():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-e2e", action="store_true",
                         help="skip the end-to-end denoising loop (BASELINE config 4)")
+    parser.add_argument("--only-e2e", action="store_true",
+                        help="run only the end-to-end denoising loop and print its JSON "
+                             "(profiling runs)")
     parser.add_argument("--only-sparse", action="store_true",
                         help="time only the sparse call (profiling runs)")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -283,6 +286,9 @@ def main():
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.only_e2e:
+        print(json.dumps({"e2e": e2e_loop(device)}), flush=True)
+        return
     q, k, v = clustered_inputs(device)
     route = bernoulli_route(device)
     csr = ops.route_to_csr(route)
