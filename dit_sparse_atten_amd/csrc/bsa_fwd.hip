@@ -28,6 +28,8 @@
 //  * online softmax with a lazily moved reference max (rescale only when a
 //    score exceeds it by 2^8); row sums add the fp32 P in plain VALU adds
 //    (v_dot2 would contend with the matrix core for issue).
+#include <type_traits>
+
 #include "bsa_tiles.h"
 
 namespace {
@@ -121,7 +123,9 @@ __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restr
 
 // kRouted: key blocks from the CSR row (false: every key block, dense).
 // kNh: 64-key half-tiles per key block (2 for blocks of 65..128 keys, else 1).
-template <bool kRouted, int kNh>
+// kSkip: some half-tile of every block holds at most 32 valid keys (block
+// sizes 65..96, or at most 32), so those steps run one 32-key sub-tile.
+template <bool kRouted, int kNh, bool kSkip>
 __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf16* vt,
                                                           int32_t vt_keys) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
@@ -215,32 +219,37 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
 
-  auto compute = [&](const unsigned char* kt_lds, const unsigned char* vt_lds, int valid) {
-    dsa_f32x16 sacc[2];
+  // NKT: 32-key sub-tiles of the half-tile that hold valid keys (2, or 1 when
+  // at most 32 are valid: the last half of a 65..96-key block, or a block of
+  // at most 32 keys), so empty sub-tiles cost neither MFMAs nor softmax work.
+  auto compute = [&](const unsigned char* kt_lds, const unsigned char* vt_lds, int valid,
+                     auto nkt_c) __attribute__((always_inline)) {
+    constexpr int NKT = decltype(nkt_c)::value;
+    dsa_f32x16 sacc[NKT];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
 #pragma unroll
     for (int dc = 0; dc < 8; ++dc) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+      for (int kt = 0; kt < NKT; ++kt) {
         const int row = kt * 32 + qi;
         const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
             kt_lds + row * kRowBytes + k2_swz(row, dc * 2 + g) * 16);
         sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], sacc[kt], 0, 0, 0);
       }
     }
-    if (valid < kHalfKeys) {
+    if (valid < NKT * 32) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if (kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= valid) sacc[kt][r] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -256,10 +265,10 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    dsa_bf16x8 pf[4];
+    dsa_bf16x8 pf[2 * NKT];
     float sum0 = 0.f, sum1 = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2 * NKT; ++j) {
       const int kt = j >> 1, hf = j & 1;
 #pragma unroll
       for (int t = 0; t < 8; t += 2) {
@@ -277,7 +286,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     }
     l_run += sum0 + sum1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2 * NKT; ++j) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         const int d = dt * 32 + qi;
@@ -289,32 +298,44 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
   };
 
   // One pipelined step: wait for the current stage, prefetch the next
-  // half-tile (next_kb == -2: none), then compute on the current one.
+  // half-tile (next_kb == -2: none), then compute on the current one
+  // (skip_c: this step may hold at most 32 valid keys).
   auto step = [&](int kb, int half, int next_kb, int next_half, const unsigned char* kc,
-                  const unsigned char* vc, unsigned char* kn, unsigned char* vn) {
+                  const unsigned char* vc, unsigned char* kn, unsigned char* vn,
+                  auto skip_c) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     if (next_kb != -2) issue(next_kb, next_half, kn, vn);
-    if (wave_active) compute(kc, vc, valid_of(kb, half));
+    if (wave_active) {
+      const int valid = valid_of(kb, half);
+      if (decltype(skip_c)::value && valid <= 32)
+        compute(kc, vc, valid, std::integral_constant<int, 1>{});
+      else
+        compute(kc, vc, valid, std::integral_constant<int, 2>{});
+    }
   };
+  const std::bool_constant<false> no_skip;
+  const std::bool_constant<kSkip> may_skip;
 
   if (nblk > 0) {
     int kb = block_of(0);
     issue(kb, 0, lds_k0, lds_v0);
     if (kNh == 2) {
+      // The first half of a 65..128-key block always holds 64 keys (short
+      // only at the sequence end, which the masked two-sub-tile path covers).
       for (int j = 0; j < nblk; ++j) {
         const int kb_after = j + 1 < nblk ? block_of(j + 1) : -2;
-        step(kb, 0, kb, 1, lds_k0, lds_v0, lds_k1, lds_v1);
-        step(kb, 1, kb_after, 0, lds_k1, lds_v1, lds_k0, lds_v0);
+        step(kb, 0, kb, 1, lds_k0, lds_v0, lds_k1, lds_v1, no_skip);
+        step(kb, 1, kb_after, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip);
         kb = kb_after;
       }
     } else {
       for (int j = 0; j < nblk; j += 2) {
         const int kb1 = j + 1 < nblk ? block_of(j + 1) : -2;
-        step(kb, 0, kb1, 0, lds_k0, lds_v0, lds_k1, lds_v1);
+        step(kb, 0, kb1, 0, lds_k0, lds_v0, lds_k1, lds_v1, may_skip);
         if (kb1 == -2) break;
         const int kb2 = j + 2 < nblk ? block_of(j + 2) : -2;
-        step(kb1, 0, kb2, 0, lds_k1, lds_v1, lds_k0, lds_v0);
+        step(kb1, 0, kb2, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip);
         kb = kb2;
       }
     }
@@ -445,13 +466,18 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
                      block_size, nh, vt_keys);
   const dim3 blocks((unsigned)grid), threads(256);
   const __bf16* vtc = vt;
-  if (row_ptr && nh == 2)
-    hipLaunchKernelGGL((bsa_fwd_kernel<true, 2>), blocks, threads, 0, stream, p, vtc, vt_keys);
-  else if (row_ptr)
-    hipLaunchKernelGGL((bsa_fwd_kernel<true, 1>), blocks, threads, 0, stream, p, vtc, vt_keys);
-  else if (nh == 2)
-    hipLaunchKernelGGL((bsa_fwd_kernel<false, 2>), blocks, threads, 0, stream, p, vtc, vt_keys);
-  else
-    hipLaunchKernelGGL((bsa_fwd_kernel<false, 1>), blocks, threads, 0, stream, p, vtc, vt_keys);
+  // Blocks whose last half-tile holds 1..32 keys run it as one sub-tile.
+  const int rem = block_size % kHalfKeys;
+  const bool skip = rem != 0 && rem <= 32;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p, vtc, vt_keys);
+  };
+  if (row_ptr) {
+    if (nh == 2) skip ? launch(bsa_fwd_kernel<true, 2, true>) : launch(bsa_fwd_kernel<true, 2, false>);
+    else skip ? launch(bsa_fwd_kernel<true, 1, true>) : launch(bsa_fwd_kernel<true, 1, false>);
+  } else {
+    if (nh == 2) skip ? launch(bsa_fwd_kernel<false, 2, true>) : launch(bsa_fwd_kernel<false, 2, false>);
+    else skip ? launch(bsa_fwd_kernel<false, 1, true>) : launch(bsa_fwd_kernel<false, 1, false>);
+  }
   return dsa::check_launch("dsa_bsa_fwd");
 }
