@@ -25,6 +25,7 @@
 #include <hip/hip_fp16.h>
 
 #include <cmath>
+#include <type_traits>
 
 namespace {
 
@@ -156,10 +157,14 @@ __global__ void __launch_bounds__(256, 2) tile_stats_kernel(TileStatsParams p) {
 
   float am = 0.f, aky = 0.f, akx = 0.f;
   // Accumulates one staged half-tile of key tile kt into the lane sums.
-  auto compute = [&](const unsigned char* cur, int half, int valid)
+  // NKK: 32-key sub-tiles holding valid keys (1 when at most 32 are valid);
+  // kFull: all 64 keys valid (no per-key mask).
+  auto compute = [&](const unsigned char* cur, int half, int valid, auto nkk_c, auto full_c)
                      __attribute__((always_inline)) {
+    constexpr int NKK = decltype(nkk_c)::value;
+    constexpr bool kFull = decltype(full_c)::value;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < NKK; ++kk) {
       dsa_f32x16 sacc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
@@ -181,7 +186,7 @@ __global__ void __launch_bounds__(256, 2) tile_stats_kernel(TileStatsParams p) {
         for (int e = 0; e < 4; ++e) {
           const int key_in_half = kk * 32 + 8 * quad + 4 * g + e;
           float pv = __builtin_amdgcn_exp2f(fmaf(sacc[quad * 4 + e], p.scale_log2, -lse2));
-          pv = key_in_half < valid ? pv : 0.f;
+          if (!kFull) pv = key_in_half < valid ? pv : 0.f;
           am += pv;
           aky = fmaf(pv, ky[e], aky);
           akx = fmaf(pv, kx[e], akx);
@@ -228,7 +233,12 @@ __global__ void __launch_bounds__(256, 2) tile_stats_kernel(TileStatsParams p) {
         valid = min(kHalfKeys, p.tile - half * kHalfKeys);
         valid = min(valid, p.tokens - (kt * p.tile + half * kHalfKeys));
       }
-      compute((sidx & 1) ? lds_k1 : lds_k0, half, valid);
+      const unsigned char* cur = (sidx & 1) ? lds_k1 : lds_k0;
+      using one = std::integral_constant<int, 1>;
+      using two = std::integral_constant<int, 2>;
+      if (valid == kHalfKeys) compute(cur, half, valid, two{}, std::true_type{});
+      else if (valid > 32) compute(cur, half, valid, two{}, std::false_type{});
+      else compute(cur, half, valid, one{}, std::false_type{});
     }
     if (half == kNh - 1) {
       end_tile(j);
