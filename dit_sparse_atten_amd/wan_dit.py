@@ -17,8 +17,8 @@ model's shape so the same loop runs here:
     classifier-free-guidance pair per step (branch 0 conditional, branch 1
     unconditional); the update is a plain Euler step, where Wan uses a
     multistep solver: the model calls, which are what is timed, are the same.
-GEMMs go through torch (hipBLASLt); the norms, modulation, RoPE and residuals
-are libdsa HIP kernels; self-attention is whatever backend the caller passes,
+GEMMs go through torch (hipBLASLt, the FFN's GELU-tanh in the GEMM epilogue);
+the norms, modulation, RoPE and residuals are libdsa HIP kernels; self-attention is whatever backend the caller passes,
 cross-attention is the dense libdsa kernel.  The routing context (layer,
 step, branch, grid) is set before every self-attention call, as the
 reference's context hooks do (context.py:43-49).
@@ -164,9 +164,11 @@ class WanDiT:
         attn = ops.bsa_fwd(q.view(shape), k.view(ctx_shape), v.view(ctx_shape))
         x = ops.gated_residual(x, F.linear(attn.reshape(batch, tokens, c.dim), *blk["co"]),
                                out=x)
-        # Feed-forward.
+        # Feed-forward; the GELU-tanh runs in the GEMM's epilogue (hipBLASLt).
         h = ops.layernorm_modulate(x, shift=mod[3:4], scale=mod[4:5], eps=c.eps)
-        f = F.linear(F.gelu(F.linear(h, *blk["ffn1"]), approximate="tanh"), *blk["ffn2"])
+        w1, b1 = blk["ffn1"]
+        f = torch._addmm_activation(b1, h.view(-1, c.dim), w1.t(), use_gelu=True)
+        f = F.linear(f, *blk["ffn2"]).view(batch, tokens, c.dim)
         return ops.gated_residual(x, f, gate=mod[5:6], out=x)
 
     def forward(self, latents, timestep, ctx, backend, step=0, branch=0):
