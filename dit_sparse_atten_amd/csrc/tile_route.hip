@@ -2,7 +2,7 @@
 // the next-step expansion policies.
 //
 // Replaces attention_backends/sparse.py:
-//   _drop_low_mass + _preserve_one_per_row  339-348, 327-336  -> head_mean + drop_kernel
+//   _drop_low_mass + _preserve_one_per_row  339-348, 327-336  -> head stats + drop_kernel
 //   first-frame sink of the next mask      883-884
 //   _expand "all" / "directional"          350-373 (+ _spatial_neighbors 258-276,
 //                                          _apply_directional_steps 285-324)
@@ -35,21 +35,38 @@ __device__ __forceinline__ float load_mass(const void* mass, int is_f16, int64_t
                 : static_cast<const float*>(mass)[i];
 }
 
-// Per head: exact sum of the selected mass (rounded once to fp32) and the
-// number of selected cells.  One 256-thread workgroup per head.
-__global__ void __launch_bounds__(256) head_mean_kernel(const uint8_t* mask, const void* mass,
-                                                       int is_f16, int32_t cells,
-                                                       float* head_sum, int32_t* head_count) {
+// Per head: exact fixed-point sum of the selected mass and the number of
+// selected cells.  The head's cells split into chunks of kHeadChunk, one
+// workgroup each; integer sums are exact, so the atomic adds of the
+// workgroup partials give the same total in any order.  Readers round the
+// total once to fp32 (fixed_to_f32).  `acc` / `cnt` start at zero
+// (head_zero_kernel).
+constexpr int kHeadChunk = 16384;
+
+__global__ void __launch_bounds__(256) head_zero_kernel(unsigned long long* acc, int32_t* cnt,
+                                                       int32_t heads) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < heads) {
+    acc[i] = 0ull;
+    cnt[i] = 0;
+  }
+}
+
+__global__ void __launch_bounds__(256) head_partial_kernel(const uint8_t* mask, const void* mass,
+                                                          int is_f16, int32_t cells,
+                                                          unsigned long long* acc, int32_t* cnt) {
   __shared__ int64_t wsum[4];
   __shared__ int32_t wcnt[4];
-  const int h = blockIdx.x;
+  const int h = blockIdx.y;
   const int tid = threadIdx.x;
-  const uint8_t* m = mask + (int64_t)h * cells;
+  const int c0 = blockIdx.x * kHeadChunk;
+  const int c1 = min(c0 + kHeadChunk, cells);
+  const int64_t base = (int64_t)h * cells;
   int64_t s = 0;
   int32_t c = 0;
-  for (int i = tid; i < cells; i += 256) {
-    if (m[i]) {
-      const float v = load_mass(mass, is_f16, (int64_t)h * cells + i);
+  for (int i = c0 + tid; i < c1; i += 256) {
+    if (mask[base + i]) {
+      const float v = load_mass(mass, is_f16, base + i);
       s += to_fixed(v > 0.f ? v : 0.f);
       ++c;
     }
@@ -62,15 +79,38 @@ __global__ void __launch_bounds__(256) head_mean_kernel(const uint8_t* mask, con
   }
   dsa::lds_barrier();
   if (tid == 0) {
-    head_sum[h] = fixed_to_f32((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]));
-    head_count[h] = (wcnt[0] + wcnt[1]) + (wcnt[2] + wcnt[3]);
+    const int64_t total = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    const int32_t count = (wcnt[0] + wcnt[1]) + (wcnt[2] + wcnt[3]);
+    if (total) atomicAdd(&acc[h], (unsigned long long)total);
+    if (count) atomicAdd(&cnt[h], count);
   }
+}
+
+// head_scratch (float[4 * heads], 8-byte aligned) holds the per-head int64
+// fixed-point sums, then the int32 counts.
+struct HeadStats {
+  unsigned long long* acc;
+  int32_t* cnt;
+};
+
+HeadStats head_stats_of(float* head_scratch, int32_t heads) {
+  return {reinterpret_cast<unsigned long long*>(head_scratch),
+          reinterpret_cast<int32_t*>(head_scratch + 2 * heads)};
+}
+
+void launch_head_stats(const uint8_t* mask, const void* mass, int is_f16, int32_t heads,
+                       int32_t cells, HeadStats hs, hipStream_t stream) {
+  hipLaunchKernelGGL(head_zero_kernel, dim3((unsigned)((heads + 255) / 256)), dim3(256), 0,
+                     stream, hs.acc, hs.cnt, heads);
+  const dim3 grid((unsigned)((cells + kHeadChunk - 1) / kHeadChunk), (unsigned)heads);
+  hipLaunchKernelGGL(head_partial_kernel, grid, dim3(256), 0, stream, mask, mass, is_f16, cells,
+                     hs.acc, hs.cnt);
 }
 
 struct DropParams {
   const uint8_t* mask;
   const void* mass;
-  const float* head_sum;
+  const unsigned long long* head_acc;  // exact fixed-point selected-mass sums
   const int32_t* head_count;
   uint8_t* out;
   int32_t* counts;
@@ -87,14 +127,15 @@ __global__ void __launch_bounds__(256) drop_kernel(DropParams p) {
   const int K = p.tiles;
   const int64_t base = (int64_t)row * K;
   const int count = max(p.head_count[h], 1);
+  const float head_sum = fixed_to_f32((int64_t)p.head_acc[h]);
   float mean;
   float drop = p.drop;
   if (p.is_f16) {
-    const float sum16 = __half2float(__float2half(p.head_sum[h]));
+    const float sum16 = __half2float(__float2half(head_sum));
     mean = __half2float(__float2half(sum16 / (float)count));
     drop = __half2float(__float2half(p.drop));
   } else {
-    mean = fmaxf(p.head_sum[h] / (float)count, 1e-12f);
+    mean = fmaxf(head_sum / (float)count, 1e-12f);
   }
   auto kept_at = [&](int k, float& m) -> bool {
     m = load_mass(p.mass, p.is_f16, base + k);
@@ -155,7 +196,7 @@ struct ExpandParams {
   const __half* cqx;
   const __half* cky;
   const __half* ckx;
-  const float* head_sum;
+  const unsigned long long* head_acc;  // exact fixed-point sums (directional only)
   const int32_t* head_count;
   uint8_t* out;
   int32_t heads, tiles, frames, blocks_h, blocks_w, policy;
@@ -198,7 +239,7 @@ __global__ void __launch_bounds__(256) expand_kernel(ExpandParams p) {
   bool huge = p.policy == kPolicyAll;
   if (p.policy == kPolicyDirectional) {
     const float count = (float)max(p.head_count[h], 1);
-    const float mean = fmaxf(p.head_sum[h] / count, 1e-12f);
+    const float mean = fmaxf(fixed_to_f32((int64_t)p.head_acc[h]) / count, 1e-12f);
     huge = __half2float(p.mass[idx]) / mean >= p.huge;
   }
   if (huge) {
@@ -238,11 +279,11 @@ extern "C" int dsa_drop_low_mass(const uint8_t* mask, const void* mass, int32_t 
   if (!(drop_factor > 0.f))
     return dsa::set_error(DSA_EINVAL, "dsa_drop_low_mass: drop_factor must be positive "
                                       "(a non-positive factor keeps the mask unchanged)");
-  float* head_sum = head_scratch;
-  int32_t* head_count = reinterpret_cast<int32_t*>(head_scratch + heads);
-  hipLaunchKernelGGL(head_mean_kernel, dim3((unsigned)heads), dim3(256), 0, stream, mask, mass,
-                     mass_is_f16 ? 1 : 0, tiles * tiles, head_sum, head_count);
-  DropParams p{mask, mass, head_sum, head_count, out, counts, heads, tiles,
+  if (reinterpret_cast<uintptr_t>(head_scratch) % 8 != 0)
+    return dsa::set_error(DSA_EINVAL, "dsa_drop_low_mass: head_scratch must be 8-byte aligned");
+  const HeadStats hs = head_stats_of(head_scratch, heads);
+  launch_head_stats(mask, mass, mass_is_f16 ? 1 : 0, heads, tiles * tiles, hs, stream);
+  DropParams p{mask, mass, hs.acc, hs.cnt, out, counts, heads, tiles,
                sink_tiles < 0 ? 0 : sink_tiles, mass_is_f16 ? 1 : 0, drop_factor};
   hipLaunchKernelGGL(drop_kernel, dim3((unsigned)(((int64_t)heads * tiles + 3) / 4)), dim3(256),
                      0, stream, p);
@@ -275,11 +316,11 @@ extern "C" int dsa_expand_route(const uint8_t* mask, const void* mass_f16,
   const int64_t n = (int64_t)heads * tiles * tiles;
   hipLaunchKernelGGL(copy_bytes_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                      mask, out, n);
-  float* head_sum = head_scratch;
-  int32_t* head_count = head_scratch ? reinterpret_cast<int32_t*>(head_scratch + heads) : nullptr;
+  if (head_scratch && reinterpret_cast<uintptr_t>(head_scratch) % 8 != 0)
+    return dsa::set_error(DSA_EINVAL, "dsa_expand_route: head_scratch must be 8-byte aligned");
+  const HeadStats hs = head_scratch ? head_stats_of(head_scratch, heads) : HeadStats{nullptr, nullptr};
   if (policy == kPolicyDirectional)
-    hipLaunchKernelGGL(head_mean_kernel, dim3((unsigned)heads), dim3(256), 0, stream, mask,
-                       mass_f16, 1, tiles * tiles, head_sum, head_count);
+    launch_head_stats(mask, mass_f16, 1, heads, tiles * tiles, hs, stream);
   ExpandParams p;
   p.mask = mask;
   p.mass = static_cast<const __half*>(mass_f16);
@@ -287,8 +328,8 @@ extern "C" int dsa_expand_route(const uint8_t* mask, const void* mass_f16,
   p.cqx = static_cast<const __half*>(centroid_q_x);
   p.cky = static_cast<const __half*>(centroid_k_y);
   p.ckx = static_cast<const __half*>(centroid_k_x);
-  p.head_sum = head_sum;
-  p.head_count = head_count;
+  p.head_acc = hs.acc;
+  p.head_count = hs.cnt;
   p.out = out;
   p.heads = heads;
   p.tiles = tiles;

@@ -439,7 +439,7 @@ def drop_low_mass(mask, mass, drop_factor, sink_tiles=0):
     mass = mass.contiguous()
     out = torch.empty_like(mask)
     counts = torch.empty((heads, tiles), dtype=torch.int32, device=mask.device)
-    scratch = torch.empty(2 * heads, dtype=torch.float32, device=mask.device)
+    scratch = torch.empty(4 * heads, dtype=torch.float32, device=mask.device)
     with torch.cuda.device(mask.device):
         status = lib.dsa_drop_low_mass(
             mask.data_ptr(), mass.data_ptr(), int(mass.dtype == torch.float16), heads, tiles,
@@ -475,7 +475,7 @@ def expand_route(mask, grid_tiles, policy, mass=None, centroids=None, centroid_t
                 raise ValueError("directional expansion needs fp16 mass and centroids")
         tensors = [tensor.contiguous() for tensor in tensors]
         pointers = [tensor.data_ptr() for tensor in tensors]
-        scratch = torch.empty(2 * heads, dtype=torch.float32, device=mask.device)
+        scratch = torch.empty(4 * heads, dtype=torch.float32, device=mask.device)
     out = torch.empty_like(mask)
     with torch.cuda.device(mask.device):
         status = lib.dsa_expand_route(

@@ -177,7 +177,7 @@ int dsa_directional_update(const float* mass, const uint8_t* previous,
  * (attention_backends/sparse.py:327-348) and the sink of sparse.py:883-884.
  *   mask, out: [heads, tiles, tiles] bytes; mass: the same shape, fp16
  *   (mass_is_f16 = 1, the reference's stored route mass) or fp32 (0);
- *   drop_factor > 0; head_scratch: device float[2 * heads];
+ *   drop_factor > 0; head_scratch: device float[4 * heads], 8-byte aligned;
  *   counts: [heads, tiles] entries set per output row.
  */
 int dsa_drop_low_mass(const uint8_t* mask, const void* mass, int32_t mass_is_f16, int32_t heads,
@@ -194,7 +194,7 @@ int dsa_drop_low_mass(const uint8_t* mask, const void* mass, int32_t mass_is_f16
  * `_apply_directional_steps` 285-324).  Tiles are numbered frame-major over
  * frames x blocks_h x blocks_w; mask, out: [heads, tiles, tiles] bytes;
  * mass_f16 and the centroids: fp16 of the same shape (directional only);
- * head_scratch: device float[2 * heads] (directional only).
+ * head_scratch: device float[4 * heads], 8-byte aligned (directional only).
  */
 int dsa_expand_route(const uint8_t* mask, const void* mass_f16, const void* centroid_q_y,
                      const void* centroid_q_x, const void* centroid_k_y,
