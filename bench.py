@@ -183,7 +183,7 @@ def e2e_loop(device):
     from dit_sparse_atten_amd.attention_backends import context
     from dit_sparse_atten_amd.attention_backends.dense import DenseBackend
     from dit_sparse_atten_amd.attention_backends.flex import FlexReuseBackend, FlexReuseConfig
-    from dit_sparse_atten_amd.wan_dit import WanDiT, denoise
+    from dit_sparse_atten_amd.wan_dit import WanDiT, WanDiTConfig, denoise
 
     model = WanDiT(device=device, seed=11)
     gen = torch.Generator(device=device).manual_seed(12)
@@ -228,38 +228,56 @@ def e2e_loop(device):
         dit_ops[name] = {"ms": round(ms, 4), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                          "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3)}
     del x, y, out
-    runs = {}
-    for name, backend in (("dense", DenseBackend()), ("flex_hybrid_0.58", hybrid(0.58)),
-                          ("flex_no_dense_dispatch", hybrid(None))):
+    def run_loops(model, named_backends):
+        runs = {}
+        for name, backend in named_backends:
+            context.reset_runtime_state()
+            marks = []
+
+            def on_call(step, branch, phase):
+                event = torch.cuda.Event(enable_timing=True)
+                event.record()
+                marks.append(event)
+
+            denoise(model, backend, latents, text_cond, text_uncond, steps=5, on_call=on_call)
+            torch.cuda.synchronize()
+            calls = [marks[i].elapsed_time(marks[i + 1]) for i in range(0, len(marks), 2)]
+            entry = {"model_forward_ms": round(sum(calls), 1),
+                     "forward_ms_per_call": [round(t, 1) for t in calls]}
+            if hasattr(backend, "profile_summary"):
+                summary = backend.profile_summary()
+                entry["phase_counts"] = summary["phase_counts"]
+                keep = summary["mean_route_keep"]
+                entry["mean_route_keep"] = None if keep is None else round(float(keep), 4)
+                entry["dense_dispatched_routes"] = summary["dense_dispatched_routes"]
+            runs[name] = entry
+            print(f"e2e {name}: {entry['model_forward_ms']} ms", file=sys.stderr, flush=True)
+        dense_ms = runs["dense"]["model_forward_ms"]
+        for entry in runs.values():
+            entry["speedup_vs_dense"] = round(dense_ms / entry["model_forward_ms"], 3)
         context.reset_runtime_state()
-        marks = []
+        return runs
 
-        def on_call(step, branch, phase):
-            event = torch.cuda.Event(enable_timing=True)
-            event.record()
-            marks.append(event)
-
-        denoise(model, backend, latents, text_cond, text_uncond, steps=5, on_call=on_call)
-        torch.cuda.synchronize()
-        calls = [marks[i].elapsed_time(marks[i + 1]) for i in range(0, len(marks), 2)]
-        entry = {"model_forward_ms": round(sum(calls), 1),
-                 "forward_ms_per_call": [round(t, 1) for t in calls]}
-        if hasattr(backend, "profile_summary"):
-            summary = backend.profile_summary()
-            entry["phase_counts"] = summary["phase_counts"]
-            keep = summary["mean_route_keep"]
-            entry["mean_route_keep"] = None if keep is None else round(float(keep), 4)
-            entry["dense_dispatched_routes"] = summary["dense_dispatched_routes"]
-        runs[name] = entry
-        print(f"e2e {name}: {entry['model_forward_ms']} ms", file=sys.stderr, flush=True)
-    dense_ms = runs["dense"]["model_forward_ms"]
-    for entry in runs.values():
-        entry["speedup_vs_dense"] = round(dense_ms / entry["model_forward_ms"], 3)
-    context.reset_runtime_state()
+    runs = run_loops(model, (("dense", DenseBackend()), ("flex_hybrid_0.58", hybrid(0.58)),
+                             ("flex_no_dense_dispatch", hybrid(None))))
+    # Random projections give diffuse attention (every route at the 0.625 cap,
+    # so all dispatch dense at 0.58).  The same shape with a shared q/k bias and
+    # sharper q/k norms has spatially local attention, whose 0.95-mass routes
+    # keep about half the blocks, as the reference's trained-model run did.
+    del model
+    local_config = WanDiTConfig(qk_position_bias=1.0, qk_norm_scale=2.0)
+    local = WanDiT(local_config, device=device, seed=11)
+    local_runs = run_loops(local, (("dense", DenseBackend()),
+                                   ("flex_hybrid_0.58", hybrid(0.58))))
+    del local
     return {"workload": "Wan2.1-1.3B shape (30 layers, dim 1536, 12 heads, d=128), random "
                         "init, latents 16x16x90x160 -> 57,600 tokens, 5 steps x CFG pair, "
                         "text 512x4096",
             "runs": runs,
+            "local_attention_model": {
+                "config": "same shape and seed, qk_position_bias 1.0, qk_norm_scale 2.0 "
+                          "(synthetic spatial locality, not a trained model)",
+                "runs": local_runs},
             "dit_kernels_57600x1536": dit_ops,
             "reference_published": {
                 "device": "PPU-ZW810E (reference's own run, Wan2.1-14B, 40 layers)",

@@ -50,6 +50,14 @@ class WanDiTConfig:
     out_channels: int = 16
     patch: tuple = (1, 2, 2)
     eps: float = 1e-6
+    # > 0: every block's q and k projections share one random bias vector of
+    # this scale.  After RMSNorm and 3D RoPE its self-product depends only on
+    # the relative (frame, y, x) offset and peaks at zero, so attention gains
+    # the spatial locality of a trained video DiT.  0: plain random init.
+    qk_position_bias: float = 0.0
+    # Scale of the self-attention q/k RMSNorm weights (a softmax temperature:
+    # scores scale with its square).  1: the plain random init.
+    qk_norm_scale: float = 1.0
 
     @property
     def head_dim(self):
@@ -117,11 +125,16 @@ class WanDiT:
         self.time_proj = linear(6 * c.dim, c.dim)
         self.blocks = []
         for _ in range(c.layers):
+            q_proj, k_proj = linear(c.dim, c.dim), linear(c.dim, c.dim)
+            if c.qk_position_bias > 0:
+                shared = (randn(c.dim) * c.qk_position_bias).to(torch.bfloat16)
+                q_proj, k_proj = (q_proj[0], shared), (k_proj[0], shared)
             self.blocks.append({
                 "table": randn(6, c.dim) / math.sqrt(c.dim),
-                "q": linear(c.dim, c.dim), "k": linear(c.dim, c.dim),
+                "q": q_proj, "k": k_proj,
                 "v": linear(c.dim, c.dim), "o": linear(c.dim, c.dim),
-                "norm_q": vector(c.dim, offset=1.0), "norm_k": vector(c.dim, offset=1.0),
+                "norm_q": vector(c.dim, offset=1.0) * c.qk_norm_scale,
+                "norm_k": vector(c.dim, offset=1.0) * c.qk_norm_scale,
                 "cq": linear(c.dim, c.dim), "ck": linear(c.dim, c.dim),
                 "cv": linear(c.dim, c.dim), "co": linear(c.dim, c.dim),
                 "cnorm_q": vector(c.dim, offset=1.0), "cnorm_k": vector(c.dim, offset=1.0),
