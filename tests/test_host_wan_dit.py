@@ -28,3 +28,19 @@ def test_rope_table_matches_angles():
 def test_config_is_wan_1_3b_shape():
     c = WanDiTConfig()
     assert (c.layers, c.dim, c.heads, c.head_dim, c.ffn_dim) == (30, 1536, 12, 128, 8960)
+
+
+def test_local_attention_knobs_share_qk_bias_and_scale_norms():
+    """qk_position_bias ties one bias vector to every block's q and k
+    projections; qk_norm_scale multiplies the q/k RMSNorm weights."""
+    from dit_sparse_atten_amd.wan_dit import WanDiT
+    small = dict(layers=2, dim=64, heads=1, ffn_dim=64, text_dim=32, freq_dim=16)
+    plain = WanDiT(WanDiTConfig(**small), device="cpu", seed=3)
+    local = WanDiT(WanDiTConfig(**small, qk_position_bias=1.0, qk_norm_scale=2.0),
+                   device="cpu", seed=3)
+    for blk_plain, blk in zip(plain.blocks, local.blocks):
+        assert blk["q"][1] is blk["k"][1]
+        assert not torch.equal(blk_plain["q"][1], blk_plain["k"][1])
+        torch.testing.assert_close(blk["norm_q"].abs().mean() / blk_plain["norm_q"].abs().mean(),
+                                   torch.tensor(2.0), rtol=0.1, atol=0)
+    assert not torch.equal(local.blocks[0]["q"][1], local.blocks[1]["q"][1])
