@@ -207,3 +207,32 @@ def test_dense_backend_dtype_and_q_scale(cuda_device):
     expected, _ = A.block_sparse_attention(qs.float().numpy(), k.bfloat16().float().numpy(),
                                            v.bfloat16().float().numpy(), None, 128, scale=0.1)
     _assert_close(out.cpu().numpy(), expected)
+
+
+@pytest.mark.parametrize("name", ["dense", "flex_reuse", "sparse"])
+def test_diffusers_processor_call_pattern(cuda_device, name):
+    """wan_diffusers.py:52-68: [B,T,H,D] views of BHSD storage, the processor's
+    keywords (attention_mask included), output [B,T,H,D] in the caller's dtype;
+    infer.py:259-260 sets an attribute on the backend."""
+    from dit_sparse_atten_amd.attention_backends import BACKENDS, context
+    context.reset_runtime_state()
+    try:
+        backend = BACKENDS[name]()
+        backend.svg_operator_status = {"enabled": False}
+        grid = (2, 8, 16)
+        tokens, heads = math.prod(grid), 2
+        generator = torch.Generator().manual_seed(31)
+        storage = [torch.randn(1, heads, tokens, 128, generator=generator).bfloat16()
+                   for _ in range(3)]
+        q, k, v = (x.to(cuda_device).transpose(1, 2) for x in storage)
+        assert q.stride() == (heads * tokens * 128, 128, tokens * 128, 1)
+        # Layer 1, step 0: flex_reuse and sparse bootstrap (dense output + route).
+        context.set_routing_context(attention_id=1, step=0, branch=0, grid=grid)
+        out = backend(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
+                      window_size=(-1, -1), dtype=q.dtype, attention_mask=None)
+        assert out.shape == q.shape and out.dtype == q.dtype
+        expected, _ = A.block_sparse_attention(
+            *(x.transpose(1, 2).float().numpy() for x in storage), None, 128)
+        _assert_close(out.float().cpu().numpy(), expected)
+    finally:
+        context.reset_runtime_state()
