@@ -7,9 +7,12 @@ blocks with the diagonal and the 29 frame-0 sink blocks forced on.  A "step"
 is one call.  Also measured in the same run: the same call with a full route
 (dense fallback), the sampled route update of config 3 (16 samples/block,
 persistence 0.5 on a Bernoulli(0.625) previous route, target 0.95, cap
-ceil(450*0.625)=282, CSR build) and its ratio to the dense call, and the CPU
-baseline: the oracle's restatement of the reference's sparse.py path timed on
-a bounded row sample of the same workload on the host cores.
+ceil(450*0.625)=282, CSR build) and its ratio to the dense call, the layout
+gather/scatter, the exact route estimate, the matrix-sparse backend at 720p,
+the end-to-end denoising loop of config 4 (random-init Wan2.1-1.3B shape,
+dense vs the flex_reuse hybrid, plus a spatially-local-attention variant), and
+the CPU baseline: the oracle's restatement of the reference's sparse.py path
+timed on a bounded row sample of the same workload on the host cores.
 
 Prints one JSON line (rank 0).  Effective TFLOP/s counts kept blocks only:
 4 * d * sum over routed (q-block, k-block) pairs of valid_q * valid_k.
