@@ -239,7 +239,7 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
 
 // ---------------------------------------------------------------------------
 // Top-mass selection: one wave per (head, query-block) row, K <= 64 * kPer
-// (512 or 1024).
+// (512, 1024 or 2048).
 // ---------------------------------------------------------------------------
 
 struct SelectParams {
@@ -507,8 +507,8 @@ extern "C" int dsa_route_select(const float* mass, const uint8_t* previous, int3
   dsa::clear_error();
   if (!mass || !route || !counts) return dsa::set_error(DSA_EINVAL, "dsa_route_select: null pointer");
   if (rows <= 0 || keys <= 0) return dsa::set_error(DSA_EINVAL, "dsa_route_select: empty route");
-  if (keys > 1024)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_route_select: at most 1024 key blocks (got %d)",
+  if (keys > 2048)
+    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_route_select: at most 2048 key blocks (got %d)",
                           keys);
   if (!(target > 0.f && target <= 1.f))
     return dsa::set_error(DSA_EINVAL, "mass_target must be in (0, 1]");
@@ -528,8 +528,10 @@ extern "C" int dsa_route_select(const float* mass, const uint8_t* previous, int3
   const dim3 groups((unsigned)((rows + 3) / 4)), threads(256);
   if (keys <= 512)
     hipLaunchKernelGGL(route_select_kernel<8>, groups, threads, 0, stream, p);
-  else
+  else if (keys <= 1024)
     hipLaunchKernelGGL(route_select_kernel<16>, groups, threads, 0, stream, p);
+  else
+    hipLaunchKernelGGL(route_select_kernel<32>, groups, threads, 0, stream, p);
   return dsa::check_launch("dsa_route_select");
 }
 

@@ -1,5 +1,5 @@
 // Row arithmetic shared by the route kernels (gfx950): exact fixed-point row
-// sums and a one-wave bitonic sort of up to 1024 keys.
+// sums and a one-wave bitonic sort of up to 2048 keys.
 //
 // A row value m >= 0 is represented as the integer floor(m * 2^52), so row and
 // prefix sums are exact and independent of summation order; a sum is rounded
@@ -74,7 +74,5 @@ __device__ __forceinline__ void sort_desc(uint64_t key[kPer], int lane) {
     }
   }
 }
-
-__device__ __forceinline__ void sort512_desc(uint64_t key[8], int lane) { sort_desc<8>(key, lane); }
 
 }  // namespace dsa

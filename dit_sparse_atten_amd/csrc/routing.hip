@@ -164,40 +164,49 @@ __global__ void __launch_bounds__(256) dir_expand_kernel(DirParams p) {
   }
 }
 
-// Order-preserving image of a float (-0.0 taken as +0.0), key index below.
+// Order-preserving image of a float (-0.0 taken as +0.0), key index below
+// (kN - 1 - e in the low bits, so equal values order by ascending index).
+template <int kN>
 __device__ __forceinline__ uint64_t order_key(bool flag, float value, int e) {
   uint32_t bits = __float_as_uint(value == 0.f ? 0.f : value);
   bits = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-  return ((uint64_t)flag << 63) | ((uint64_t)bits << 31) | (uint32_t)(511 - e);
+  return ((uint64_t)flag << 63) | ((uint64_t)bits << 31) | (uint32_t)(kN - 1 - e);
 }
 
-__device__ __forceinline__ int key_index(uint64_t key) { return 511 - (int)(key & 511u); }
+template <int kN>
+__device__ __forceinline__ int key_index(uint64_t key) {
+  return kN - 1 - (int)(key & (uint64_t)(kN - 1));
+}
 
-// Scatters the first `count` sorted keys as flags into f[0..511] (LDS) and
-// returns this lane's eight flags e = lane * 8 + j.
-__device__ __forceinline__ void sorted_prefix_flags(const uint64_t key[8], int lane, int count,
+// Scatters the first `count` sorted keys as flags into f[0..kN) (LDS) and
+// returns this lane's kPer flags e = lane * kPer + j.
+template <int kPer>
+__device__ __forceinline__ void sorted_prefix_flags(const uint64_t key[kPer], int lane, int count,
                                                     bool need_flag_bit, uint8_t* f,
-                                                    bool out[8]) {
+                                                    bool out[kPer]) {
+  constexpr int kN = 64 * kPer;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) f[lane * 8 + j] = 0;
+  for (int j = 0; j < kPer; ++j) f[lane * kPer + j] = 0;
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int pos = lane * 8 + j;
-    if (pos < count && (!need_flag_bit || (key[j] >> 63))) f[key_index(key[j])] = 1;
+  for (int j = 0; j < kPer; ++j) {
+    const int pos = lane * kPer + j;
+    if (pos < count && (!need_flag_bit || (key[j] >> 63))) f[key_index<kN>(key[j])] = 1;
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
-  for (int j = 0; j < 8; ++j) out[j] = f[lane * 8 + j] != 0;
+  for (int j = 0; j < kPer; ++j) out[j] = f[lane * kPer + j] != 0;
   __builtin_amdgcn_wave_barrier();
 }
 
 // One wave per (head, query block): final candidates, exploration, scores
-// and the fixed-budget selection, then the sink columns.
+// and the fixed-budget selection, then the sink columns.  K <= 64 * kPer.
+template <int kPer>
 __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
-  __shared__ uint8_t flags[4][512];
+  constexpr int kN = 64 * kPer;
+  __shared__ uint8_t flags[4][kN];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + wave;
@@ -206,13 +215,13 @@ __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
   const int64_t base = (int64_t)row * K;
   uint8_t* f = flags[wave];
 
-  float m[8];
-  bool prev[8], cand[8], pool[8];
+  float m[kPer];
+  bool prev[kPer], cand[kPer], pool[kPer];
   int prev_count = 0, pool_count = 0;
   int64_t fixed_sum = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = lane * 8 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
     const bool in = e < K;
     m[j] = in ? p.mass[base + e] : 0.f;
     prev[j] = in && p.previous[base + e] != 0;
@@ -222,25 +231,25 @@ __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
     fixed_sum += in ? to_fixed(m[j] > 0.f ? m[j] : 0.f) : 0;
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = lane * 8 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
     if (e < K) p.candidates[base + e] = cand[j];
   }
 
-  uint64_t key[8];
+  uint64_t key[kPer];
   if (p.explore > 0) {
     // Highest-mass blocks outside the pool (pool blocks rank last, by index).
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane * 8 + j;
-      key[j] = e < K ? order_key(!pool[j], pool[j] ? 0.f : m[j], e) : 0ull;
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane * kPer + j;
+      key[j] = e < K ? order_key<kN>(!pool[j], pool[j] ? 0.f : m[j], e) : 0ull;
     }
-    dsa::sort512_desc(key, lane);
-    bool ex[8];
-    sorted_prefix_flags(key, lane, p.explore < K ? p.explore : K, false, f, ex);
+    dsa::sort_desc<kPer>(key, lane);
+    bool ex[kPer];
+    sorted_prefix_flags<kPer>(key, lane, p.explore < K ? p.explore : K, false, f, ex);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane * 8 + j;
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane * kPer + j;
       if (e < K) {
         if (p.exploration) p.exploration[base + e] = ex[j];
         pool[j] = pool[j] || ex[j];
@@ -248,14 +257,14 @@ __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
     }
   } else if (p.exploration) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane * 8 + j;
+    for (int j = 0; j < kPer; ++j) {
+      const int e = lane * kPer + j;
       if (e < K) p.exploration[base + e] = 0;
     }
   }
 
 #pragma unroll
-  for (int j = 0; j < 8; ++j) pool_count += pool[j];
+  for (int j = 0; j < kPer; ++j) pool_count += pool[j];
   pool_count = wave_sum_i32(pool_count);
   prev_count = wave_sum_i32(prev_count);
   fixed_sum = wave_sum_i64(fixed_sum);
@@ -268,21 +277,21 @@ __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
   count = count < 1 ? 1 : count;
 
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = lane * 8 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
     float score = m[j];
     if (prev[j]) score = score + prior;
     if (p.bonus != 0.f && cand[j]) score = score + bonus;
-    key[j] = e < K ? order_key(pool[j], pool[j] ? score : 0.f, e) : 0ull;
+    key[j] = e < K ? order_key<kN>(pool[j], pool[j] ? score : 0.f, e) : 0ull;
   }
-  dsa::sort512_desc(key, lane);
-  bool sel[8];
-  sorted_prefix_flags(key, lane, count, true, f, sel);
+  dsa::sort_desc<kPer>(key, lane);
+  bool sel[kPer];
+  sorted_prefix_flags<kPer>(key, lane, count, true, f, sel);
 
   int selected = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int e = lane * 8 + j;
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
     if (e < K) {
       const uint8_t on = (sel[j] || e < p.sink) ? 1 : 0;
       p.route[base + e] = on;
@@ -297,11 +306,14 @@ __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
 
 unsigned row_groups(int64_t rows) { return (unsigned)((rows + 3) / 4); }
 
+constexpr int kMaxBlocks = 2048;  // 64 lanes x 32 keys per selection wave
+
 int check_route_shape(const char* what, int32_t heads, int32_t blocks, const int32_t* nb) {
   if (heads <= 0 || blocks <= 0)
     return dsa::set_error(DSA_EINVAL, "%s: heads and blocks must be positive", what);
-  if (blocks > 512)
-    return dsa::set_error(DSA_EUNSUPPORTED, "%s: %d blocks (at most 512)", what, blocks);
+  if (blocks > kMaxBlocks)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: %d blocks (at most %d)", what, blocks,
+                          kMaxBlocks);
   if (!nb) return dsa::set_error(DSA_EINVAL, "%s: neighbors must be given", what);
   if ((int64_t)heads * blocks * blocks > 0x7fffffffLL)
     return dsa::set_error(DSA_EINVAL, "%s: route too large", what);
@@ -374,6 +386,11 @@ extern "C" int dsa_directional_update(
                      stream, candidates, cells);
   const unsigned groups = row_groups((int64_t)heads * blocks);
   hipLaunchKernelGGL(dir_expand_kernel, dim3(groups), dim3(256), 0, stream, p);
-  hipLaunchKernelGGL(dir_select_kernel, dim3(groups), dim3(256), 0, stream, p);
+  if (blocks <= 512)
+    hipLaunchKernelGGL(dir_select_kernel<8>, dim3(groups), dim3(256), 0, stream, p);
+  else if (blocks <= 1024)
+    hipLaunchKernelGGL(dir_select_kernel<16>, dim3(groups), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(dir_select_kernel<32>, dim3(groups), dim3(256), 0, stream, p);
   return dsa::check_launch("dsa_directional_update");
 }

@@ -126,7 +126,7 @@ int dsa_tile_stats(const void* q, const void* k, const int64_t* strides, int32_t
  * (flex.py:83-94, == sparse.py:171-181 `_row_mask`) and `_add_first_frame_sink`
  * (flex.py:550-566).  mass: [rows, keys] fp32, non-negative; previous: [rows,
  * keys] bytes or NULL (no prior); cap = max(1, ceil(keys * keep)); the first
- * sink_blocks columns are set after the cap.  keys <= 1024.  Outputs route
+ * sink_blocks columns are set after the cap.  keys <= 2048.  Outputs route
  * [rows, keys] bytes and counts [rows] (selected blocks per row, sink included).
  */
 int dsa_route_select(const float* mass, const uint8_t* previous, int32_t rows, int32_t keys,
@@ -138,7 +138,7 @@ int dsa_route_select(const float* mass, const uint8_t* previous, int32_t rows, i
  * neighbour along the query axis (route[h, nb[q][d], k]) or the key axis
  * (route[h, q, nb[k][d]]).  Replaces `frontier_mask`
  * (attention_backends/routing.py:10-41).  route, frontier: [heads, blocks,
- * blocks] bytes; neighbors: [blocks, 4] int32 (-1 = none), blocks <= 512.
+ * blocks] bytes; neighbors: [blocks, 4] int32 (-1 = none), blocks <= 2048.
  * count (optional, device) receives the number of frontier cells.
  */
 int dsa_frontier_mask(const uint8_t* route, int32_t heads, int32_t blocks,
@@ -152,7 +152,7 @@ int dsa_frontier_mask(const uint8_t* route, int32_t heads, int32_t blocks,
  * first-frame sink that flex.py:544-546 applies to its result.
  *   mass: [heads, blocks, blocks] fp32, non-negative; previous: route bytes;
  *   previous_frontier: bytes or NULL (then the frontier of previous);
- *   neighbors: [blocks, 4] int32, blocks <= 512; cap = max(1, ceil(blocks *
+ *   neighbors: [blocks, 4] int32, blocks <= 2048; cap = max(1, ceil(blocks *
  *   keep)); explore_count = 0 or max(1, ceil(blocks * exploration_fraction));
  *   expand_flags: 1 query axis, 2 key axis, 4 joint.
  * Outputs (bytes, [heads, blocks, blocks]): route (selection, then the first

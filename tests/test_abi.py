@@ -57,8 +57,8 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 128, 128,
                              None, None, 1, 0.1, None, fake, 16, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
-    status = lib.dsa_route_select(fake, None, 4, 1100, 0.5, 0.95, 1, 0, fake, fake, None)
-    assert status == _lib.DSA_EUNSUPPORTED and "1024" in _lib.last_error()
+    status = lib.dsa_route_select(fake, None, 4, 2100, 0.5, 0.95, 1, 0, fake, fake, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "2048" in _lib.last_error()
     status = lib.dsa_sampled_mass(fake, fake, _lib.int64_array([8] * 4), 1024, 2, 128, 128, 3,
                                   0.1, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "power of two" in _lib.last_error()
@@ -77,8 +77,8 @@ def test_exact_and_routing_entry_points_validate_first(lib):
     status = lib.dsa_block_mass(fake, fake, strides, 256, 2, 128, 128, fake, 256, -1.0, fake,
                                 None)
     assert status == _lib.DSA_EINVAL and "scale" in _lib.last_error()
-    status = lib.dsa_frontier_mask(fake, 2, 600, fake, fake, None, None)
-    assert status == _lib.DSA_EUNSUPPORTED and "512" in _lib.last_error()
+    status = lib.dsa_frontier_mask(fake, 2, 2100, fake, fake, None, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "2048" in _lib.last_error()
     status = lib.dsa_frontier_mask(fake, 2, 16, None, fake, None, None)
     assert status == _lib.DSA_EINVAL and "neighbors" in _lib.last_error()
     aligned = ctypes.c_void_p(4096)

@@ -185,3 +185,26 @@ def test_permute_tokens_bit_exact(ops, cuda_device, grid, head_major):
         expected = src.transpose(1, 2)[:, layout["permutation"]]
         assert torch.equal(got.cpu(), expected)
         assert torch.equal(restored.cpu(), src.transpose(1, 2))
+
+
+@pytest.mark.parametrize("keys", [591, 1339, 2048])
+def test_route_select_beyond_1024_keys(ops, cuda_device, keys):
+    """Longer videos: 81 frames at 720p (591 blocks), 1080p x 81 frames
+    (1,339 blocks) and the 2,048-key maximum; prior and sink, bit-exact."""
+    mass = _random_mass((2, 24, keys), seed=keys)
+    rng = np.random.default_rng(keys + 1)
+    previous = rng.random((2, 24, keys)) < 0.625
+    route, counts = ops.route_select(
+        torch.from_numpy(mass).to(cuda_device), 0.95, 0.625,
+        previous=torch.from_numpy(previous).to(cuda_device), persistence=0.5, sink_blocks=29)
+    torch.cuda.synchronize()
+    expected = R.top_mass_route(R.persistence_prior(mass, previous, 0.5), 0.95, 0.625)
+    expected[..., :29] = True
+    got = route.cpu().numpy()
+    assert (got == expected).all(), np.argwhere((got != expected).any(-1))[:5]
+    assert (counts.cpu().numpy() == expected.sum(-1)).all()
+
+
+def test_route_select_rejects_more_than_2048_keys(ops, cuda_device):
+    with pytest.raises(ValueError, match="2048"):
+        ops.route_select(torch.zeros(1, 1, 2049, device=cuda_device), 0.95, 0.625)

@@ -149,3 +149,27 @@ def test_backend_directional_update_uses_frontier(cuda_device):
                                       G.frontier_mask(route, nb))
     finally:
         context.reset_runtime_state()
+
+
+@pytest.mark.parametrize("grid", [(21, 45, 80), (62, 45, 80)])
+def test_frontier_and_directional_beyond_512_blocks(ops, cuda_device, grid):
+    """81 frames at 720p (591 blocks) and 244 frames (1,744 blocks): the
+    spatial layout's neighbour table, bit-exact against the oracle."""
+    from dit_sparse_atten_amd.attention_backends.spatial import build_spatial_layout
+    layout = build_spatial_layout(grid, 128, 32)
+    nb = layout.neighbors_cpu.numpy()
+    blocks = nb.shape[0]
+    mass = route_mass(2, blocks, seed=blocks).numpy()
+    previous = random_route(2, blocks, seed=blocks + 1, keep=0.5).numpy()
+    frontier = ops.frontier_mask(_dev(previous, cuda_device), _dev(nb, cuda_device))
+    kwargs = dict(keep=0.625, persistence=0.5, min_ratio=0.25, candidate_bonus=0.5,
+                  budget_scale=1.1, exploration_fraction=0.01)
+    result = ops.directional_update(_dev(mass, cuda_device), _dev(previous, cuda_device),
+                                    _dev(nb, cuda_device), sink_blocks=29, **kwargs)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(frontier.cpu().numpy(), G.frontier_mask(previous, nb))
+    expected = G.directional_budget_update(mass, previous, nb, **kwargs)
+    route = expected["route"].copy()
+    route[..., :29] = True
+    np.testing.assert_array_equal(result["route"].cpu().numpy(), route)
+    np.testing.assert_array_equal(result["counts"].cpu().numpy(), route.sum(-1))
