@@ -236,3 +236,48 @@ def test_diffusers_processor_call_pattern(cuda_device, name):
         _assert_close(out.float().cpu().numpy(), expected)
     finally:
         context.reset_runtime_state()
+
+
+def test_flex_hybrid_at_81_frames(backends, cuda_device):
+    """Wan's default 81 frames at 720p: grid (21, 45, 80), 75,600 tokens, 591
+    blocks (above the 512 of a one-wave 8-key-per-lane sort).  Sampled
+    bootstrap, activation with frontier, sampled update; routes hold the sink
+    and stay within the cap; outputs are finite and sampled rows match a
+    float32 softmax over the route's key blocks."""
+    flex, context = backends
+    grid = (21, 45, 80)
+    tokens, heads = math.prod(grid), 2
+    generator = torch.Generator(device=cuda_device).manual_seed(81)
+    q, k, v = (torch.randn(1, tokens, heads, 128, device=cuda_device,
+                           generator=generator).bfloat16() for _ in range(3))
+    backend = flex.FlexReuseBackend(flex.FlexReuseConfig(
+        bootstrap_mode="sampled", prefetch_sampled_bootstrap=True, sampled_update_interval=2,
+        prefetch_sampled_update=False, route_samples=16, mass_target=0.95, keep=0.625,
+        total_steps=5, spatial_reorder=True))
+    layout = backend._spatial_layout(grid, tokens)
+    blocks = layout.neighbors_cpu.shape[0]
+    assert blocks == 591
+    cap = math.ceil(blocks * 0.625)
+    sink = math.ceil(45 * 80 / 128)
+    for step in range(3):
+        context.set_routing_context(attention_id=4, step=step, branch=0, grid=grid)
+        out = backend(q, k, v)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all()
+    state = next(iter(backend.state.values()))
+    route = state["route"]
+    assert route.shape == (heads, blocks, blocks) and route[..., :sink].all()
+    assert int(route.sum(-1).max()) <= cap + sink
+    assert backend.phase_counts["sampled_bootstrap"] == 1
+    assert backend.phase_counts["sampled_update"] == 1
+    # 32 sampled query rows of head 1 against a float32 softmax over the route.
+    perm = layout.permutation_cpu.long()
+    qp, kp, vp = (x[0, perm.to(cuda_device), 1].float() for x in (q, k, v))
+    rows = torch.randperm(tokens, generator=torch.Generator().manual_seed(5))[:32]
+    keys_on = route[1][(rows // 128).to(cuda_device)].repeat_interleave(128, dim=-1)[:, :tokens]
+    scores = qp[rows.to(cuda_device)] @ kp.T * 128 ** -0.5
+    probs = torch.softmax(scores.masked_fill(~keys_on, float("-inf")), dim=-1)
+    expected = probs @ vp
+    got = out[0, perm.to(cuda_device)[rows.to(cuda_device)], 1].float()
+    cosine = torch.nn.functional.cosine_similarity(got.flatten(), expected.flatten(), dim=0)
+    assert (got - expected).abs().max().item() <= MAX_ABS and cosine.item() >= MIN_COSINE
