@@ -34,7 +34,7 @@ using dsa::kKStage;
 using dsa::kRowBytes;
 
 constexpr int kStats = 5;  // mass, q_y, q_x, k_y, k_x
-constexpr int kMaxTiles = 1024;
+constexpr int kMaxTiles = 2048;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct TileStatsParams {

@@ -102,7 +102,7 @@ int dsa_block_mass(const void* q, const void* k, const int64_t* strides, int32_t
 /*
  * Spatial-tile attention statistics of one batch-1 self-attention call over
  * tile-major tokens (tile_h * tile_w <= 128 tokens per tile, tokens a whole
- * number of tiles, at most 1024 tiles).  Replaces the statistics of the
+ * number of tiles, at most 2048 tiles).  Replaces the statistics of the
  * matrix-sparse backend: `_dense_route` (attention_backends/sparse.py:184-233)
  * with row_ptr == col_idx == NULL, `sparse_chunk` (sparse.py:718-750) with the
  * CSR of the tiles each (head, query tile) row attended, and the

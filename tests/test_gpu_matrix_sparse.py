@@ -72,10 +72,12 @@ def _compare_stats(got, expected):
                                    atol=CENTROID_ATOL, err_msg=key)
 
 
-@pytest.mark.parametrize("grid", [(4, 16, 16), (2, 18, 32), (2, 24, 32)])
-def test_dense_tile_stats_match_oracle(ops, cuda_device, grid):
-    """Tiles of 8x8 (64 tokens) and 9x8 (72 tokens: two half-tiles per tile)."""
-    case, q, k, v = _tile_major_inputs(grid, 3, seed=sum(grid))
+@pytest.mark.parametrize("grid,tile", [((4, 16, 16), 64), ((2, 18, 32), 64), ((2, 24, 32), 64),
+                                       ((1, 44, 100), 4)])
+def test_dense_tile_stats_match_oracle(ops, cuda_device, grid, tile):
+    """Tiles of 8x8 (64 tokens), 9x8 (72 tokens: two half-tiles per tile) and
+    2x2 (1,100 tiles: more than 1,024 per row)."""
+    case, q, k, v = _tile_major_inputs(grid, 3, seed=sum(grid), tile=tile)
     qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
     _, lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
     got = ops.tile_stats(qd, kd, lse, case.tile_shape)
@@ -105,10 +107,11 @@ def test_routed_tile_attention_and_stats_match_oracle(ops, cuda_device, grid):
     assert (got["mass"].cpu().numpy()[~route] == 0).all()
 
 
-def test_route_select_up_to_1024_tiles(ops, cuda_device):
-    """The 720p tile route has 800 key tiles per row (one-wave 1024-key sort)."""
+def test_route_select_up_to_2048_tiles(ops, cuda_device):
+    """The 720p tile route has 800 key tiles per row at 61 frames and 1,050 at
+    81 frames (one-wave sorts of 1,024 and 2,048 keys)."""
     rng = np.random.default_rng(5)
-    for keys in (513, 800, 1024):
+    for keys in (513, 800, 1024, 1050, 2048):
         mass = rng.dirichlet(np.full(keys, 0.3), size=(3, 40)).astype(np.float32)
         route, counts = ops.route_select(torch.from_numpy(mass).to(cuda_device), 0.95, 0.625,
                                          sink_blocks=100)
