@@ -292,9 +292,9 @@ def e2e_loop(device):
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every GPU box "
-              "in this build has one GPU, and the multi-GPU sharding of this path is a design "
-              "(head sharding) described in DESIGN.md.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this path "
+              "runs on one GPU; across GPUs it would shard by head (each GPU running these "
+              "kernels on its share of the heads), which is not built.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
