@@ -47,7 +47,7 @@ def parse_args():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
-    parser.add_argument("--cpu-sample-rows", type=int, default=64,
+    parser.add_argument("--cpu-sample-rows", type=int, default=512,
                         help="(head, query-block) rows timed for the CPU baseline")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-e2e", action="store_true",
@@ -144,17 +144,21 @@ def cpu_baseline(q, k, v, route, rows):
     staged = {}
     for head in sorted(set(int(h) for h in heads)):  # host copies, outside the timed region
         staged[head] = tuple(x[:, :, head:head + 1].float().cpu().numpy() for x in (q, k, v))
-    flops = 0.0
-    started = time.perf_counter()
-    for head, q_block in zip(heads, q_blocks):
-        qn, kn, vn = staged[int(head)]
-        sub_route = routes[head:head + 1]
-        start, end = int(q_block) * BLOCK, (int(q_block) + 1) * BLOCK
-        stats = sparse_path.empty_stats(1, TOKENS // BLOCK)
-        sparse_path.sparse_chunk(qn, kn, vn, sub_route, BLOCK, start, end,
-                                 HEAD_DIM ** -0.5, stats)
-        flops += kept_flops(int(sub_route[0, q_block].sum()))
-    seconds = time.perf_counter() - started
+    def run(with_stats):
+        flops = 0.0
+        started = time.perf_counter()
+        for head, q_block in zip(heads, q_blocks):
+            qn, kn, vn = staged[int(head)]
+            sub_route = routes[head:head + 1]
+            start, end = int(q_block) * BLOCK, (int(q_block) + 1) * BLOCK
+            stats = sparse_path.empty_stats(1, TOKENS // BLOCK) if with_stats else None
+            sparse_path.sparse_chunk(qn, kn, vn, sub_route, BLOCK, start, end,
+                                     HEAD_DIM ** -0.5, stats)
+            flops += kept_flops(int(sub_route[0, q_block].sum()))
+        return flops, time.perf_counter() - started
+
+    flops, seconds = run(True)
+    core_flops, core_seconds = run(False)
     cpu_model = ""
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -172,6 +176,9 @@ def cpu_baseline(q, k, v, route, rows):
                    f"sparse.py restatement (numpy fp32, 128-token tiles, statistics included): "
                    f"{flops / 1e9:.1f} GFLOP in {seconds:.2f} s; cpu {cpu_model or platform.machine()}"),
         "ms_per_call_extrapolated": seconds / flops * kept_flops(int(route.sum())) * 1e3,
+        "attention_only_tflops": core_flops / core_seconds / 1e12,
+        "attention_only_note": "the same rows without the statistics the reference's "
+                               "PyTorch path adds (sparse.py:716-751)",
     }
 
 
