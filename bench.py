@@ -182,6 +182,89 @@ def cpu_baseline(q, k, v, route, rows):
     }
 
 
+def config0_baseline(device, repeats=5, warmup=2):
+    """one sparse.py self-attention call on the 4x16x16
+    latent grid (1,024 tokens, 12 heads, d=128, 8x8 = 64-token tiles, 16
+    tiles).  The oracle's restatement runs on the host in fp32: its step-0
+    bootstrap builds the route (top-mass 0.95, cap 0.625, the frame-0 tiles as
+    key sink), then a later call over that route (sparse.py:794-930, policy
+    "reuse") is timed with its statistics and without them.  bsa_fwd runs the
+    same call on the GPU over the same route and the same bf16-rounded inputs;
+    the outputs are compared with the reference's benchmark metrics
+    (profiles/backend/metrics.py:8-30)."""
+    from oracle import sparse_path
+
+    from dit_sparse_atten_amd import ops
+
+    heads = 12
+    case = sparse_path.SparsePathCase((4, 16, 16), tile=64, keep=0.625, mass_target=0.95)
+    tokens = case.permutation.size
+    tiles = tokens // case.tile
+    shape = (1, tokens, heads, HEAD_DIM)
+    generator = torch.Generator().manual_seed(0)
+
+    def clustered():  # tile-major: the tokens of one spatial tile are consecutive
+        noise = torch.randn(shape, generator=generator)
+        centroid = torch.randn((1, tiles, 1, heads, HEAD_DIM), generator=generator)
+        return (0.5 * noise.view(1, tiles, case.tile, heads, HEAD_DIM) + centroid).view(shape)
+
+    q_tm, k_tm = clustered(), clustered()
+    v_tm = torch.randn(shape, generator=generator)
+    q_tm, k_tm, v_tm = (x.to(torch.bfloat16) for x in (q_tm, k_tm, v_tm))
+    host = [case.from_tile_major(x.float().numpy()) for x in (q_tm, k_tm, v_tm)]
+    case.bootstrap(*host)
+
+    def median_ms(function):
+        for _ in range(warmup):
+            function()
+        samples = []
+        for _ in range(repeats):
+            started = time.perf_counter()
+            function()
+            samples.append(time.perf_counter() - started)
+        samples.sort()
+        return samples[len(samples) // 2] * 1e3
+
+    expected = case.step(*host)
+    full_ms = median_ms(lambda: case.step(*host))
+    core_ms = median_ms(lambda: case.step(*host, collect_stats=False))
+
+    route = torch.as_tensor(case.route).to(device)
+    csr = ops.route_to_csr(route, block_size=case.tile)
+    qd, kd, vd = (x.to(device) for x in (q_tm, k_tm, v_tm))
+    out = torch.empty_like(qd)
+
+    def gpu_call():
+        ops.bsa_fwd(qd, kd, vd, csr, out=out, block_size=case.tile)
+
+    for _ in range(warmup):
+        gpu_call()
+    torch.cuda.synchronize()
+    gpu_ms, _ = EventTimer().time(gpu_call, 20)
+    actual = torch.from_numpy(case.from_tile_major(out.float().cpu().numpy()))
+    reference = torch.from_numpy(expected)
+    difference = actual - reference
+    return {
+        "workload": ("config0: one sparse.py self-attention call, B=1, 12 heads, d=128, grid "
+                     "4x16x16 (1,024 tokens), 8x8 = 64-token tiles, top-mass 0.95 / cap 0.625 "
+                     "route from the step-0 bootstrap plus the 4 frame-0 sink tiles"),
+        "route_keep": float(case.route.mean()),
+        "cpu_full_ms": full_ms,
+        "cpu_attention_only_ms": core_ms,
+        "cpu_timing": (f"median of {repeats} after {warmup} warm-up calls, numpy fp32, "
+                       f"{len(os.sched_getaffinity(0))} threads; full = tile-major reorder, "
+                       f"sparse_chunk with statistics, restore"),
+        "gpu_bsa_fwd_ms": gpu_ms,
+        "parity": {
+            "relative_l2": float(difference.norm() / reference.norm().clamp_min(1e-12)),
+            "max_absolute_error": float(difference.abs().max()),
+            "cosine_similarity": float(torch.nn.functional.cosine_similarity(
+                actual.flatten(), reference.flatten(), dim=0)),
+        },
+        "parity_bar": {"max_absolute_error": 2e-2, "cosine_similarity": 0.9995},
+    }
+
+
 def e2e_loop(device):
     """random-init Wan2.1-1.3B-shaped DiT, 5 steps at
     1280x720x61 (57,600 tokens), CFG pair, 512 x 4096 text embeddings; the
@@ -560,6 +643,7 @@ def main():
 
     if not args.no_cpu_baseline and not args.only_sparse:
         result["cpu_baseline"] = cpu_baseline(q, k, v, route, args.cpu_sample_rows)
+        result["cpu_baseline"]["config0"] = config0_baseline(device)
     print(json.dumps(result), flush=True)
 
 
