@@ -492,6 +492,30 @@ def main():
         result["roofline"]["frac_of_measured_gemm"] = round(achieved / gemm_tflops, 4)
         del ga, gb, gc
 
+        # One GPU's share when the heads are split over GPUs: 40 heads over 8
+        # GPUs (5 each) and the 1.3B model's 12 heads over 4 (3 each), taken
+        # as head slices of the same inputs and routes.
+        shares = {}
+        for share_heads in (5, 3):
+            share_csr = ops.route_to_csr(route[:share_heads].contiguous())
+            share_out = torch.empty((1, TOKENS, share_heads, HEAD_DIM), dtype=torch.bfloat16,
+                                    device=device)
+            q_s, k_s, v_s = (x[:, :, :share_heads] for x in (q, k, v))
+
+            def share_call():
+                ops.bsa_fwd(q_s, k_s, v_s, share_csr, out=share_out)
+
+            share_call()
+            torch.cuda.synchronize()
+            share_ms, _ = timer.time(share_call, 20)
+            share_flops = kept_flops(share_csr.nnz_value())
+            shares[f"{share_heads}_heads"] = {
+                "ms_per_call": round(share_ms, 4),
+                "tflops": round(share_flops / (share_ms * 1e-3) / 1e12, 2),
+                "workgroups": share_heads * blocks,
+            }
+        result["per_gpu_share"] = shares
+
     if not args.only_sparse:
         def dense_call():
             ops.bsa_fwd(q, k, v, out=out)
