@@ -48,6 +48,7 @@ struct BsaParams {
   const int32_t* col_idx;
   int32_t batch, heads, q_tokens, kv_tokens, q_blocks, kv_blocks, route_batches;
   int32_t block;     // tokens per query block and per key block (1..128)
+  int32_t block_pad; // gathered stream: key slots per block (block rounded up to 8)
   float scale;       // softmax scale applied to <q, k>
   float scale_log2;  // scale * log2(e)
 };
@@ -121,11 +122,58 @@ __global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restr
   }
 }
 
+// V^T workspace of the gathered key stream: one WG per (key block, b, h)
+// writes the block's keys as [128 dims][block_pad] in plain key order, zeros
+// in the pad slots, so every 8-key group of a block is one 16-byte run.
+// Per (b, h): [kv_blocks][128][block_pad]; the host requires whole blocks.
+__global__ void __launch_bounds__(256) vt_blocks_kernel(const __bf16* __restrict__ v,
+                                                        __bf16* __restrict__ vt, int64_t v_sb,
+                                                        int64_t v_st, int64_t v_sh,
+                                                        int32_t heads, int32_t block,
+                                                        int32_t block_pad, int32_t vt_keys) {
+  __shared__ __bf16 tile[128][kHeadDim + 8];
+  const int kb = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / heads, h = bh % heads;
+  const int tid = threadIdx.x;
+  const __bf16* src = v + b * v_sb + h * v_sh + (int64_t)kb * block * v_st;
+  for (int idx = tid; idx < block * 16; idx += 256) {
+    const int r = idx >> 4, c = idx & 15;
+    *reinterpret_cast<dsa_u32x4*>(&tile[r][c * 8]) =
+        *reinterpret_cast<const dsa_u32x4*>(src + (int64_t)r * v_st + c * 8);
+  }
+  dsa::lds_barrier();
+  __bf16* out = vt + (int64_t)bh * kHeadDim * vt_keys + (int64_t)kb * kHeadDim * block_pad;
+  const int groups = block_pad >> 3;
+  for (int idx = tid; idx < kHeadDim * groups; idx += 256) {
+    const int d = idx / groups, c = idx - d * groups;
+    dsa_bf16x8 val;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = c * 8 + e;
+      val[e] = key < block ? tile[key][d] : (__bf16)0.0f;
+    }
+    *reinterpret_cast<dsa_bf16x8*>(out + d * block_pad + c * 8) = val;
+  }
+}
+
+// The 4-key quads of each 16-key group in the order 0, 2, 1, 3 (an involution).
+__device__ __forceinline__ int quad_swap(int i) {
+  const int q = (i >> 2) & 3;
+  return (i & ~15) | ((((q & 1) << 1) | (q >> 1)) << 2) | (i & 3);
+}
+
 // kRouted: key blocks from the CSR row (false: every key block, dense).
 // kNh: 64-key half-tiles per key block (2 for blocks of 65..128 keys, else 1).
 // kSkip: some half-tile of every block holds at most 32 valid keys (block
 // sizes 65..96, or at most 32), so those steps run one 32-key sub-tile.
-template <bool kRouted, int kNh, bool kSkip>
+// kGather (routed, whole blocks of 65..127 keys): the row's kept blocks are
+// concatenated, each padded to block_pad keys, and streamed as 64-key chunks,
+// so a 72-key block costs 72 key slots instead of 64 + 32.  A chunk's K stage
+// row r holds stream position quad_swap(r) and its V^T stage holds the
+// positions in order; the lane layout of S^T and P^T then matches the plain
+// layout in which the V^T workspace carries the quad swap instead.
+template <bool kRouted, int kNh, bool kSkip, bool kGather = false>
 __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf16* vt,
                                                           int32_t vt_keys) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
@@ -190,6 +238,16 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     voff[j] = d * kHalfKeys + vt9_swz(d, idx & 7) * 8;
   }
 
+  // Gathered stream: the stream position of each K row this lane stages and
+  // the first position of each 8-key V^T group it stages.
+  int kpos[4], vpos[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = (wave * 4 + j) * 64 + lane;
+    kpos[j] = quad_swap(idx >> 4);
+    vpos[j] = vt9_swz(idx >> 3, idx & 7) * 8;
+  }
+
   auto block_of = [&](int j) -> int {
     const int it = start + j;
     const int kb = kRouted ? cidx[it] : it;
@@ -210,6 +268,34 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     for (int j = 0; j < 4; ++j)
       lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, voff[j] * 2, vsoff);
   };
+  // Stages the 64-key chunk that starts `o0` slots into stream block kb0 and
+  // runs on into kb1 (the blocks are in range; pad and tail slots load
+  // whatever they address, or zeros past the end, and are masked).
+  const __amdgpu_buffer_rsrc_t k_all_rsrc = make_rsrc(
+      kbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.k_st * 2 + kRowBytes));
+  auto issue_gather = [&](int kb0, int kb1, int o0, unsigned char* kdst, unsigned char* vdst)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int o = o0 + kpos[j];
+      const bool first = o < p.block_pad;
+      const int token = (first ? kb0 : kb1) * p.block + (first ? o : o - p.block_pad);
+      const int row = (wave * 4 + j) * 4 + (lane >> 4);
+      const uint32_t off = (uint32_t)token * (uint32_t)(p.k_st * 2) +
+                           (uint32_t)(k2_swz(row, lane & 15) * 16);
+      lds_load16(k_all_rsrc, kdst + (wave * 4 + j) * 1024, off, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int o = o0 + vpos[j];
+      const bool first = o < p.block_pad;
+      const int d = ((wave * 4 + j) * 64 + lane) >> 3;
+      const uint32_t slot = (uint32_t)((first ? kb0 : kb1) * kHeadDim + d) *
+                                (uint32_t)p.block_pad +
+                            (uint32_t)(first ? o : o - p.block_pad);
+      lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, slot * 2, 0);
+    }
+  };
   // Valid keys of half-tile `half` of block kb (0 for an invalid block).
   auto valid_of = [&](int kb, int half) -> int {
     if (kb < 0) return 0;
@@ -229,8 +315,11 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
   // NKT: 32-key sub-tiles of the half-tile that hold valid keys (2, or 1 when
   // at most 32 are valid: the last half of a 65..96-key block, or a block of
   // at most 32 keys), so empty sub-tiles cost neither MFMAs nor softmax work.
+  // Gathered stream: `invalid` has bit p set when stream position p of the
+  // chunk is a pad slot, past the row's last key or in an out-of-range block;
+  // lane half g holds positions 32 kt + 16 (r >> 3) + 8 g + (r & 7).
   auto compute = [&](const unsigned char* kt_lds, const unsigned char* vt_lds, int valid,
-                     auto nkt_c) __attribute__((always_inline)) {
+                     uint64_t invalid, auto nkt_c) __attribute__((always_inline)) {
     constexpr int NKT = decltype(nkt_c)::value;
     dsa_f32x16 sacc[NKT];
 #pragma unroll
@@ -247,7 +336,18 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
         sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], sacc[kt], 0, 0, 0);
       }
     }
-    if (valid < NKT * 32) {
+    if constexpr (kGather) {
+      if (invalid != 0) {
+        const uint64_t mine = g ? invalid >> 8 : invalid;
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+          const uint32_t bits = (uint32_t)(mine >> (32 * kt));
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (bits & (1u << (16 * (r >> 3) + (r & 7)))) sacc[kt][r] = -INFINITY;
+        }
+      }
+    } else if (valid < NKT * 32) {
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
@@ -316,15 +416,73 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     if (wave_active) {
       const int valid = valid_of(kb, half);
       if (decltype(skip_c)::value && valid <= 32)
-        compute(kc, vc, valid, std::integral_constant<int, 1>{});
+        compute(kc, vc, valid, 0ull, std::integral_constant<int, 1>{});
       else
-        compute(kc, vc, valid, std::integral_constant<int, 2>{});
+        compute(kc, vc, valid, 0ull, std::integral_constant<int, 2>{});
+    }
+  };
+  // Gathered stream step: chunk at slot o0 of stream block j0 (whose block
+  // index is kb0; kb0 < 0 or kb1 < 0: out of range), `left` valid stream
+  // slots from the chunk start to the row's last key; next_kb0 == -2: no
+  // next chunk.
+  auto step_gather = [&](int kb0, int kb1, int o0, int left, int next_kb0, int next_kb1,
+                         int next_o0, const unsigned char* kc, const unsigned char* vc,
+                         unsigned char* kn, unsigned char* vn) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (next_kb0 != -2)
+      issue_gather(next_kb0 < 0 ? 0 : next_kb0, next_kb1 < 0 ? 0 : next_kb1, next_o0, kn, vn);
+    if (wave_active) {
+      const int second = p.block_pad - o0;  // first slot of block kb1
+      uint64_t invalid = 0;
+      if (left < 64) invalid = ~0ull << left;
+      if (p.block_pad > p.block) {
+        const int lo = max(p.block - o0, 0);
+        const int hi = min(second, 64);
+        if (lo < hi)
+          invalid |= (hi == 64 ? ~0ull : (1ull << hi) - 1) & ~((1ull << lo) - 1);
+      }
+      if (kb0 < 0) invalid |= second >= 64 ? ~0ull : (1ull << second) - 1;
+      if (kb1 < 0 && second < 64) invalid |= ~0ull << second;
+      if (left <= 32)
+        compute(kc, vc, 0, invalid, std::integral_constant<int, 1>{});
+      else
+        compute(kc, vc, 0, invalid, std::integral_constant<int, 2>{});
     }
   };
   const std::bool_constant<false> no_skip;
   const std::bool_constant<kSkip> may_skip;
 
-  if (nblk > 0) {
+  if (kGather && nblk > 0) {
+    // Stream block j: CSR entry j clamped to the row (slots past the row's
+    // last key are masked), -1 when out of range.
+    auto gblock = [&](int j) -> int {
+      const int kb = cidx[start + (j < nblk ? j : nblk - 1)];
+      return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
+    };
+    const int bp = p.block_pad;
+    const int total = (nblk - 1) * bp + p.block;  // slots up to the row's last key
+    const int chunks = (total + 63) >> 6;
+    int j0 = 0, o0 = 0;
+    int kb0 = gblock(0), kb1 = gblock(1);
+    issue_gather(kb0 < 0 ? 0 : kb0, kb1 < 0 ? 0 : kb1, 0, lds_k0, lds_v0);
+    for (int c = 0; c < chunks; c += 2) {
+      int j1 = j0, o1 = o0 + 64;
+      if (o1 >= bp) { o1 -= bp; ++j1; }
+      const bool more1 = c + 1 < chunks;
+      const int kb0n = more1 ? gblock(j1) : -2, kb1n = more1 ? gblock(j1 + 1) : -2;
+      step_gather(kb0, kb1, o0, total - c * 64, kb0n, kb1n, o1, lds_k0, lds_v0, lds_k1,
+                  lds_v1);
+      if (!more1) break;
+      int j2 = j1, o2 = o1 + 64;
+      if (o2 >= bp) { o2 -= bp; ++j2; }
+      const bool more2 = c + 2 < chunks;
+      const int kb0m = more2 ? gblock(j2) : -2, kb1m = more2 ? gblock(j2 + 1) : -2;
+      step_gather(kb0n, kb1n, o1, total - (c + 1) * 64, kb0m, kb1m, o2, lds_k1, lds_v1,
+                  lds_k0, lds_v0);
+      j0 = j2; o0 = o2; kb0 = kb0m; kb1 = kb1m;
+    }
+  } else if (!kGather && nblk > 0) {
     int kb = block_of(0);
     issue(kb, 0, lds_k0, lds_v0);
     if (kNh == 2) {
@@ -371,6 +529,18 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
 }
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// Routed calls take the gathered key stream when every key block is whole and
+// holds 65..127 keys and its 8-rounded size is below the plain layout's slots
+// per block (64 + 32 up to 96 keys, else 128), and the whole K sequence of one
+// head spans < 2 GiB (one buffer resource addresses it).
+bool use_gather(int32_t block, int32_t kv_tokens, int64_t k_token_stride) {
+  if (block <= kHalfKeys || block >= 2 * kHalfKeys || kv_tokens % block != 0) return false;
+  const int32_t pad = (block + 7) & ~7;
+  const int32_t plain = block - kHalfKeys <= 32 ? kHalfKeys + 32 : 2 * kHalfKeys;
+  if (pad >= plain) return false;
+  return ((int64_t)kv_tokens + 8) * k_token_stride * 2 + kRowBytes <= 0x7fffffff;
+}
 
 // Half-tiles per key block, and keys of the per-(b, h) V^T workspace.
 int32_t halves_per_block(int32_t block) { return block > kHalfKeys ? 2 : 1; }
@@ -465,14 +635,27 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   p.q_blocks = q_blocks; p.kv_blocks = kv_blocks;
   p.route_batches = row_ptr ? route_batches : 1;
   p.block = block_size;
+  p.block_pad = (block_size + 7) & ~7;
   p.scale = scale;
   p.scale_log2 = scale * 1.4426950408889634f;
   __bf16* vt = static_cast<__bf16*>(workspace);
+  const dim3 blocks((unsigned)grid), threads(256);
+  const __bf16* vtc = vt;
+  if (row_ptr && use_gather(block_size, kv_tokens, strides[4])) {
+    // Whole blocks of 65..127 keys: the gathered key stream, whose V^T
+    // workspace ([kv_blocks][128][block_pad] per (b, h)) fits in the plain
+    // one because block_pad is below that layout's slots per block.
+    const int32_t gather_keys = kv_blocks * p.block_pad;
+    hipLaunchKernelGGL(vt_blocks_kernel, dim3((unsigned)kv_blocks, (unsigned)(batch * heads)),
+                       dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads,
+                       block_size, p.block_pad, gather_keys);
+    hipLaunchKernelGGL((bsa_fwd_kernel<true, 2, true, true>), blocks, threads, 0, stream, p,
+                       vtc, gather_keys);
+    return dsa::check_launch("dsa_bsa_fwd");
+  }
   hipLaunchKernelGGL(vt_transpose_kernel, dim3((unsigned)(vt_keys / 64), (unsigned)(batch * heads)),
                      dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads, kv_tokens,
                      block_size, nh, vt_keys);
-  const dim3 blocks((unsigned)grid), threads(256);
-  const __bf16* vtc = vt;
   // Blocks whose last half-tile holds 1..32 keys run it as one sub-tile.
   const int rem = block_size % kHalfKeys;
   const bool skip = rem != 0 && rem <= 32;

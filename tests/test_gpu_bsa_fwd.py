@@ -145,7 +145,8 @@ def test_config1_dense_rope_against_sdpa_and_fp32(cuda_device):
 
 
 @pytest.mark.parametrize("block,tokens", [(8, 200), (40, 600), (64, 1024), (65, 650),
-                                          (72, 1440), (72, 1400), (100, 777), (128, 1000)])
+                                          (72, 1440), (72, 1400), (80, 960), (100, 777),
+                                          (100, 1000), (120, 1200), (127, 1270), (128, 1000)])
 def test_tile_blocks_match_oracle(cuda_device, block, tokens):
     """Blocks of 1..128 tokens (the matrix-sparse backend's spatial tiles,
     sparse.py:670-751): one 64-key half-tile per block up to 64 keys, two
@@ -164,6 +165,59 @@ def test_tile_blocks_match_oracle(cuda_device, block, tokens):
     _, expected_lse = block_sparse_attention(
         q.float().numpy(), k.float().numpy(), v.float().numpy(), route.numpy(), block)
     np.testing.assert_allclose(lse.cpu().numpy(), expected_lse, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("block,blocks,keep", [(72, 64, 0.7), (65, 40, 0.3), (100, 30, 0.9)])
+def test_gathered_key_stream_long_rows(cuda_device, block, blocks, keep):
+    """Whole blocks of 65..127 keys stream the row's kept blocks as one
+    gathered sequence of 64-key chunks (pad slots and the tail masked): long
+    rows with chunks straddling blocks, a row with one block, and B=2 with a
+    per-batch route."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    tokens = block * blocks
+    q, k, v = _inputs(2, tokens, 2, seed=blocks)
+    generator = torch.Generator().manual_seed(blocks)
+    route = torch.rand(2, 2, blocks, blocks, generator=generator) < keep
+    route[..., 0] = True
+    route[0, 0, 1] = False
+    route[0, 0, 1, 0] = True  # one-block row
+    csr = csr_from_route(route.to(cuda_device), block_size=block)
+    out, lse = bsa_fwd(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device), csr,
+                       return_lse=True, block_size=block)
+    torch.cuda.synchronize()
+    for b in range(2):
+        _check(out[b:b + 1], q[b:b + 1], k[b:b + 1], v[b:b + 1], route[b], block=block)
+        _, expected_lse = block_sparse_attention(
+            q[b:b + 1].float().numpy(), k[b:b + 1].float().numpy(),
+            v[b:b + 1].float().numpy(), route[b].numpy(), block)
+        np.testing.assert_allclose(lse[b:b + 1].cpu().numpy(), expected_lse, atol=1e-3,
+                                   rtol=1e-4)
+
+
+def test_gathered_key_stream_skips_out_of_range_blocks(cuda_device):
+    """Out-of-range key blocks in a CSR row are skipped (the documented
+    contract) in the gathered stream too, wherever they fall in the row."""
+    from dit_sparse_atten_amd.ops import RouteCSR, bsa_fwd
+    block, blocks = 72, 12
+    tokens = block * blocks
+    q, k, v = _inputs(1, tokens, 1, seed=5)
+    generator = torch.Generator().manual_seed(5)
+    route = torch.rand(1, blocks, blocks, generator=generator) < 0.5
+    route[..., 0] = True
+    rows, bad = [], [-1, blocks, blocks + 9, 1 << 20]
+    for qb in range(blocks):
+        cols = torch.nonzero(route[0, qb]).flatten().tolist()
+        cols.insert(qb % (len(cols) + 1), bad[qb % len(bad)])
+        rows.append(cols)
+    row_ptr = torch.tensor([0] + np.cumsum([len(r) for r in rows]).tolist(), dtype=torch.int32)
+    col_idx = torch.tensor([c for r in rows for c in r], dtype=torch.int32)
+    counts = torch.tensor([len(r) for r in rows], dtype=torch.int32)
+    csr = RouteCSR(row_ptr.to(cuda_device), col_idx.to(cuda_device), counts.to(cuda_device),
+                   1, 1, blocks, blocks, block)
+    out = bsa_fwd(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device), csr,
+                  block_size=block)
+    torch.cuda.synchronize()
+    _check(out, q, k, v, route, block=block)
 
 
 @pytest.mark.parametrize("block", [24, 72, 128])
