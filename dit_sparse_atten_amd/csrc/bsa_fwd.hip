@@ -359,7 +359,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = dsa::pair32_max(mx);
     const float mx2 = mx * p.scale_log2;
     const bool up = mx2 > m_run + kRescaleLog2;
     if (__any(up)) {
@@ -506,7 +506,7 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     }
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = dsa::pair32_sum(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (row_ok) {
     __bf16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;

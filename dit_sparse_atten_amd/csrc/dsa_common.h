@@ -40,6 +40,36 @@ constexpr int kNumXcd = 8;
 
 // Remaps a dispatch index so that each XCD receives one contiguous range of
 // the logical work order (consecutive workgroups on one XCD share L2 lines).
+// Lanes l and l ^ 32 combine through v_permlane32_swap, a VALU op with no LDS
+// round trip.  Both lanes of a pair get the same result (max is exact, and
+// a + b == b + a in IEEE arithmetic).
+__device__ __forceinline__ float pair32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over the 64 lanes in a fixed order, the same value in every lane: DPP
+// butterflies inside each 16-lane row (quad xor 1, quad xor 2, half-row
+// mirror, row mirror), then the four row sums read from lanes 0, 16, 32, 48.
+// Every lane of the wave must be active.
+__device__ __forceinline__ float wave_total(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ int xcd_remap(int wg, int total) {
   const int per = total / kNumXcd;
   const int rem = total % kNumXcd;

@@ -20,6 +20,16 @@
 // v_mfma_f32_32x32x16_bf16 so each lane owns one query row, fixed-order
 // reductions through LDS), plus key-offset lookups from two per-tile LDS
 // tables read as 16-byte vectors.
+//
+// Tiles of 65..127 tokens whose 8-rounded size is below the half-tile slots
+// (64 + 32 up to 96 tokens, else 128) take the gathered key stream instead:
+// the row's key tiles are concatenated, each padded to tile_pad (the tile
+// rounded up to 8), and staged as 64-key chunks, so a 72-token tile costs 72
+// key slots rather than 96.  A chunk spans at most two tiles, and the tile
+// boundary (a multiple of 8 positions into the chunk) falls between the
+// lanes' 4-key runs, so each run accumulates into one tile and the earlier
+// tile is reduced at the boundary.  Those kernels also run one wave per 32
+// query rows (3 for tiles of up to 96 tokens), so no wave idles.
 #include "bsa_tiles.h"
 
 #include <hip/hip_fp16.h>
@@ -51,14 +61,9 @@ struct TileStatsParams {
   __half* ckx;
   int64_t q_st, q_sh, k_st, k_sh, lse_sh;
   int32_t tokens, heads, tiles, tile, tile_h, tile_w;
+  int32_t tile_pad;  // gathered stream: key slots per tile (tile rounded up to 8)
   float scale_log2;
 };
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-  return v;
-}
 
 // (i - center) / scale for one tile axis, as sparse.py:141-146 computes it in fp32.
 __device__ __forceinline__ float axis_offset(int i, int length) {
@@ -67,13 +72,15 @@ __device__ __forceinline__ float axis_offset(int i, int length) {
   return ((float)i - center) / scale;
 }
 
-template <bool kRouted, int kNh>
-__global__ void __launch_bounds__(256, 2) tile_stats_kernel(TileStatsParams p) {
+// kWaves: waves per workgroup (4, or 3 for gathered tiles of up to 96 tokens).
+template <bool kRouted, int kNh, bool kGather = false, int kWaves = 4>
+__global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsParams p) {
+  constexpr int kThreads = kWaves * 64;
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(16))) float off_y[128];
   __shared__ __attribute__((aligned(16))) float off_x[128];
-  __shared__ float part[2][4][kStats];
+  __shared__ float part[2][kWaves][kStats];
   __shared__ uint32_t listed[kMaxTiles / 32];
 
   const int tid = threadIdx.x;
@@ -132,22 +139,25 @@ __global__ void __launch_bounds__(256, 2) tile_stats_kernel(TileStatsParams p) {
   const int64_t cell0 = ((int64_t)h * p.tiles + qt) * p.tiles;
   // Writes the cell of key tile kt, the j-th of this row (its partials sit in
   // part[j & 1]).
+  // Lane s < 5 of wave 0 sums statistic s over the waves and writes it.
   auto flush = [&](int j, int kt) __attribute__((always_inline)) {
-    if (wave == 0 && lane == 0 && kt >= 0) {
-      float v[kStats];
+    if (wave == 0 && lane < kStats && kt >= 0) {
       const float(*pr)[kStats] = part[j & 1];
-#pragma unroll
-      for (int s = 0; s < kStats; ++s) v[s] = (pr[0][s] + pr[1][s]) + (pr[2][s] + pr[3][s]);
+      auto total = [&](int s) {
+        return kWaves == 4 ? (pr[0][s] + pr[1][s]) + (pr[2][s] + pr[3][s])
+                           : (pr[0][s] + pr[1][s]) + pr[2][s];
+      };
+      const float mass = total(0);
       const int64_t cell = cell0 + kt;
-      const float normalized = v[0] / (float)p.tokens;
-      p.mass32[cell] = normalized;
-      if (p.mass16) p.mass16[cell] = __float2half(normalized);
-      const float den = fmaxf(v[0], 1e-12f);
-      if (p.cqy) p.cqy[cell] = __float2half(v[1] / den);
-      if (p.cqx) p.cqx[cell] = __float2half(v[2] / den);
-      if (p.cky) p.cky[cell] = __float2half(v[3] / den);
-      if (p.ckx) p.ckx[cell] = __float2half(v[4] / den);
-      if (kRouted) listed[kt >> 5] |= 1u << (kt & 31);
+      if (lane == 0) {
+        const float normalized = mass / (float)p.tokens;
+        p.mass32[cell] = normalized;
+        if (p.mass16) p.mass16[cell] = __float2half(normalized);
+        if (kRouted) listed[kt >> 5] |= 1u << (kt & 31);
+      } else {
+        __half* dst = lane == 1 ? p.cqy : lane == 2 ? p.cqx : lane == 3 ? p.cky : p.ckx;
+        if (dst) dst[cell] = __float2half(total(lane) / fmaxf(mass, 1e-12f));
+      }
     }
   };
 
@@ -196,11 +206,11 @@ __global__ void __launch_bounds__(256, 2) tile_stats_kernel(TileStatsParams p) {
   };
 
   auto end_tile = [&](int j) __attribute__((always_inline)) {
-    const float m = wave_sum(am);
-    const float qy = wave_sum(am * oyq);
-    const float qx = wave_sum(am * oxq);
-    const float ky = wave_sum(aky);
-    const float kx = wave_sum(akx);
+    const float m = dsa::wave_total(am);
+    const float qy = dsa::wave_total(am * oyq);
+    const float qx = dsa::wave_total(am * oxq);
+    const float ky = dsa::wave_total(aky);
+    const float kx = dsa::wave_total(akx);
     if (lane == 0) {
       float* dst = part[j & 1][wave];
       dst[0] = m;
@@ -212,6 +222,116 @@ __global__ void __launch_bounds__(256, 2) tile_stats_kernel(TileStatsParams p) {
     am = aky = akx = 0.f;
   };
 
+  if constexpr (kGather) {
+    const int bp = p.tile_pad;
+    const __amdgpu_buffer_rsrc_t k_all = dsa::make_rsrc(
+        kbase, (uint32_t)((int64_t)(p.tokens - 1) * p.k_st * 2 + kRowBytes));
+    const uint32_t kst2 = (uint32_t)(p.k_st * 2);
+    // Stages the chunk that starts `o0` slots into tile kta and runs on into
+    // tile ktb (both in range): stream position r lands in K stage row r;
+    // pad slots load whatever they address and are masked.
+    auto issue_gather = [&](int kta, int ktb, int o0, unsigned char* dst)
+        __attribute__((always_inline)) {
+      for (int i = wave; i < kKStage / 1024; i += kWaves) {
+        const int row = i * 4 + (lane >> 4);
+        const int o = o0 + row;
+        const bool first = o < bp;
+        const int token = (first ? kta : ktb) * p.tile + (first ? o : o - bp);
+        dsa::lds_load16(k_all, dst + i * 1024,
+                        (uint32_t)token * kst2 + (uint32_t)(dsa::k2_swz(row, lane & 15) * 16),
+                        0);
+      }
+    };
+    // Accumulates chunk positions [0, 32 NKK): those before `second` belong
+    // to tile ja (at tile-local offset o0 + position), the rest to the next
+    // tile (offset position - second).  At position `split` tile ja ends and
+    // is reduced.  masked: pad slots, positions >= left and out-of-range
+    // tiles (ok_a / ok_b false) count zero.
+    auto compute_gather = [&](const unsigned char* cur, int o0, int second, int split, int ja,
+                              bool masked, int left, bool ok_a, bool ok_b, auto nkk_c)
+        __attribute__((always_inline)) {
+      constexpr int NKK = decltype(nkk_c)::value;
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) {
+        dsa_f32x16 sacc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+        const int row = kk * 32 + qi;
+#pragma unroll
+        for (int dc = 0; dc < 8; ++dc) {
+          const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
+              cur + row * kRowBytes + dsa::k2_swz(row, dc * 2 + g) * 16);
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], sacc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int quad = 0; quad < 4; ++quad) {
+          // This lane's keys: positions 8 unit + 4 g + (0..3); a tile
+          // boundary (a multiple of 8) never splits them.
+          const int unit = kk * 4 + quad;
+          if (8 * unit == split) end_tile(ja);
+          const bool in_a = 8 * unit < second;
+          const int base = (in_a ? o0 : -second) + 8 * unit + 4 * g;
+          const dsa_f32x4 ky = *reinterpret_cast<const dsa_f32x4*>(&off_y[base]);
+          const dsa_f32x4 kx = *reinterpret_cast<const dsa_f32x4*>(&off_x[base]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float pv = __builtin_amdgcn_exp2f(fmaf(sacc[quad * 4 + e], p.scale_log2, -lse2));
+            if (masked) {
+              const bool ok = (in_a ? ok_a : ok_b) && base + e < p.tile &&
+                              8 * unit + 4 * g + e < left;
+              pv = ok ? pv : 0.f;
+            }
+            am += pv;
+            aky = fmaf(pv, ky[e], aky);
+            akx = fmaf(pv, kx[e], akx);
+          }
+        }
+      }
+    };
+
+    const int n = ntile;
+    if (n > 0) {
+      const int total = (n - 1) * bp + p.tile;  // slots up to the row's last key
+      const int chunks = (total + 63) >> 6;
+      auto tile_at = [&](int j) { return tile_of(j < n ? j : n - 1); };
+      int j0 = 0, o0 = 0;
+      int ka = tile_at(0), kb = tile_at(1);
+      issue_gather(ka < 0 ? 0 : ka, kb < 0 ? 0 : kb, 0, lds_k0);
+      int pend_j = -1, pend_kt = -1;
+      for (int c = 0; c < chunks; ++c) {
+        dsa::lds_barrier<true>();
+        if (pend_j >= 0) flush(pend_j, pend_kt);
+        pend_j = -1;
+        int j1 = j0, o1 = o0 + 64;
+        if (o1 >= bp) { o1 -= bp; ++j1; }
+        const int ka1 = tile_at(j1), kb1 = tile_at(j1 + 1);
+        if (c + 1 < chunks)
+          issue_gather(ka1 < 0 ? 0 : ka1, kb1 < 0 ? 0 : kb1, o1, (c & 1) ? lds_k0 : lds_k1);
+        const int second = bp - o0;
+        const bool has_next = j0 + 1 < n;
+        const int split = has_next && second < 64 ? second : -1;
+        const int left = total - c * 64;
+        const bool masked = bp > p.tile || left < 64 || ka < 0 || kb < 0;
+        const unsigned char* cur = (c & 1) ? lds_k1 : lds_k0;
+        using one = std::integral_constant<int, 1>;
+        using two = std::integral_constant<int, 2>;
+        if (left <= 32)
+          compute_gather(cur, o0, second, split, j0, masked, left, ka >= 0, kb >= 0, one{});
+        else
+          compute_gather(cur, o0, second, split, j0, masked, left, ka >= 0, kb >= 0, two{});
+        if (has_next && second <= 64) {
+          if (second == 64) end_tile(j0);
+          pend_j = j0;
+          pend_kt = ka;
+        }
+        j0 = j1; o0 = o1; ka = ka1; kb = kb1;
+      }
+      end_tile(n - 1);
+      dsa::lds_barrier();
+      if (pend_j >= 0) flush(pend_j, pend_kt);
+      flush(n - 1, tile_at(n - 1));
+    }
+  } else {
   // Steps walk (tile j, half i); every step waits for its stage, flushes the
   // previous tile once all partials are in LDS, prefetches, then computes.
   const int nsteps = ntile * kNh;
@@ -247,11 +367,12 @@ __global__ void __launch_bounds__(256, 2) tile_stats_kernel(TileStatsParams p) {
   }
   dsa::lds_barrier();
   if (nsteps > 0) flush(ntile - 1, prev_kt);
+  }
   if (kRouted) {
     dsa::lds_barrier();
     // Cells this row does not list hold zero mass and zero centroids.
     const __half zero = __float2half(0.f);
-    for (int kt = tid; kt < p.tiles; kt += 256) {
+    for (int kt = tid; kt < p.tiles; kt += kThreads) {
       if (listed[kt >> 5] & (1u << (kt & 31))) continue;
       const int64_t cell = cell0 + kt;
       p.mass32[cell] = 0.f;
@@ -333,10 +454,25 @@ extern "C" int dsa_tile_stats(const void* q, const void* k, const int64_t* strid
   p.tile = tile;
   p.tile_h = tile_h;
   p.tile_w = tile_w;
+  p.tile_pad = (tile + 7) & ~7;
   p.scale_log2 = scale * kLog2e;
   const dim3 blocks((unsigned)grid), threads(256);
   const bool routed = row_ptr != nullptr;
-  if (tile > kHalfKeys) {
+  const int32_t plain_slots = tile - kHalfKeys <= 32 ? kHalfKeys + 32 : 2 * kHalfKeys;
+  const bool gather = tile > kHalfKeys && tile < 2 * kHalfKeys && p.tile_pad < plain_slots &&
+                      ((int64_t)tokens + 8) * strides[2] * 2 + kRowBytes <= 0x7fffffff;
+  if (gather && tile <= 96) {
+    const dim3 three(192);
+    if (routed)
+      hipLaunchKernelGGL((tile_stats_kernel<true, 2, true, 3>), blocks, three, 0, stream, p);
+    else
+      hipLaunchKernelGGL((tile_stats_kernel<false, 2, true, 3>), blocks, three, 0, stream, p);
+  } else if (gather) {
+    if (routed)
+      hipLaunchKernelGGL((tile_stats_kernel<true, 2, true, 4>), blocks, threads, 0, stream, p);
+    else
+      hipLaunchKernelGGL((tile_stats_kernel<false, 2, true, 4>), blocks, threads, 0, stream, p);
+  } else if (tile > kHalfKeys) {
     if (routed)
       hipLaunchKernelGGL((tile_stats_kernel<true, 2>), blocks, threads, 0, stream, p);
     else

@@ -73,10 +73,11 @@ def _compare_stats(got, expected):
 
 
 @pytest.mark.parametrize("grid,tile", [((4, 16, 16), 64), ((2, 18, 32), 64), ((2, 24, 32), 64),
-                                       ((1, 44, 100), 4)])
+                                       ((1, 44, 100), 4), ((2, 15, 26), 64), ((1, 20, 30), 100)])
 def test_dense_tile_stats_match_oracle(ops, cuda_device, grid, tile):
-    """Tiles of 8x8 (64 tokens), 9x8 (72 tokens: two half-tiles per tile) and
-    2x2 (1,100 tiles: more than 1,024 per row)."""
+    """Tiles of 8x8 (64 tokens), 9x8 (72 tokens, gathered key stream, 3 waves),
+    2x2 (1,100 tiles: more than 1,024 per row), 5x13 (65 tokens padded to 72)
+    and 10x10 (100 tokens padded to 104, 4 waves)."""
     case, q, k, v = _tile_major_inputs(grid, 3, seed=sum(grid), tile=tile)
     qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
     _, lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
@@ -89,9 +90,10 @@ def test_dense_tile_stats_match_oracle(ops, cuda_device, grid, tile):
                                case.tile / q.shape[1], rtol=1e-4)
 
 
-@pytest.mark.parametrize("grid", [(4, 16, 16), (2, 18, 32)])
-def test_routed_tile_attention_and_stats_match_oracle(ops, cuda_device, grid):
-    case, q, k, v = _tile_major_inputs(grid, 2, seed=7)
+@pytest.mark.parametrize("grid,tile", [((4, 16, 16), 64), ((2, 18, 32), 64), ((2, 15, 26), 64),
+                                       ((1, 20, 30), 100)])
+def test_routed_tile_attention_and_stats_match_oracle(ops, cuda_device, grid, tile):
+    case, q, k, v = _tile_major_inputs(grid, 2, seed=7, tile=tile)
     tiles = q.shape[1] // case.tile
     route = random_route(2, tiles, seed=3, keep=0.5).numpy()
     route[..., 0] = True
@@ -105,6 +107,32 @@ def test_routed_tile_attention_and_stats_match_oracle(ops, cuda_device, grid):
     metrics = A.summarize(out.float().cpu().numpy(), expected_out)
     assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
     assert (got["mass"].cpu().numpy()[~route] == 0).all()
+
+
+def test_routed_tile_stats_skip_out_of_range_tiles(ops, cuda_device):
+    """Out-of-range key tiles in a CSR row are skipped by the gathered
+    statistics stream wherever they fall, and their cells stay zero."""
+    case, q, k, v = _tile_major_inputs((2, 18, 32), 1, seed=11)
+    tiles = q.shape[1] // case.tile
+    route = random_route(1, tiles, seed=4, keep=0.5).numpy()
+    route[..., 0] = True
+    rows, bad = [], [-1, tiles, tiles + 5, 1 << 20]
+    for qt in range(tiles):
+        cols = np.flatnonzero(route[0, qt]).tolist()
+        cols.insert(qt % (len(cols) + 1), bad[qt % len(bad)])
+        rows.append(cols)
+    row_ptr = torch.tensor([0] + np.cumsum([len(r) for r in rows]).tolist(), dtype=torch.int32)
+    col_idx = torch.tensor([c for r in rows for c in r], dtype=torch.int32)
+    counts = torch.tensor([len(r) for r in rows], dtype=torch.int32)
+    csr = ops.RouteCSR(row_ptr.to(cuda_device), col_idx.to(cuda_device), counts.to(cuda_device),
+                       1, 1, tiles, tiles, case.tile)
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    valid_csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=case.tile)
+    _, lse = ops.bsa_fwd(qd, kd, vd, valid_csr, return_lse=True, block_size=case.tile)
+    got = ops.tile_stats(qd, kd, lse, case.tile_shape, csr=csr)
+    torch.cuda.synchronize()
+    expected, _ = _oracle_stats(case, q, k, v, route)
+    _compare_stats(got, expected)
 
 
 def test_route_select_up_to_2048_tiles(ops, cuda_device):
