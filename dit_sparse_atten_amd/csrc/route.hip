@@ -227,10 +227,17 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
       step(t + 1, sweep, t + 2 < tiles ? t + 2 : -1, st1, st0);
     }
     if (sweep == 0) {  // each query's log-sum-exp (log2 units)
-      const float mo = __shfl_xor(m2, 32);
-      const float lo = __shfl_xor(l2, 32);
-      const float mx = fmaxf(m2, mo);
-      const float tot = l2 * __builtin_amdgcn_exp2f(m2 - mx) + lo * __builtin_amdgcn_exp2f(mo - mx);
+      // Lanes l and l ^ 32 hold the two halves of one query's keys; both get
+      // the same total (the pair's two terms in one fixed order, so a
+      // contracted fma rounds alike in both lanes).
+      const auto ms = __builtin_amdgcn_permlane32_swap(__float_as_uint(m2), __float_as_uint(m2),
+                                                       false, false);
+      const auto ls = __builtin_amdgcn_permlane32_swap(__float_as_uint(l2), __float_as_uint(l2),
+                                                       false, false);
+      const float ma = __uint_as_float(ms[0]), mb = __uint_as_float(ms[1]);
+      const float mx = fmaxf(ma, mb);
+      const float tot = __uint_as_float(ls[0]) * __builtin_amdgcn_exp2f(ma - mx) +
+                        __uint_as_float(ls[1]) * __builtin_amdgcn_exp2f(mb - mx);
       lse2 = mx + __builtin_log2f(tot);
       __syncthreads();  // every wave done with st0/st1 before sweep 2 refills st0
     }
