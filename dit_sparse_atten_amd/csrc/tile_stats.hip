@@ -28,8 +28,8 @@
 // key slots rather than 96.  A chunk spans at most two tiles, and the tile
 // boundary (a multiple of 8 positions into the chunk) falls between the
 // lanes' 4-key runs, so each run accumulates into one tile and the earlier
-// tile is reduced at the boundary.  Those kernels also run one wave per 32
-// query rows (3 for tiles of up to 96 tokens), so no wave idles.
+// tile is reduced at the boundary.  Every kernel runs one wave per 32 query
+// rows of the tile (at least two), so no wave idles above 32 tokens.
 #include "bsa_tiles.h"
 
 #include <hip/hip_fp16.h>
@@ -72,7 +72,7 @@ __device__ __forceinline__ float axis_offset(int i, int length) {
   return ((float)i - center) / scale;
 }
 
-// kWaves: waves per workgroup (4, or 3 for gathered tiles of up to 96 tokens).
+// kWaves: waves per workgroup, one per 32 query rows of the tile (2..4).
 template <bool kRouted, int kNh, bool kGather = false, int kWaves = 4>
 __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsParams p) {
   constexpr int kThreads = kWaves * 64;
@@ -93,11 +93,11 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
   const int qt = work % p.tiles;
   const int h = work / p.tiles;
 
-  if (tid < 128) {
+  for (int i = tid; i < 128; i += kThreads) {
     // Local token index -> (row, column) inside the tile, row-major.
-    const int r = tid / p.tile_w, c = tid % p.tile_w;
-    off_y[tid] = tid < p.tile ? axis_offset(r, p.tile_h) : 0.f;
-    off_x[tid] = tid < p.tile ? axis_offset(c, p.tile_w) : 0.f;
+    const int r = i / p.tile_w, c = i % p.tile_w;
+    off_y[i] = i < p.tile ? axis_offset(r, p.tile_h) : 0.f;
+    off_x[i] = i < p.tile ? axis_offset(c, p.tile_w) : 0.f;
   }
   if (tid < kMaxTiles / 32) listed[tid] = 0u;
 
@@ -132,8 +132,17 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
   auto issue = [&](int kt, int half, unsigned char* dst) __attribute__((always_inline)) {
     const int key0 = (kt < 0 ? 0 : kt) * p.tile + half * kHalfKeys;
     const __amdgpu_buffer_rsrc_t rsrc = dsa::k_tile_rsrc(kbase, p.k_st, key0, p.tokens);
+    if constexpr (kWaves == 4) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dsa::lds_load16(rsrc, dst + (wave * 4 + j) * 1024, koff[j], 0);
+      for (int j = 0; j < 4; ++j) dsa::lds_load16(rsrc, dst + (wave * 4 + j) * 1024, koff[j], 0);
+    } else {
+      // The stage's 16 1-KB slices, dealt round-robin over the waves.
+      for (int i = wave; i < kKStage / 1024; i += kWaves) {
+        const int row = i * 4 + (lane >> 4);
+        dsa::lds_load16(rsrc, dst + i * 1024,
+                        (uint32_t)((row * (int)p.k_st + dsa::k2_swz(row, lane & 15) * 8) * 2), 0);
+      }
+    }
   };
 
   const int64_t cell0 = ((int64_t)h * p.tiles + qt) * p.tiles;
@@ -143,9 +152,11 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
   auto flush = [&](int j, int kt) __attribute__((always_inline)) {
     if (wave == 0 && lane < kStats && kt >= 0) {
       const float(*pr)[kStats] = part[j & 1];
-      auto total = [&](int s) {
-        return kWaves == 4 ? (pr[0][s] + pr[1][s]) + (pr[2][s] + pr[3][s])
-                           : (pr[0][s] + pr[1][s]) + pr[2][s];
+      auto total = [&](int s) {  // (w0 + w1) + (w2 + w3) over the waves present
+        if constexpr (kWaves == 1) return pr[0][s];
+        else if constexpr (kWaves == 2) return pr[0][s] + pr[1][s];
+        else if constexpr (kWaves == 3) return (pr[0][s] + pr[1][s]) + pr[2][s];
+        else return (pr[0][s] + pr[1][s]) + (pr[2][s] + pr[3][s]);
       };
       const float mass = total(0);
       const int64_t cell = cell0 + kt;
@@ -472,16 +483,24 @@ extern "C" int dsa_tile_stats(const void* q, const void* k, const int64_t* strid
       hipLaunchKernelGGL((tile_stats_kernel<true, 2, true, 4>), blocks, threads, 0, stream, p);
     else
       hipLaunchKernelGGL((tile_stats_kernel<false, 2, true, 4>), blocks, threads, 0, stream, p);
-  } else if (tile > kHalfKeys) {
+  } else if (tile > 96) {
     if (routed)
       hipLaunchKernelGGL((tile_stats_kernel<true, 2>), blocks, threads, 0, stream, p);
     else
       hipLaunchKernelGGL((tile_stats_kernel<false, 2>), blocks, threads, 0, stream, p);
-  } else {
+  } else if (tile > kHalfKeys) {
     if (routed)
-      hipLaunchKernelGGL((tile_stats_kernel<true, 1>), blocks, threads, 0, stream, p);
+      hipLaunchKernelGGL((tile_stats_kernel<true, 2, false, 3>), blocks, dim3(192), 0, stream, p);
     else
-      hipLaunchKernelGGL((tile_stats_kernel<false, 1>), blocks, threads, 0, stream, p);
+      hipLaunchKernelGGL((tile_stats_kernel<false, 2, false, 3>), blocks, dim3(192), 0, stream, p);
+  } else {
+    // Two waves even for tiles of at most 32 tokens (one of them then only
+    // stages K): one-wave workgroups, four per CU, leave too few waves to
+    // hide the dense pass's latency.
+    if (routed)
+      hipLaunchKernelGGL((tile_stats_kernel<true, 1, false, 2>), blocks, dim3(128), 0, stream, p);
+    else
+      hipLaunchKernelGGL((tile_stats_kernel<false, 1, false, 2>), blocks, dim3(128), 0, stream, p);
   }
   return dsa::check_launch("dsa_tile_stats");
 }
