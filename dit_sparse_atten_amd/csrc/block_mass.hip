@@ -38,11 +38,6 @@ struct BlockMassParams {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-  return v;
-}
 
 __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
@@ -121,7 +116,7 @@ __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
       }
     }
     if (sub & 1) {
-      const float total = wave_sum(acc0 + acc1);
+      const float total = dsa::wave_total(acc0 + acc1);
       if (lane == 0) part[(sub >> 1) & 1][wave] = total;
       acc0 = 0.f;
       acc1 = 0.f;
