@@ -31,12 +31,6 @@ constexpr int kRowsPerWave = 4;
 constexpr int kRowsPerGroup = kWaves * kRowsPerWave;
 constexpr int kMaxChunks = 16;  // dim <= 64 * 8 * 16 = 8192
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-  return v;
-}
-
 __device__ __forceinline__ void load8(const __bf16* src, float out[8]) {
   const dsa_bf16x8 v = *reinterpret_cast<const dsa_bf16x8*>(src);
 #pragma unroll
@@ -115,7 +109,7 @@ __global__ void __launch_bounds__(256) layernorm_modulate_kernel(LnParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) s += v[i][e];
       }
-    const float mean = wave_sum(s) / (float)p.dim;
+    const float mean = dsa::wave_total(s) / (float)p.dim;
     float q = 0.f;
 #pragma unroll
     for (int i = 0; i < kC; ++i)
@@ -126,7 +120,7 @@ __global__ void __launch_bounds__(256) layernorm_modulate_kernel(LnParams p) {
           q = fmaf(d, d, q);
         }
       }
-    const float rstd = rsqrtf(wave_sum(q) / (float)p.dim + p.eps);
+    const float rstd = rsqrtf(dsa::wave_total(q) / (float)p.dim + p.eps);
     const int64_t group_off = (int64_t)(row / p.rows_per_group) * p.dim;
     __bf16* out = p.out + (int64_t)row * p.out_stride;
 #pragma unroll
@@ -206,7 +200,7 @@ __global__ void __launch_bounds__(256) rmsnorm_rope_kernel(RmsRopeParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) q = fmaf(v[i][e], v[i][e], q);
       }
-    const float rstd = rsqrtf(wave_sum(q) / (float)p.dim + p.eps);
+    const float rstd = rsqrtf(dsa::wave_total(q) / (float)p.dim + p.eps);
     const float* cs_row =
         p.cos_sin ? p.cos_sin + (int64_t)(row % p.tokens) * p.head_dim : nullptr;
     __bf16* out = p.out + (int64_t)row * p.out_stride;
