@@ -173,9 +173,13 @@ __device__ __forceinline__ int quad_swap(int i) {
 // row r holds stream position quad_swap(r) and its V^T stage holds the
 // positions in order; the lane layout of S^T and P^T then matches the plain
 // layout in which the V^T workspace carries the quad swap instead.
-template <bool kRouted, int kNh, bool kSkip, bool kGather = false>
-__global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf16* vt,
-                                                          int32_t vt_keys) {
+//
+// kWaves: waves per workgroup, 32 query rows each (4; 2 for routed blocks of
+// at most 64 tokens, whose rows two waves cover: smaller workgroups spread
+// over the four SIMDs instead of leaving two waves per workgroup idle).
+template <bool kRouted, int kNh, bool kSkip, bool kGather = false, int kWaves = 4>
+__global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
+    bsa_fwd_kernel(BsaParams p, const __bf16* vt, int32_t vt_keys) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
@@ -227,11 +231,14 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
 
   const __bf16* kbase = p.k + b * p.k_sb + h * p.k_sh;
   const __bf16* vtbase = vt + ((int64_t)(b * p.heads + h) * kHeadDim) * vt_keys;
+  // Each wave stages kSlices of the 16 1-KB slices of a K or V^T stage.
+  static_assert(kWaves == 4 || (kWaves == 2 && !kGather), "2-wave groups: plain stream only");
+  constexpr int kSlices = 16 / kWaves;
   // Per-lane source offsets (elements) relative to the half-tile's first key.
-  int koff[4], voff[4];
+  int koff[kSlices], voff[kSlices];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = (wave * 4 + j) * 64 + lane;
+  for (int j = 0; j < kSlices; ++j) {
+    const int idx = (wave * kSlices + j) * 64 + lane;
     const int row = idx >> 4;
     koff[j] = row * (int)p.k_st + k2_swz(row, idx & 15) * 8;
     const int d = idx >> 3;
@@ -262,11 +269,12 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_kernel(BsaParams p, const __bf
     const int key0 = kbc * p.block + half * kHalfKeys;
     const __amdgpu_buffer_rsrc_t k_rsrc = k_tile_rsrc(kbase, p.k_st, key0, p.kv_tokens);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) lds_load16(k_rsrc, kdst + (wave * 4 + j) * 1024, koff[j] * 2, 0);
+    for (int j = 0; j < kSlices; ++j)
+      lds_load16(k_rsrc, kdst + (wave * kSlices + j) * 1024, koff[j] * 2, 0);
     const uint32_t vsoff = (uint32_t)(kbc * kNh + half) * (uint32_t)kKStage;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, voff[j] * 2, vsoff);
+    for (int j = 0; j < kSlices; ++j)
+      lds_load16(vt_rsrc, vdst + (wave * kSlices + j) * 1024, voff[j] * 2, vsoff);
   };
   // Stages the 64-key chunk that starts `o0` slots into stream block kb0 and
   // runs on into kb1 (the blocks are in range; pad and tail slots load
@@ -639,7 +647,7 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   p.scale = scale;
   p.scale_log2 = scale * 1.4426950408889634f;
   __bf16* vt = static_cast<__bf16*>(workspace);
-  const dim3 blocks((unsigned)grid), threads(256);
+  const dim3 blocks((unsigned)grid), threads(256), two_waves(128);
   const __bf16* vtc = vt;
   if (row_ptr && use_gather(block_size, kv_tokens, strides[4])) {
     // Whole blocks of 65..127 keys: the gathered key stream, whose V^T
@@ -664,7 +672,12 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   };
   if (row_ptr) {
     if (nh == 2) skip ? launch(bsa_fwd_kernel<true, 2, true>) : launch(bsa_fwd_kernel<true, 2, false>);
-    else skip ? launch(bsa_fwd_kernel<true, 1, true>) : launch(bsa_fwd_kernel<true, 1, false>);
+    else if (skip)
+      hipLaunchKernelGGL((bsa_fwd_kernel<true, 1, true, false, 2>), blocks, two_waves, 0, stream,
+                         p, vtc, vt_keys);
+    else
+      hipLaunchKernelGGL((bsa_fwd_kernel<true, 1, false, false, 2>), blocks, two_waves, 0, stream,
+                         p, vtc, vt_keys);
   } else {
     if (nh == 2) skip ? launch(bsa_fwd_kernel<false, 2, true>) : launch(bsa_fwd_kernel<false, 2, false>);
     else skip ? launch(bsa_fwd_kernel<false, 1, true>) : launch(bsa_fwd_kernel<false, 1, false>);
