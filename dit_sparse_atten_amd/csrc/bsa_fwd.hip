@@ -27,7 +27,12 @@
 //    MFMA operands are conflict-free 16-byte LDS reads;
 //  * online softmax with a lazily moved reference max (rescale only when a
 //    score exceeds it by 2^8); row sums add the fp32 P in plain VALU adds
-//    (v_dot2 would contend with the matrix core for issue).
+//    (v_dot2 would contend with the matrix core for issue); the row max and
+//    the final row sum pair lanes l and l ^ 32 with v_permlane32_swap;
+//  * query / key blocks of 1..128 tokens (the matrix-sparse backend's spatial
+//    tiles): routed whole blocks of 65..127 keys stream the row's kept blocks
+//    as one gathered key sequence (kGather), and routed blocks of at most 64
+//    tokens run 2-wave workgroups (kWaves).
 #include <type_traits>
 
 #include "bsa_tiles.h"
