@@ -194,6 +194,24 @@ def test_gathered_key_stream_long_rows(cuda_device, block, blocks, keep):
                                    rtol=1e-4)
 
 
+def test_gathered_key_stream_at_720p_tile_shape(cuda_device):
+    """The matrix-sparse backend's 720p call: 57,600 tokens in 800 tiles of
+    72 (9x8), rows of about 520 kept tiles (some 585 gathered chunks); a
+    sample of query tiles is checked against the float64 closed form."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    block, blocks, heads = 72, 800, 2
+    q, k, v = _inputs(1, block * blocks, heads, seed=720)
+    generator = torch.Generator().manual_seed(720)
+    route = torch.rand(heads, blocks, blocks, generator=generator) < 0.65
+    route[..., :50] = True
+    csr = csr_from_route(route.to(cuda_device), block_size=block)
+    out = bsa_fwd(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device), csr,
+                  block_size=block)
+    torch.cuda.synchronize()
+    rows = [(0, h, qb) for h in range(heads) for qb in (0, 1, 399, 555, 799)]
+    _check(out, q, k, v, route, block=block, rows=rows)
+
+
 def test_gathered_key_stream_skips_out_of_range_blocks(cuda_device):
     """Out-of-range key blocks in a CSR row are skipped (the documented
     contract) in the gathered stream too, wherever they fall in the row."""
