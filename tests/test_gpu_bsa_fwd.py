@@ -167,6 +167,33 @@ def test_tile_blocks_match_oracle(cuda_device, block, tokens):
     np.testing.assert_allclose(lse.cpu().numpy(), expected_lse, atol=1e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("whole", [True, False])
+def test_every_block_size_matches_oracle(cuda_device, whole):
+    """Every block size 1..128 through every kernel variant it selects
+    (one or two half-tiles, the 32-key sub-tile skip, the gathered stream for
+    whole blocks of 65..127 keys, 2-wave workgroups up to 64), with whole
+    blocks or a partial last block, against the float64 closed form."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    failures = []
+    for block in range(1, 129):
+        blocks = 5
+        tokens = blocks * block if whole else (blocks - 1) * block + max(1, block // 3)
+        q, k, v = _inputs(1, tokens, 1, seed=block)
+        generator = torch.Generator().manual_seed(block)
+        route = torch.rand(1, blocks, blocks, generator=generator) < 0.6
+        route[..., blocks - 1] = True  # the (possibly partial) last block in every row
+        csr = csr_from_route(route.to(cuda_device), block_size=block)
+        out = bsa_fwd(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device), csr,
+                      block_size=block)
+        torch.cuda.synchronize()
+        expected, _ = block_sparse_attention(q.float().numpy(), k.float().numpy(),
+                                             v.float().numpy(), route.numpy(), block)
+        metrics = summarize(out.float().cpu().numpy(), expected)
+        if metrics["max_absolute_error"] > MAX_ABS or metrics["cosine_similarity"] < MIN_COSINE:
+            failures.append((block, tokens, metrics))
+    assert not failures, failures
+
+
 @pytest.mark.parametrize("block,blocks,keep", [(72, 64, 0.7), (65, 40, 0.3), (100, 30, 0.9)])
 def test_gathered_key_stream_long_rows(cuda_device, block, blocks, keep):
     """Whole blocks of 65..127 keys stream the row's kept blocks as one

@@ -109,6 +109,38 @@ def test_routed_tile_attention_and_stats_match_oracle(ops, cuda_device, grid, ti
     assert (got["mass"].cpu().numpy()[~route] == 0).all()
 
 
+@pytest.mark.parametrize("routed", [True, False])
+def test_tile_stats_every_tile_size(ops, cuda_device, routed):
+    """Tiles of 1..128 tokens (as 1 x t rows, 5 tiles per head) through every
+    statistics variant they select (2, 3 or 4 waves; one or two half-tiles;
+    the gathered stream for 65..88 and 97..120) against the oracle."""
+    import types
+    failures = []
+    for t in range(1, 129):
+        tiles = 5
+        tokens = tiles * t
+        q, k, v = clustered_qkv(tokens, 2, 128, group=t, seed=t, dtype=torch.bfloat16)
+        case = types.SimpleNamespace(tile=t, tile_shape=(1, t))
+        qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+        if routed:
+            route = random_route(2, tiles, seed=t, keep=0.6).numpy()
+            route[..., tiles - 1] = True
+            csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=t)
+            _, lse = ops.bsa_fwd(qd, kd, vd, csr, return_lse=True, block_size=t)
+            got = ops.tile_stats(qd, kd, lse, (1, t), csr=csr)
+            expected, _ = _oracle_stats(case, q, k, v, route)
+        else:
+            _, lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
+            got = ops.tile_stats(qd, kd, lse, (1, t))
+            expected, _ = _oracle_stats(case, q, k, v)
+        torch.cuda.synchronize()
+        try:
+            _compare_stats(got, expected)
+        except AssertionError as error:
+            failures.append((t, str(error)[:200]))
+    assert not failures, failures
+
+
 def test_routed_tile_stats_skip_out_of_range_tiles(ops, cuda_device):
     """Out-of-range key tiles in a CSR row are skipped by the gathered
     statistics stream wherever they fall, and their cells stay zero."""
