@@ -56,7 +56,18 @@ struct BsaParams {
   int32_t block_pad; // gathered stream: key slots per block (block rounded up to 8)
   float scale;       // softmax scale applied to <q, k>
   float scale_log2;  // scale * log2(e)
+  // Split tail: workgroups from split_from on each compute one of `parts` key
+  // ranges of query block split_from + (wg - split_from) / parts and leave
+  // their unnormalised partial in `part` for bsa_merge_kernel.
+  int32_t split_from;
+  int32_t parts;
+  float* part;
 };
+
+// One split partial: O [128 rows][128 dims] relative to the row's reference
+// max, then m (log2 units of the scaled scores) and l per row, in fp32.
+constexpr int kPartFloats = 128 * 128 + 2 * 128;
+constexpr int kMaxPartGroups = 1024;  // split workgroups per call (two rounds of 512 slots)
 
 using dsa::kHeadDim;
 using dsa::kRowBytes;
@@ -203,7 +214,16 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // head to head (spatially local attention keeps from 0.2 to 0.65 per head)
   // would otherwise leave the XCDs holding the dense heads working alone
   // (5.7% of an end-to-end sparse step; 0.6% the other way on i.i.d. routes).
-  const int work = kRouted ? (int)blockIdx.x : dsa::xcd_remap(blockIdx.x, gridDim.x);
+  const int wg = (int)blockIdx.x;
+  const bool split = wg >= p.split_from;
+  int work, part = 0;
+  if (split) {
+    const int t = wg - p.split_from;
+    work = p.split_from + t / p.parts;
+    part = t % p.parts;
+  } else {
+    work = kRouted ? wg : dsa::xcd_remap(wg, p.split_from);
+  }
   const int qb = work % p.q_blocks;
   const int bh = work / p.q_blocks;
   const int h = bh % p.heads;
@@ -216,6 +236,11 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     const int64_t row = ((int64_t)rb * p.heads + h) * p.q_blocks + qb;
     start = rp[row];
     end = rp[row + 1];
+  }
+  if (split) {  // key part `part` of the row's blocks
+    const int n = end - start;
+    end = start + (int)((int64_t)n * (part + 1) / p.parts);
+    start = start + (int)((int64_t)n * part / p.parts);
   }
   const dsa_const_i32 cidx = (dsa_const_i32)p.col_idx;
   const int nblk = end - start;
@@ -520,6 +545,25 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   }
 
   const float l_tot = dsa::pair32_sum(l_run);
+  if (split) {
+    if (row_ok) {
+      float* po = p.part + (int64_t)(wg - p.split_from) * kPartFloats;
+      float* prow = po + local_row * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const dsa_f32x4 v4 = {oacc[dt][rr * 4 + 0], oacc[dt][rr * 4 + 1],
+                                oacc[dt][rr * 4 + 2], oacc[dt][rr * 4 + 3]};
+          *reinterpret_cast<dsa_f32x4*>(prow + dt * 32 + rr * 8 + g * 4) = v4;
+        }
+      if (g == 0) {
+        po[128 * 128 + local_row] = m_run;
+        po[128 * 128 + 128 + local_row] = l_tot;
+      }
+    }
+    return;
+  }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (row_ok) {
     __bf16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
@@ -541,7 +585,104 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   }
 }
 
+// Combines the `parts` partials of each split query block: with M the largest
+// row max, O = sum_i O_i 2^(m_i - M) / sum_i l_i 2^(m_i - M) and
+// LSE = M ln 2 + ln(sum_i l_i 2^(m_i - M)).  Two threads per row, 64 dims each.
+__global__ void __launch_bounds__(256) bsa_merge_kernel(BsaParams p) {
+  const int item = blockIdx.x;
+  const int work = p.split_from + item;
+  const int qb = work % p.q_blocks;
+  const int bh = work / p.q_blocks;
+  const int h = bh % p.heads;
+  const int b = bh / p.heads;
+  const int r = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const int tq = qb * p.block + r;
+  if (r >= p.block || tq >= p.q_tokens) return;
+  const float* base = p.part + (int64_t)item * p.parts * kPartFloats;
+  float m_max = -INFINITY;
+  for (int i = 0; i < p.parts; ++i) m_max = fmaxf(m_max, base[i * kPartFloats + 128 * 128 + r]);
+  float w[8];
+  float l = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    w[i] = 0.f;
+    if (i < p.parts) {
+      const float m_i = base[i * kPartFloats + 128 * 128 + r];
+      w[i] = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_max);
+      l = fmaf(w[i], base[i * kPartFloats + 128 * 128 + 128 + r], l);
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  __bf16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
+  for (int c = half * 8; c < half * 8 + 8; ++c) {  // 8-dim chunks of this thread's 64
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i >= p.parts) break;
+      const float* src = base + i * kPartFloats + r * kHeadDim + c * 8;
+      const dsa_f32x4 a = *reinterpret_cast<const dsa_f32x4*>(src);
+      const dsa_f32x4 bq = *reinterpret_cast<const dsa_f32x4*>(src + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[e] = fmaf(w[i], a[e], acc[e]);
+        acc[4 + e] = fmaf(w[i], bq[e], acc[4 + e]);
+      }
+    }
+    dsa_bf16x8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (__bf16)(acc[e] * inv);
+    *reinterpret_cast<dsa_bf16x8*>(orow + c * 8) = out;
+  }
+  if (p.lse && half == 0)
+    p.lse[((int64_t)b * p.heads + h) * p.q_tokens + tq] =
+        l > 0.f ? m_max * 0.6931471805599453f + logf(l) : -INFINITY;
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// Workgroup slots of one device (two attention workgroups per CU), cached.
+int device_slots() {
+  static int slots[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 0;
+  if (slots[device] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+      return 0;
+    slots[device] = 2 * cus;
+  }
+  return slots[device];
+}
+
+// Split of the last round: the last k of n query blocks each run as `parts`
+// key ranges, chosen to minimise the predicted time in rounds of one
+// workgroup's time, (n - k) / slots + ceil(parts k / slots) / parts, over k =
+// n mod slots (or that plus one round) and 2..8 parts, at most kMaxPartGroups
+// split workgroups.  Returns k (0: no split).
+int choose_split(int64_t n, int slots, int* parts) {
+  *parts = 1;
+  if (slots <= 0 || n <= 0) return 0;
+  const int64_t rem = n % slots;
+  if (rem == 0) return 0;
+  double best = (double)((n + slots - 1) / slots) - 0.05;  // split only for a clear gain
+  int best_k = 0;
+  for (int extra = 0; extra <= 1; ++extra) {
+    const int64_t k = rem + (int64_t)extra * slots;
+    if (k > n) break;
+    for (int pp = 2; pp <= 8; ++pp) {
+      if (k * pp > kMaxPartGroups) break;
+      const double t = (double)((n - k) / slots) +
+                       (double)((k * pp + slots - 1) / slots) / (double)pp;
+      if (t < best) {
+        best = t;
+        best_k = (int)k;
+        *parts = pp;
+      }
+    }
+  }
+  if (best_k == 0) *parts = 1;
+  return best_k;
+}
 
 // Routed calls take the gathered key stream when every key block is whole and
 // holds 65..127 keys and its 8-rounded size is below the plain layout's slots
@@ -563,6 +704,14 @@ int64_t vt_keys_for(int32_t kv_tokens, int32_t block) {
   return blocks * halves_per_block(block) * kHalfKeys;
 }
 
+// Bytes of the V^T workspace, rounded up to 256; the split partials follow.
+size_t split_offset(int32_t batch, int32_t heads, int32_t kv_tokens, int32_t head_dim,
+                    int32_t block) {
+  const size_t vt = (size_t)batch * heads * head_dim * vt_keys_for(kv_tokens, block) *
+                    sizeof(__bf16);
+  return (vt + 255) & ~(size_t)255;
+}
+
 }  // namespace
 
 extern "C" size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads,
@@ -570,7 +719,8 @@ extern "C" size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads,
                                                 int32_t block_size) {
   if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
   if (block_size <= 0 || block_size > 128) return 0;
-  return (size_t)batch * heads * head_dim * vt_keys_for(kv_tokens, block_size) * sizeof(__bf16);
+  return split_offset(batch, heads, kv_tokens, head_dim, block_size) +
+         (size_t)kMaxPartGroups * kPartFloats * sizeof(float);
 }
 
 extern "C" size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
@@ -615,8 +765,10 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
     return dsa::set_error(DSA_EUNSUPPORTED,
                           "dsa_bsa_fwd: key token stride %lld too large (64 rows must span < 2 GiB)",
                           (long long)strides[4]);
-  const size_t need = dsa_bsa_workspace_bytes_block(batch, heads, kv_tokens, head_dim,
-                                                    block_size);
+  // The V^T transpose needs this much; with the split partials' room as well
+  // (dsa_bsa_workspace_bytes_block) the last round of workgroups may split.
+  const size_t need = (size_t)batch * heads * head_dim *
+                      vt_keys_for(kv_tokens, block_size) * sizeof(__bf16);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return dsa::set_error(DSA_EINVAL,
                           "dsa_bsa_fwd: workspace of %zu bytes (16-byte aligned) required, got %zu",
@@ -652,7 +804,20 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   p.scale = scale;
   p.scale_log2 = scale * 1.4426950408889634f;
   __bf16* vt = static_cast<__bf16*>(workspace);
-  const dim3 blocks((unsigned)grid), threads(256), two_waves(128);
+  const size_t part_at = split_offset(batch, heads, kv_tokens, head_dim, block_size);
+  int parts = 1, split = 0;
+  if (workspace_bytes >= part_at + (size_t)kMaxPartGroups * kPartFloats * sizeof(float))
+    split = choose_split(grid, device_slots(), &parts);
+  p.split_from = (int32_t)grid - split;
+  p.parts = parts;
+  p.part = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + part_at);
+  const dim3 blocks((unsigned)(grid - split + (int64_t)split * parts)), threads(256),
+      two_waves(128);
+  auto finish = [&]() {
+    if (split > 0)
+      hipLaunchKernelGGL(bsa_merge_kernel, dim3((unsigned)split), dim3(256), 0, stream, p);
+    return dsa::check_launch("dsa_bsa_fwd");
+  };
   const __bf16* vtc = vt;
   if (row_ptr && use_gather(block_size, kv_tokens, strides[4])) {
     // Whole blocks of 65..127 keys: the gathered key stream, whose V^T
@@ -664,7 +829,7 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
                        block_size, p.block_pad, gather_keys);
     hipLaunchKernelGGL((bsa_fwd_kernel<true, 2, true, true>), blocks, threads, 0, stream, p,
                        vtc, gather_keys);
-    return dsa::check_launch("dsa_bsa_fwd");
+    return finish();
   }
   hipLaunchKernelGGL(vt_transpose_kernel, dim3((unsigned)(vt_keys / 64), (unsigned)(batch * heads)),
                      dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads, kv_tokens,
@@ -687,5 +852,5 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
     if (nh == 2) skip ? launch(bsa_fwd_kernel<false, 2, true>) : launch(bsa_fwd_kernel<false, 2, false>);
     else skip ? launch(bsa_fwd_kernel<false, 1, true>) : launch(bsa_fwd_kernel<false, 1, false>);
   }
-  return dsa::check_launch("dsa_bsa_fwd");
+  return finish();
 }

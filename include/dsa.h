@@ -49,9 +49,13 @@ const char* dsa_last_error(void);
  *                skipped; a row with no key blocks yields zeros.
  *   scale: softmax scale (d^-1/2 for softmax_scale=None).
  *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
- *   workspace: device scratch of dsa_bsa_workspace_bytes_block() bytes, 16-byte
- *                aligned, that receives the transposed V for this call; its
- *                contents need no initialisation and are dead after the call.
+ *   workspace: device scratch, 16-byte aligned, that receives the transposed V
+ *                for this call, plus (when it holds dsa_bsa_workspace_bytes_block()
+ *                bytes) the fp32 partials of query blocks in the last round of
+ *                workgroups, which then run as 2..8 key ranges merged by a second
+ *                launch; at least the transposed V's bytes (the function's value
+ *                less 68,157,440).  Contents need no initialisation and are dead
+ *                after the call.
  * Keys past kv_tokens in a partial last block are masked.
  */
 int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, const int64_t* strides,
@@ -60,14 +64,17 @@ int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, const int6
                 const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* Workspace bytes dsa_bsa_fwd needs with 128-token blocks (batch * heads *
- * head_dim * kv_tokens rounded up to 128, in bf16); 0 for invalid sizes.  No
- * counterpart in the reference, whose FlexAttention allocates internally. */
+/* Workspace bytes for dsa_bsa_fwd with 128-token blocks: the transposed V
+ * (batch * heads * head_dim * kv_tokens rounded up to 128, in bf16), rounded
+ * up to 256 bytes, plus 68,157,440 bytes for the split partials (1,024
+ * workgroups of 128 x 130 fp32); 0 for invalid sizes.  No counterpart in the
+ * reference, whose FlexAttention allocates internally. */
 size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
                                int32_t head_dim);
 
-/* The same for any block_size in 1..128: batch * heads * head_dim * 64 *
- * (key blocks * (block_size > 64 ? 2 : 1)) bf16 values; 0 for invalid sizes. */
+/* The same for any block_size in 1..128, whose transposed V holds batch *
+ * heads * head_dim * 64 * (key blocks * (block_size > 64 ? 2 : 1)) bf16
+ * values; 0 for invalid sizes. */
 size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_tokens,
                                      int32_t head_dim, int32_t block_size);
 

@@ -37,8 +37,14 @@ def test_header_symbols_are_exported_and_bound(lib):
 
 def test_version_and_workspace_size(lib):
     assert lib.dsa_version() == 1
-    # 2 x 12 heads x 128 dims x 32,760 tokens padded to 32,768, bf16.
-    assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == 2 * 12 * 128 * 32768 * 2
+    # 2 x 12 heads x 128 dims x 32,760 tokens padded to 32,768, bf16, then
+    # room for 1,024 split partials of 128 x (128 + 2) fp32.
+    split = 1024 * (128 * 128 + 256) * 4
+    assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == 2 * 12 * 128 * 32768 * 2 + split
+    # 72-token blocks: 10 key blocks of two 64-key halves; one 1-token block
+    # still takes one 64-key half.
+    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 720, 128, 72) == 128 * 1280 * 2 + split
+    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 1, 128, 1) == 128 * 64 * 2 + split
     assert lib.dsa_bsa_workspace_bytes(0, 12, 10, 128) == 0
 
 
