@@ -465,7 +465,8 @@ def main():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
     result["roofline"] = {
         "bound": "mfma",
-        "kernel": "bsa_fwd_kernel<true, 2, false, false> (event window also holds vt_transpose_kernel)",
+        "kernel": ("bsa_fwd_kernel<true, 2, false, false, 4> (event window also holds "
+                   "vt_transpose_kernel and the split-tail bsa_merge_kernel)"),
         "achieved": round(achieved, 2),
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
