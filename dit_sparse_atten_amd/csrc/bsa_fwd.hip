@@ -33,6 +33,7 @@
 //    tiles): routed whole blocks of 65..127 keys stream the row's kept blocks
 //    as one gathered key sequence (kGather), and routed blocks of at most 64
 //    tokens run 2-wave workgroups (kWaves).
+#include <algorithm>
 #include <type_traits>
 
 #include "bsa_tiles.h"
@@ -657,11 +658,11 @@ int device_slots() {
 // Split of the last round: the last k of n query blocks each run as `parts`
 // key ranges, chosen to minimise the predicted time in rounds of one
 // workgroup's time, (n - k) / slots + ceil(parts k / slots) / parts, over k =
-// n mod slots (or that plus one round) and 2..8 parts, at most kMaxPartGroups
-// split workgroups.  Returns k (0: no split).
-int choose_split(int64_t n, int slots, int* parts) {
+// n mod slots (or that plus one round) and 2..max_parts parts, at most
+// kMaxPartGroups split workgroups.  Returns k (0: no split).
+int choose_split(int64_t n, int slots, int max_parts, int* parts) {
   *parts = 1;
-  if (slots <= 0 || n <= 0) return 0;
+  if (slots <= 0 || n <= 0 || max_parts < 2) return 0;
   const int64_t rem = n % slots;
   if (rem == 0) return 0;
   double best = (double)((n + slots - 1) / slots) - 0.05;  // split only for a clear gain
@@ -669,7 +670,7 @@ int choose_split(int64_t n, int slots, int* parts) {
   for (int extra = 0; extra <= 1; ++extra) {
     const int64_t k = rem + (int64_t)extra * slots;
     if (k > n) break;
-    for (int pp = 2; pp <= 8; ++pp) {
+    for (int pp = 2; pp <= max_parts; ++pp) {
       if (k * pp > kMaxPartGroups) break;
       const double t = (double)((n - k) / slots) +
                        (double)((k * pp + slots - 1) / slots) / (double)pp;
@@ -807,7 +808,10 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   const size_t part_at = split_offset(batch, heads, kv_tokens, head_dim, block_size);
   int parts = 1, split = 0;
   if (workspace_bytes >= part_at + (size_t)kMaxPartGroups * kPartFloats * sizeof(float))
-    split = choose_split(grid, device_slots(), &parts);
+    // Parts of at least 8 key blocks (of the whole key range; routed rows
+    // are shorter): short key ranges, such as 512 text tokens, gain less
+    // than the merge costs.
+    split = choose_split(grid, device_slots(), std::min(8, kv_blocks / 8), &parts);
   p.split_from = (int32_t)grid - split;
   p.parts = parts;
   p.part = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + part_at);

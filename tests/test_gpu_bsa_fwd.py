@@ -239,6 +239,33 @@ def test_gathered_key_stream_at_720p_tile_shape(cuda_device):
     _check(out, q, k, v, route, block=block, rows=rows)
 
 
+@pytest.mark.parametrize("routed", [True, False])
+def test_split_last_round_matches_unsplit(cuda_device, monkeypatch, routed):
+    """With room for the split partials the last round of query blocks runs
+    as key ranges merged by a second launch (here 128 blocks of 64-block rows:
+    all of them, in 4 parts); with a transposed-V-only workspace the call runs
+    unsplit.  Both match the closed form, and each other closely."""
+    from dit_sparse_atten_amd import _lib
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    q, k, v = _inputs(1, 8192, 2, seed=64)
+    route = torch.rand(2, 64, 64, generator=torch.Generator().manual_seed(64)) < 0.5
+    route[..., 0] = True
+    csr = csr_from_route(route.to(cuda_device), block_size=128) if routed else None
+    qd, kd, vd = (t.to(cuda_device) for t in (q, k, v))
+    split_out, split_lse = bsa_fwd(qd, kd, vd, csr, return_lse=True)
+    lib = _lib.load()
+    full = lib.dsa_bsa_workspace_bytes_block
+    monkeypatch.setattr(lib, "dsa_bsa_workspace_bytes_block",
+                        lambda *args: full(*args) - 1024 * (128 * 128 + 256) * 4)
+    plain_out, plain_lse = bsa_fwd(qd, kd, vd, csr, return_lse=True)
+    torch.cuda.synchronize()
+    expected_route = route if routed else None
+    _check(split_out, q, k, v, expected_route)
+    _check(plain_out, q, k, v, expected_route)
+    assert (split_out.float() - plain_out.float()).abs().max().item() <= 8e-3
+    np.testing.assert_allclose(split_lse.cpu().numpy(), plain_lse.cpu().numpy(), atol=1e-4)
+
+
 def test_gathered_key_stream_skips_out_of_range_blocks(cuda_device):
     """Out-of-range key blocks in a CSR row are skipped (the documented
     contract) in the gathered stream too, wherever they fall in the row."""
