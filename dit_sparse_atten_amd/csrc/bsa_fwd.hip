@@ -32,7 +32,9 @@
 //  * query / key blocks of 1..128 tokens (the matrix-sparse backend's spatial
 //    tiles): routed whole blocks of 65..127 keys stream the row's kept blocks
 //    as one gathered key sequence (kGather), and routed blocks of at most 64
-//    tokens run 2-wave workgroups (kWaves).
+//    tokens run 2-wave workgroups (kWaves);
+//  * the last, partial round of query blocks may run as 2..8 key ranges each
+//    (choose_split), whose fp32 partials bsa_merge_kernel combines.
 #include <algorithm>
 #include <type_traits>
 
