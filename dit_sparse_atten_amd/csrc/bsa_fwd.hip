@@ -15,16 +15,17 @@
 //    v_mfma_f32_32x32x16_bf16 so each lane's accumulators belong to one query
 //    row (row max / sum stay in registers, one cross-half exchange) and P^T
 //    leaves the accumulators already in the B-operand layout of O^T = V^T P^T;
-//  * keys stream as 64-key half-tiles, double-buffered in LDS by direct
-//    buffer->LDS loads issued one half-tile ahead; the two stages are distinct
-//    LDS objects so reads of one never wait on the DMA into the other, and
-//    rows past the sequence end read as zeros (buffer range check);
-//  * V is first transposed into a V^T workspace tiled by 64-key half-tiles
-//    ([b, h][T/64][128 dims][64 keys], every half-tile 16 KB contiguous, so a
-//    stage load touches one contiguous block rather than 128 rows spread
-//    over the whole sequence); inside a half-tile the 16-key groups store
-//    their 4-key quads as 0, 2, 1, 3 (the key order of the P^T slots), so both
-//    MFMA operands are conflict-free 16-byte LDS reads;
+//  * keys stream as 64-key half-tiles of K and V, double-buffered in LDS by
+//    direct buffer->LDS loads issued one half-tile ahead; the two stages are
+//    distinct LDS objects so reads of one never wait on the DMA into the
+//    other, and rows past the sequence end read as zeros (buffer range check);
+//  * V is staged row-major like K, straight from the caller's tensor; the
+//    V^T A-operand fragments of O^T = V^T P^T come out of that stage through
+//    gfx950's transposing LDS read (ds_read_b64_tr_b16: in each 16-lane
+//    group, lane j receives element j % 4 of the 8 bytes that lane
+//    4 r + j / 4 addresses, r = 0..3), so no transposed copy of V exists;
+//    each lane addresses the 4-key quads in the order 0, 2, 1, 3 (the key
+//    order of the P^T slots);
 //  * online softmax with a lazily moved reference max (rescale only when a
 //    score exceeds it by 2^8); row sums add the fp32 P in plain VALU adds
 //    (v_dot2 would contend with the matrix core for issue); the row max and
@@ -84,102 +85,20 @@ typedef dsa::const_i32 dsa_const_i32;
 
 constexpr float kRescaleLog2 = 8.0f;  // move the max once p could exceed 2^8
 
-constexpr int kVtHalfRow = kHalfKeys * 2;  // 128 B: one head dim of a 64-key half-tile
+// V stage [64 keys][128 dims], row-major like K: the 16-byte chunk c of key
+// row r sits at chunk position c ^ v_swz_mask(r), masks 0, 6, 10, 12 for
+// r & 3 = 0..3.  One transposed read of a 16-lane group touches 4 consecutive
+// key rows x 32 bytes (two chunks); these masks give the 4 rows' segments
+// distinct bank groups, for 32 as for 64 four-byte banks per clock.
+__device__ __forceinline__ int v_swz_mask(int r) { return (0xCA60 >> (4 * (r & 3))) & 15; }
+__device__ __forceinline__ int v_swz(int r, int c) { return c ^ v_swz_mask(r); }
 
-// V^T LDS half-tile [128 dims][64 keys]: row d occupies one 128-byte bank half
-// (even / odd d alternate); chunk XOR ((d >> 1) & 7) spreads the 16 rows read
-// per 16 lanes over distinct bank groups.
-__device__ __forceinline__ int vt9_swz(int d, int c) { return c ^ ((d >> 1) & 7); }
+typedef __bf16 dsa_bf16x4_lds __attribute__((ext_vector_type(4)));
 
-// One workgroup per (b, h, 64-key chunk): rows of V through LDS, columns out.
-// Chunk c holds half-tile (c % nh) of key block (c / nh): keys
-// block * (c / nh) + 64 * (c % nh) + r for r < 64, zero past the block's end
-// or the sequence end (nh = 1 for blocks of at most 64 keys, else 2; with
-// 128-key blocks the chunks are simply consecutive 64-key ranges).
-__global__ void __launch_bounds__(256) vt_transpose_kernel(const __bf16* __restrict__ v,
-                                                           __bf16* __restrict__ vt,
-                                                           int64_t v_sb, int64_t v_st,
-                                                           int64_t v_sh, int32_t heads,
-                                                           int32_t tokens, int32_t block,
-                                                           int32_t nh, int32_t vt_keys) {
-  __shared__ __bf16 tile[64][kHeadDim + 8];  // +8 keeps column reads conflict-light
-  const int chunk = blockIdx.x;
-  const int bh = blockIdx.y;
-  const int b = bh / heads, h = bh % heads;
-  const int half = chunk % nh;
-  const int key0 = (chunk / nh) * block + half * 64;
-  int rows = min(64, block - half * 64);
-  rows = min(rows, tokens - key0);
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = j * 256 + tid;  // 64 rows x 16 chunks
-    const int r = idx >> 4, c = idx & 15;
-    dsa_u32x4 val = {0u, 0u, 0u, 0u};
-    if (r < rows)
-      val = *reinterpret_cast<const dsa_u32x4*>(v + b * v_sb + h * v_sh +
-                                                (int64_t)(key0 + r) * v_st + c * 8);
-    *reinterpret_cast<dsa_u32x4*>(&tile[r][c * 8]) = val;
-  }
-  dsa::lds_barrier();
-  __bf16* out = vt + ((int64_t)bh * kHeadDim) * vt_keys + (int64_t)chunk * 64 * kHeadDim;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = j * 256 + tid;  // 128 dims x 8 chunks of 8 slots
-    const int d = idx >> 3, c = idx & 7;
-    dsa_bf16x8 val;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int slot = c * 8 + e;        // logical slot inside the 64-key chunk
-      const int grp16 = slot >> 4;
-      // Slot quad q holds physical quad swap(q) (the swap is its own inverse).
-      const int s16 = slot & 15, q = s16 >> 2;
-      const int phys = grp16 * 16 + ((((q & 1) << 1) | (q >> 1)) << 2) + (s16 & 3);
-      val[e] = tile[phys][d];
-    }
-    *reinterpret_cast<dsa_bf16x8*>(out + d * 64 + c * 8) = val;
-  }
-}
-
-// V^T workspace of the gathered key stream: one WG per (key block, b, h)
-// writes the block's keys as [128 dims][block_pad] in plain key order, zeros
-// in the pad slots, so every 8-key group of a block is one 16-byte run.
-// Per (b, h): [kv_blocks][128][block_pad]; the host requires whole blocks.
-__global__ void __launch_bounds__(256) vt_blocks_kernel(const __bf16* __restrict__ v,
-                                                        __bf16* __restrict__ vt, int64_t v_sb,
-                                                        int64_t v_st, int64_t v_sh,
-                                                        int32_t heads, int32_t block,
-                                                        int32_t block_pad, int32_t vt_keys) {
-  __shared__ __bf16 tile[128][kHeadDim + 8];
-  const int kb = blockIdx.x;
-  const int bh = blockIdx.y;
-  const int b = bh / heads, h = bh % heads;
-  const int tid = threadIdx.x;
-  const __bf16* src = v + b * v_sb + h * v_sh + (int64_t)kb * block * v_st;
-  for (int idx = tid; idx < block * 16; idx += 256) {
-    const int r = idx >> 4, c = idx & 15;
-    *reinterpret_cast<dsa_u32x4*>(&tile[r][c * 8]) =
-        *reinterpret_cast<const dsa_u32x4*>(src + (int64_t)r * v_st + c * 8);
-  }
-  dsa::lds_barrier();
-  __bf16* out = vt + (int64_t)bh * kHeadDim * vt_keys + (int64_t)kb * kHeadDim * block_pad;
-  const int groups = block_pad >> 3;
-  for (int idx = tid; idx < kHeadDim * groups; idx += 256) {
-    const int d = idx / groups, c = idx - d * groups;
-    dsa_bf16x8 val;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int key = c * 8 + e;
-      val[e] = key < block ? tile[key][d] : (__bf16)0.0f;
-    }
-    *reinterpret_cast<dsa_bf16x8*>(out + d * block_pad + c * 8) = val;
-  }
-}
-
-// The 4-key quads of each 16-key group in the order 0, 2, 1, 3 (an involution).
-__device__ __forceinline__ int quad_swap(int i) {
-  const int q = (i >> 2) & 3;
-  return (i & ~15) | ((((q & 1) << 1) | (q >> 1)) << 2) | (i & 3);
+// ds_read_b64_tr_b16 at an LDS address.
+__device__ __forceinline__ dsa_bf16x4_lds lds_read_tr(const unsigned char* lds) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+      (__attribute__((address_space(3))) dsa_bf16x4_lds*)(lds));
 }
 
 // kRouted: key blocks from the CSR row (false: every key block, dense).
@@ -188,17 +107,16 @@ __device__ __forceinline__ int quad_swap(int i) {
 // sizes 65..96, or at most 32), so those steps run one 32-key sub-tile.
 // kGather (routed, whole blocks of 65..127 keys): the row's kept blocks are
 // concatenated, each padded to block_pad keys, and streamed as 64-key chunks,
-// so a 72-key block costs 72 key slots instead of 64 + 32.  A chunk's K stage
-// row r holds stream position quad_swap(r) and its V^T stage holds the
-// positions in order; the lane layout of S^T and P^T then matches the plain
-// layout in which the V^T workspace carries the quad swap instead.
+// so a 72-key block costs 72 key slots instead of 64 + 32.  Row r of a
+// chunk's K and V stages holds stream position r, so the S^T, P^T and V^T
+// lane layouts are those of the plain stream.
 //
 // kWaves: waves per workgroup, 32 query rows each (4; 2 for routed blocks of
 // at most 64 tokens, whose rows two waves cover: smaller workgroups spread
 // over the four SIMDs instead of leaving two waves per workgroup idle).
 template <bool kRouted, int kNh, bool kSkip, bool kGather = false, int kWaves = 4>
 __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
-    bsa_fwd_kernel(BsaParams p, const __bf16* vt, int32_t vt_keys) {
+    bsa_fwd_kernel(BsaParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
@@ -263,8 +181,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
 
   const __bf16* kbase = p.k + b * p.k_sb + h * p.k_sh;
-  const __bf16* vtbase = vt + ((int64_t)(b * p.heads + h) * kHeadDim) * vt_keys;
-  // Each wave stages kSlices of the 16 1-KB slices of a K or V^T stage.
+  const __bf16* vbase = p.v + b * p.v_sb + h * p.v_sh;
+  // Each wave stages kSlices of the 16 1-KB slices of a K or V stage.
   static_assert(kWaves == 4 || (kWaves == 2 && !kGather), "2-wave groups: plain stream only");
   constexpr int kSlices = 16 / kWaves;
   // Per-lane source offsets (elements) relative to the half-tile's first key.
@@ -274,18 +192,23 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     const int idx = (wave * kSlices + j) * 64 + lane;
     const int row = idx >> 4;
     koff[j] = row * (int)p.k_st + k2_swz(row, idx & 15) * 8;
-    const int d = idx >> 3;
-    voff[j] = d * kHalfKeys + vt9_swz(d, idx & 7) * 8;
+    voff[j] = row * (int)p.v_st + v_swz(row, idx & 15) * 8;
   }
 
-  // Gathered stream: the stream position of each K row this lane stages and
-  // the first position of each 8-key V^T group it stages.
-  int kpos[4], vpos[4];
+  // V^T fragment reads: lane (g, i = lane % 32) of the PV product needs dims
+  // 32 dt + i of the 16-key group's quads (2 g) and (2 g + 1) in slot order,
+  // i.e. key rows 4 g + r and 8 + 4 g + r (r = 0..3; the quad order 0, 2, 1, 3
+  // of the P^T slots).  In its 16-lane group, lane 4 r + c addresses key row
+  // 4 g + r, dims 32 dt + 16 ((lane >> 4) & 1) + 4 c .. + 3; the transposed
+  // read hands every lane its own dim of the 4 rows.  Byte offsets per dt.
+  int vfrag[4];
+  {
+    const int lam = lane & 15, r = lam >> 2, c = lam & 3;
+    const int row = 4 * g + r;
+    const int sub = 2 * ((lane >> 4) & 1) + (c >> 1);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = (wave * 4 + j) * 64 + lane;
-    kpos[j] = quad_swap(idx >> 4);
-    vpos[j] = vt9_swz(idx >> 3, idx & 7) * 8;
+    for (int dt = 0; dt < 4; ++dt)
+      vfrag[dt] = row * kRowBytes + v_swz(row, 4 * dt + sub) * 16 + (c & 1) * 8;
   }
 
   auto block_of = [&](int j) -> int {
@@ -294,47 +217,40 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
   };
 
-  const __amdgpu_buffer_rsrc_t vt_rsrc = make_rsrc(vtbase, (uint32_t)(kHeadDim * vt_keys * 2));
   // Stages half-tile `half` of key block kb (an invalid block stages block 0,
   // which is then fully masked).
   auto issue = [&](int kb, int half, unsigned char* kdst, unsigned char* vdst) {
     const int kbc = kb < 0 ? 0 : kb;
     const int key0 = kbc * p.block + half * kHalfKeys;
     const __amdgpu_buffer_rsrc_t k_rsrc = k_tile_rsrc(kbase, p.k_st, key0, p.kv_tokens);
+    const __amdgpu_buffer_rsrc_t v_rsrc = k_tile_rsrc(vbase, p.v_st, key0, p.kv_tokens);
 #pragma unroll
     for (int j = 0; j < kSlices; ++j)
       lds_load16(k_rsrc, kdst + (wave * kSlices + j) * 1024, koff[j] * 2, 0);
-    const uint32_t vsoff = (uint32_t)(kbc * kNh + half) * (uint32_t)kKStage;
 #pragma unroll
     for (int j = 0; j < kSlices; ++j)
-      lds_load16(vt_rsrc, vdst + (wave * kSlices + j) * 1024, voff[j] * 2, vsoff);
+      lds_load16(v_rsrc, vdst + (wave * kSlices + j) * 1024, voff[j] * 2, 0);
   };
   // Stages the 64-key chunk that starts `o0` slots into stream block kb0 and
   // runs on into kb1 (the blocks are in range; pad and tail slots load
   // whatever they address, or zeros past the end, and are masked).
   const __amdgpu_buffer_rsrc_t k_all_rsrc = make_rsrc(
       kbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.k_st * 2 + kRowBytes));
+  const __amdgpu_buffer_rsrc_t v_all_rsrc = make_rsrc(
+      vbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.v_st * 2 + kRowBytes));
   auto issue_gather = [&](int kb0, int kb1, int o0, unsigned char* kdst, unsigned char* vdst)
       __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int o = o0 + kpos[j];
+      const int row = (wave * 4 + j) * 4 + (lane >> 4);  // stream position o0 + row
+      const int o = o0 + row;
       const bool first = o < p.block_pad;
-      const int token = (first ? kb0 : kb1) * p.block + (first ? o : o - p.block_pad);
-      const int row = (wave * 4 + j) * 4 + (lane >> 4);
-      const uint32_t off = (uint32_t)token * (uint32_t)(p.k_st * 2) +
-                           (uint32_t)(k2_swz(row, lane & 15) * 16);
-      lds_load16(k_all_rsrc, kdst + (wave * 4 + j) * 1024, off, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int o = o0 + vpos[j];
-      const bool first = o < p.block_pad;
-      const int d = ((wave * 4 + j) * 64 + lane) >> 3;
-      const uint32_t slot = (uint32_t)((first ? kb0 : kb1) * kHeadDim + d) *
-                                (uint32_t)p.block_pad +
-                            (uint32_t)(first ? o : o - p.block_pad);
-      lds_load16(vt_rsrc, vdst + (wave * 4 + j) * 1024, slot * 2, 0);
+      const uint32_t token =
+          (uint32_t)((first ? kb0 : kb1) * p.block + (first ? o : o - p.block_pad));
+      lds_load16(k_all_rsrc, kdst + (wave * 4 + j) * 1024,
+                 token * (uint32_t)(p.k_st * 2) + (uint32_t)(k2_swz(row, lane & 15) * 16), 0);
+      lds_load16(v_all_rsrc, vdst + (wave * 4 + j) * 1024,
+                 token * (uint32_t)(p.v_st * 2) + (uint32_t)(v_swz(row, lane & 15) * 16), 0);
     }
   };
   // Valid keys of half-tile `half` of block kb (0 for an invalid block).
@@ -358,8 +274,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // at most 32 keys), so empty sub-tiles cost neither MFMAs nor softmax work.
   // Gathered stream: `invalid` has bit p set when stream position p of the
   // chunk is a pad slot, past the row's last key or in an out-of-range block;
-  // lane half g holds positions 32 kt + 16 (r >> 3) + 8 g + (r & 7).
-  auto compute = [&](const unsigned char* kt_lds, const unsigned char* vt_lds, int valid,
+  // accumulator r of lane half g holds position 32 kt + 8 (r >> 2) + 4 g + (r & 3).
+  auto compute = [&](const unsigned char* kt_lds, const unsigned char* v_lds, int valid,
                      uint64_t invalid, auto nkt_c) __attribute__((always_inline)) {
     constexpr int NKT = decltype(nkt_c)::value;
     dsa_f32x16 sacc[NKT];
@@ -379,13 +295,13 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     }
     if constexpr (kGather) {
       if (invalid != 0) {
-        const uint64_t mine = g ? invalid >> 8 : invalid;
+        const uint64_t mine = invalid >> (4 * g);
 #pragma unroll
         for (int kt = 0; kt < NKT; ++kt) {
           const uint32_t bits = (uint32_t)(mine >> (32 * kt));
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (bits & (1u << (16 * (r >> 3) + (r & 7)))) sacc[kt][r] = -INFINITY;
+            if (bits & (1u << (8 * (r >> 2) + (r & 3)))) sacc[kt][r] = -INFINITY;
         }
       }
     } else if (valid < NKT * 32) {
@@ -437,9 +353,11 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     for (int j = 0; j < 2 * NKT; ++j) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const int d = dt * 32 + qi;
-        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
-            vt_lds + d * kVtHalfRow + vt9_swz(d, 2 * j + g) * 16);
+        // Key rows 16 j + 4 g + r (slots 0..3) and 16 j + 8 + 4 g + r (4..7).
+        const unsigned char* at = v_lds + vfrag[dt] + j * 16 * kRowBytes;
+        const dsa_bf16x4_lds lo = lds_read_tr(at);
+        const dsa_bf16x4_lds hi = lds_read_tr(at + 8 * kRowBytes);
+        const dsa_bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[j], oacc[dt], 0, 0, 0);
       }
     }
@@ -643,11 +561,15 @@ __global__ void __launch_bounds__(256) bsa_merge_kernel(BsaParams p) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-// Workgroup slots of one device (two attention workgroups per CU), cached.
-int device_slots() {
+// Workgroup slots (two attention workgroups per CU) of the device `stream`
+// belongs to (the current device for the null stream), cached per device.
+int device_slots(hipStream_t stream) {
   static int slots[64] = {0};
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 0;
+  int device = -1;
+  if (stream == nullptr || hipStreamGetDevice(stream, &device) != hipSuccess) {
+    if (hipGetDevice(&device) != hipSuccess) return 0;
+  }
+  if (device < 0 || device >= 64) return 0;
   if (slots[device] == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
@@ -661,8 +583,8 @@ int device_slots() {
 // key ranges, chosen to minimise the predicted time in rounds of one
 // workgroup's time, (n - k) / slots + ceil(parts k / slots) / parts, over k =
 // n mod slots (or that plus one round) and 2..max_parts parts, at most
-// kMaxPartGroups split workgroups.  Returns k (0: no split).
-int choose_split(int64_t n, int slots, int max_parts, int* parts) {
+// max_groups split workgroups.  Returns k (0: no split).
+int choose_split(int64_t n, int slots, int max_parts, int64_t max_groups, int* parts) {
   *parts = 1;
   if (slots <= 0 || n <= 0 || max_parts < 2) return 0;
   const int64_t rem = n % slots;
@@ -673,7 +595,7 @@ int choose_split(int64_t n, int slots, int max_parts, int* parts) {
     const int64_t k = rem + (int64_t)extra * slots;
     if (k > n) break;
     for (int pp = 2; pp <= max_parts; ++pp) {
-      if (k * pp > kMaxPartGroups) break;
+      if (k * pp > max_groups) break;
       const double t = (double)((n - k) / slots) +
                        (double)((k * pp + slots - 1) / slots) / (double)pp;
       if (t < best) {
@@ -687,32 +609,119 @@ int choose_split(int64_t n, int slots, int max_parts, int* parts) {
   return best_k;
 }
 
+// Parts a split query block may take: at least 8 key blocks per part of the
+// whole key range (short ranges, such as 512 text tokens, gain less than the
+// merge costs), at most 8.
+int max_parts_for(int32_t kv_blocks) { return std::min(8, kv_blocks / 8); }
+
+constexpr size_t kPartBytes = sizeof(float) * kPartFloats;
+
 // Routed calls take the gathered key stream when every key block is whole and
 // holds 65..127 keys and its 8-rounded size is below the plain layout's slots
-// per block (64 + 32 up to 96 keys, else 128), and the whole K sequence of one
-// head spans < 2 GiB (one buffer resource addresses it).
-bool use_gather(int32_t block, int32_t kv_tokens, int64_t k_token_stride) {
+// per block (64 + 32 up to 96 keys, else 128), and the whole K and V
+// sequences of one head each span < 2 GiB (one buffer resource addresses each).
+bool use_gather(int32_t block, int32_t kv_tokens, int64_t k_token_stride,
+                int64_t v_token_stride) {
   if (block <= kHalfKeys || block >= 2 * kHalfKeys || kv_tokens % block != 0) return false;
   const int32_t pad = (block + 7) & ~7;
   const int32_t plain = block - kHalfKeys <= 32 ? kHalfKeys + 32 : 2 * kHalfKeys;
   if (pad >= plain) return false;
-  return ((int64_t)kv_tokens + 8) * k_token_stride * 2 + kRowBytes <= 0x7fffffff;
+  const int64_t stride = std::max(k_token_stride, v_token_stride);
+  return ((int64_t)kv_tokens + 8) * stride * 2 + kRowBytes <= 0x7fffffff;
 }
 
-// Half-tiles per key block, and keys of the per-(b, h) V^T workspace.
-int32_t halves_per_block(int32_t block) { return block > kHalfKeys ? 2 : 1; }
-
-int64_t vt_keys_for(int32_t kv_tokens, int32_t block) {
-  const int64_t blocks = (kv_tokens + block - 1) / block;
-  return blocks * halves_per_block(block) * kHalfKeys;
+// Validates the arguments of an attention call and fills `p` (without the
+// split fields).  Returns DSA_OK or the error status.
+int prepare(const void* q, const void* k, const void* v, void* o, const int64_t* strides,
+            int32_t batch, int32_t q_tokens, int32_t kv_tokens, int32_t heads,
+            int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
+            const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
+            const char* who, BsaParams* p) {
+  if (!q || !k || !v || !o || !strides)
+    return dsa::set_error(DSA_EINVAL, "%s: null tensor or stride pointer", who);
+  if (batch <= 0 || heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
+    return dsa::set_error(DSA_EINVAL, "%s: batch/heads/tokens must be positive", who);
+  if (head_dim != kHeadDim)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: head_dim %d unsupported (128 only)", who,
+                          head_dim);
+  if (block_size <= 0 || block_size > 128)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: block_size %d unsupported (1..128)", who,
+                          block_size);
+  if ((row_ptr == nullptr) != (col_idx == nullptr))
+    return dsa::set_error(DSA_EINVAL, "%s: row_ptr and col_idx must both be set or null", who);
+  if (row_ptr && route_batches != 1 && route_batches != batch)
+    return dsa::set_error(DSA_EINVAL, "%s: route_batches must be 1 or batch", who);
+  if (row_ptr && q_tokens != kv_tokens)
+    return dsa::set_error(DSA_EINVAL, "%s: a block route needs q_tokens == kv_tokens", who);
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return dsa::set_error(DSA_EINVAL, "%s: scale must be positive and finite", who);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return dsa::set_error(DSA_EINVAL, "%s: tensors must be 16-byte aligned", who);
+  for (int i = 0; i < 12; ++i)
+    if (strides[i] % 8 != 0 || strides[i] < 0)
+      return dsa::set_error(DSA_EINVAL,
+                            "%s: stride %d (=%lld) is not a non-negative multiple of 8 "
+                            "elements", who, i, (long long)strides[i]);
+  if (strides[4] * (int64_t)(2 * 64) > 0x7fffffff || strides[7] * (int64_t)(2 * 64) > 0x7fffffff)
+    return dsa::set_error(DSA_EUNSUPPORTED,
+                          "%s: key/value token stride too large (64 rows must span < 2 GiB)", who);
+  const int32_t q_blocks = (q_tokens + block_size - 1) / block_size;
+  const int32_t kv_blocks = (kv_tokens + block_size - 1) / block_size;
+  const int64_t grid = (int64_t)batch * heads * q_blocks;
+  if (grid > 0x3fffffff || (int64_t)batch * heads > 65535)
+    return dsa::set_error(DSA_EINVAL, "%s: grid too large", who);
+  p->q = static_cast<const __bf16*>(q);
+  p->k = static_cast<const __bf16*>(k);
+  p->v = static_cast<const __bf16*>(v);
+  p->o = static_cast<__bf16*>(o);
+  p->lse = lse;
+  p->q_sb = strides[0]; p->q_st = strides[1]; p->q_sh = strides[2];
+  p->k_sb = strides[3]; p->k_st = strides[4]; p->k_sh = strides[5];
+  p->v_sb = strides[6]; p->v_st = strides[7]; p->v_sh = strides[8];
+  p->o_sb = strides[9]; p->o_st = strides[10]; p->o_sh = strides[11];
+  p->row_ptr = row_ptr;
+  p->col_idx = col_idx;
+  p->batch = batch; p->heads = heads; p->q_tokens = q_tokens; p->kv_tokens = kv_tokens;
+  p->q_blocks = q_blocks; p->kv_blocks = kv_blocks;
+  p->route_batches = row_ptr ? route_batches : 1;
+  p->block = block_size;
+  p->block_pad = (block_size + 7) & ~7;
+  p->scale = scale;
+  p->scale_log2 = scale * 1.4426950408889634f;
+  return DSA_OK;
 }
 
-// Bytes of the V^T workspace, rounded up to 256; the split partials follow.
-size_t split_offset(int32_t batch, int32_t heads, int32_t kv_tokens, int32_t head_dim,
-                    int32_t block) {
-  const size_t vt = (size_t)batch * heads * head_dim * vt_keys_for(kv_tokens, block) *
-                    sizeof(__bf16);
-  return (vt + 255) & ~(size_t)255;
+// Launches the attention of a prepared call.  `part` holds room for
+// `part_groups` split partials (0: the call runs unsplit).
+int launch(BsaParams p, float* part, int64_t part_groups, hipStream_t stream, const char* who) {
+  const int64_t grid = (int64_t)p.batch * p.heads * p.q_blocks;
+  int parts = 1;
+  const int split = choose_split(grid, device_slots(stream), max_parts_for(p.kv_blocks),
+                                 std::min<int64_t>(part_groups, kMaxPartGroups), &parts);
+  p.split_from = (int32_t)(grid - split);
+  p.parts = parts;
+  p.part = part;
+  const dim3 blocks((unsigned)(grid - split + (int64_t)split * parts)), threads(256),
+      two_waves(128);
+  const int32_t nh = p.block > kHalfKeys ? 2 : 1;
+  // Blocks whose last half-tile holds 1..32 keys run it as one sub-tile.
+  const int rem = p.block % kHalfKeys;
+  const bool skip = rem != 0 && rem <= 32;
+  auto four = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p); };
+  auto two = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, two_waves, 0, stream, p); };
+  if (p.row_ptr && use_gather(p.block, p.kv_tokens, p.k_st, p.v_st)) {
+    four(bsa_fwd_kernel<true, 2, true, true>);
+  } else if (p.row_ptr) {
+    if (nh == 2) skip ? four(bsa_fwd_kernel<true, 2, true>) : four(bsa_fwd_kernel<true, 2, false>);
+    else skip ? two(bsa_fwd_kernel<true, 1, true, false, 2>)
+              : two(bsa_fwd_kernel<true, 1, false, false, 2>);
+  } else {
+    if (nh == 2) skip ? four(bsa_fwd_kernel<false, 2, true>) : four(bsa_fwd_kernel<false, 2, false>);
+    else skip ? four(bsa_fwd_kernel<false, 1, true>) : four(bsa_fwd_kernel<false, 1, false>);
+  }
+  if (split > 0)
+    hipLaunchKernelGGL(bsa_merge_kernel, dim3((unsigned)split), dim3(256), 0, stream, p);
+  return dsa::check_launch(who);
 }
 
 }  // namespace
@@ -722,8 +731,8 @@ extern "C" size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads,
                                                 int32_t block_size) {
   if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
   if (block_size <= 0 || block_size > 128) return 0;
-  return split_offset(batch, heads, kv_tokens, head_dim, block_size) +
-         (size_t)kMaxPartGroups * kPartFloats * sizeof(float);
+  const int32_t kv_blocks = (kv_tokens + block_size - 1) / block_size;
+  return max_parts_for(kv_blocks) >= 2 ? (size_t)kMaxPartGroups * kPartBytes : 0;
 }
 
 extern "C" size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
@@ -739,124 +748,13 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
                            float* lse, void* workspace, size_t workspace_bytes,
                            hipStream_t stream) {
   dsa::clear_error();
-  if (!q || !k || !v || !o || !strides)
-    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: null tensor or stride pointer");
-  if (batch <= 0 || heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
-    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: batch/heads/tokens must be positive");
-  if (head_dim != kHeadDim)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_bsa_fwd: head_dim %d unsupported (128 only)",
-                          head_dim);
-  if (block_size <= 0 || block_size > 128)
-    return dsa::set_error(DSA_EUNSUPPORTED,
-                          "dsa_bsa_fwd: block_size %d unsupported (1..128)", block_size);
-  if ((row_ptr == nullptr) != (col_idx == nullptr))
-    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: row_ptr and col_idx must both be set or null");
-  if (row_ptr && route_batches != 1 && route_batches != batch)
-    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: route_batches must be 1 or batch");
-  if (row_ptr && q_tokens != kv_tokens)
-    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: a block route needs q_tokens == kv_tokens");
-  if (!(scale > 0.f) || !std::isfinite(scale))
-    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: scale must be positive and finite");
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
-    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: tensors must be 16-byte aligned");
-  for (int i = 0; i < 12; ++i)
-    if (strides[i] % 8 != 0 || strides[i] < 0)
-      return dsa::set_error(DSA_EINVAL,
-                            "dsa_bsa_fwd: stride %d (=%lld) is not a non-negative multiple of 8 "
-                            "elements", i, (long long)strides[i]);
-  if (strides[4] * (int64_t)(2 * 64) > 0x7fffffff)
-    return dsa::set_error(DSA_EUNSUPPORTED,
-                          "dsa_bsa_fwd: key token stride %lld too large (64 rows must span < 2 GiB)",
-                          (long long)strides[4]);
-  // The V^T transpose needs this much; with the split partials' room as well
-  // (dsa_bsa_workspace_bytes_block) the last round of workgroups may split.
-  const size_t need = (size_t)batch * heads * head_dim *
-                      vt_keys_for(kv_tokens, block_size) * sizeof(__bf16);
-  if (!workspace || workspace_bytes < need || !aligned16(workspace))
-    return dsa::set_error(DSA_EINVAL,
-                          "dsa_bsa_fwd: workspace of %zu bytes (16-byte aligned) required, got %zu",
-                          need, workspace_bytes);
-  const int32_t q_blocks = (q_tokens + block_size - 1) / block_size;
-  const int32_t kv_blocks = (kv_tokens + block_size - 1) / block_size;
-  const int32_t nh = halves_per_block(block_size);
-  const int64_t vt_keys64 = vt_keys_for(kv_tokens, block_size);
-  const int64_t grid = (int64_t)batch * heads * q_blocks;
-  if (grid > 0x7fffffff || (int64_t)batch * heads > 65535)
-    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: grid too large");
-  if ((int64_t)kHeadDim * vt_keys64 * 2 > 0x7fffffff)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_bsa_fwd: kv_tokens too large");
-  const int32_t vt_keys = (int32_t)vt_keys64;
-
   BsaParams p;
-  p.q = static_cast<const __bf16*>(q);
-  p.k = static_cast<const __bf16*>(k);
-  p.v = static_cast<const __bf16*>(v);
-  p.o = static_cast<__bf16*>(o);
-  p.lse = lse;
-  p.q_sb = strides[0]; p.q_st = strides[1]; p.q_sh = strides[2];
-  p.k_sb = strides[3]; p.k_st = strides[4]; p.k_sh = strides[5];
-  p.v_sb = strides[6]; p.v_st = strides[7]; p.v_sh = strides[8];
-  p.o_sb = strides[9]; p.o_st = strides[10]; p.o_sh = strides[11];
-  p.row_ptr = row_ptr;
-  p.col_idx = col_idx;
-  p.batch = batch; p.heads = heads; p.q_tokens = q_tokens; p.kv_tokens = kv_tokens;
-  p.q_blocks = q_blocks; p.kv_blocks = kv_blocks;
-  p.route_batches = row_ptr ? route_batches : 1;
-  p.block = block_size;
-  p.block_pad = (block_size + 7) & ~7;
-  p.scale = scale;
-  p.scale_log2 = scale * 1.4426950408889634f;
-  __bf16* vt = static_cast<__bf16*>(workspace);
-  const size_t part_at = split_offset(batch, heads, kv_tokens, head_dim, block_size);
-  int parts = 1, split = 0;
-  if (workspace_bytes >= part_at + (size_t)kMaxPartGroups * kPartFloats * sizeof(float))
-    // Parts of at least 8 key blocks (of the whole key range; routed rows
-    // are shorter): short key ranges, such as 512 text tokens, gain less
-    // than the merge costs.
-    split = choose_split(grid, device_slots(), std::min(8, kv_blocks / 8), &parts);
-  p.split_from = (int32_t)grid - split;
-  p.parts = parts;
-  p.part = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + part_at);
-  const dim3 blocks((unsigned)(grid - split + (int64_t)split * parts)), threads(256),
-      two_waves(128);
-  auto finish = [&]() {
-    if (split > 0)
-      hipLaunchKernelGGL(bsa_merge_kernel, dim3((unsigned)split), dim3(256), 0, stream, p);
-    return dsa::check_launch("dsa_bsa_fwd");
-  };
-  const __bf16* vtc = vt;
-  if (row_ptr && use_gather(block_size, kv_tokens, strides[4])) {
-    // Whole blocks of 65..127 keys: the gathered key stream, whose V^T
-    // workspace ([kv_blocks][128][block_pad] per (b, h)) fits in the plain
-    // one because block_pad is below that layout's slots per block.
-    const int32_t gather_keys = kv_blocks * p.block_pad;
-    hipLaunchKernelGGL(vt_blocks_kernel, dim3((unsigned)kv_blocks, (unsigned)(batch * heads)),
-                       dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads,
-                       block_size, p.block_pad, gather_keys);
-    hipLaunchKernelGGL((bsa_fwd_kernel<true, 2, true, true>), blocks, threads, 0, stream, p,
-                       vtc, gather_keys);
-    return finish();
-  }
-  hipLaunchKernelGGL(vt_transpose_kernel, dim3((unsigned)(vt_keys / 64), (unsigned)(batch * heads)),
-                     dim3(256), 0, stream, p.v, vt, p.v_sb, p.v_st, p.v_sh, heads, kv_tokens,
-                     block_size, nh, vt_keys);
-  // Blocks whose last half-tile holds 1..32 keys run it as one sub-tile.
-  const int rem = block_size % kHalfKeys;
-  const bool skip = rem != 0 && rem <= 32;
-  auto launch = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p, vtc, vt_keys);
-  };
-  if (row_ptr) {
-    if (nh == 2) skip ? launch(bsa_fwd_kernel<true, 2, true>) : launch(bsa_fwd_kernel<true, 2, false>);
-    else if (skip)
-      hipLaunchKernelGGL((bsa_fwd_kernel<true, 1, true, false, 2>), blocks, two_waves, 0, stream,
-                         p, vtc, vt_keys);
-    else
-      hipLaunchKernelGGL((bsa_fwd_kernel<true, 1, false, false, 2>), blocks, two_waves, 0, stream,
-                         p, vtc, vt_keys);
-  } else {
-    if (nh == 2) skip ? launch(bsa_fwd_kernel<false, 2, true>) : launch(bsa_fwd_kernel<false, 2, false>);
-    else skip ? launch(bsa_fwd_kernel<false, 1, true>) : launch(bsa_fwd_kernel<false, 1, false>);
-  }
-  return finish();
+  const int status = prepare(q, k, v, o, strides, batch, q_tokens, kv_tokens, heads, head_dim,
+                             block_size, row_ptr, col_idx, route_batches, scale, lse,
+                             "dsa_bsa_fwd", &p);
+  if (status != DSA_OK) return status;
+  if (workspace_bytes > 0 && (!workspace || !aligned16(workspace)))
+    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: workspace must be 16-byte aligned");
+  return launch(p, static_cast<float*>(workspace), (int64_t)(workspace_bytes / kPartBytes),
+                stream, "dsa_bsa_fwd");
 }

@@ -1,8 +1,10 @@
 """Build libdsa.so (all HIP kernels + the C-ABI) for gfx950 with hipcc.
 
 Usage: ``python -m dit_sparse_atten_amd.csrc.build`` or ``build_library()``.
-The library is written next to the package (``dit_sparse_atten_amd/libdsa.so``)
-so it travels with the source tree.
+Every source is compiled to its own object in parallel (the kernels of one
+file never call device code of another), then the objects are linked into
+``dit_sparse_atten_amd/libdsa.so`` next to the package, so the library
+travels with the source tree.
 """
 
 from __future__ import annotations
@@ -11,12 +13,14 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 CSRC = Path(__file__).resolve().parent
 PACKAGE = CSRC.parent
 INCLUDE = PACKAGE.parent / "include"
 LIBRARY = PACKAGE / "libdsa.so"
+OBJECTS = PACKAGE / "_build"
 SOURCES = (
     "dsa_api.hip",
     "bsa_fwd.hip",
@@ -40,10 +44,10 @@ HIPCC_FLAGS = (
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 )
+_NOISE = "is not a recognized feature for this target"
 
 
 def hipcc_path() -> str:
@@ -54,21 +58,32 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found; set HIPCC or install ROCm")
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compile every HIP source into one shared library and return its path."""
-    sources = [str(CSRC / name) for name in SOURCES]
-    tmp = LIBRARY.with_suffix(".so.tmp")
-    command = [hipcc_path(), *HIPCC_FLAGS, "-I", str(CSRC), "-I", str(INCLUDE), "-o", str(tmp), *sources]
+def _run(command, verbose):
     if verbose:
         print(" ".join(command), flush=True)
     result = subprocess.run(command, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
     messages = [line for line in (result.stdout + result.stderr).splitlines()
-                if noise not in line]
+                if _NOISE not in line]
     if result.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + "\n".join(messages))
     if verbose and messages:
         print("\n".join(messages), flush=True)
+
+
+def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source into one shared library and return its path."""
+    hipcc = hipcc_path()
+    OBJECTS.mkdir(exist_ok=True)
+    objects = [OBJECTS / (Path(name).stem + ".o") for name in SOURCES]
+    commands = [[hipcc, *HIPCC_FLAGS, "-I", str(CSRC), "-I", str(INCLUDE), "-c",
+                 str(CSRC / name), "-o", str(obj)] for name, obj in zip(SOURCES, objects)]
+    jobs = jobs or min(len(commands), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        for future in [pool.submit(_run, command, verbose) for command in commands]:
+            future.result()
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp),
+          *map(str, objects)], verbose)
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

@@ -155,8 +155,10 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
         raise ValueError(f"block_size {block_size} unsupported (1..128)")
     workspace_bytes = lib.dsa_bsa_workspace_bytes_block(batch, heads, kv_tokens, head_dim,
                                                         block_size)
-    # Transposed-V scratch for this call; the caching allocator recycles it.
-    workspace = torch.empty(max(workspace_bytes, 16), dtype=torch.uint8, device=q.device)
+    # Room for the split partials of the last round of workgroups (none when
+    # the key range is too short to split); the caching allocator recycles it.
+    workspace = (torch.empty(workspace_bytes, dtype=torch.uint8, device=q.device)
+                 if workspace_bytes else None)
     with torch.cuda.device(q.device):
         status = lib.dsa_bsa_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), strides,
@@ -165,7 +167,8 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
             col_idx.data_ptr() if col_idx is not None else None,
             route_batches, float(scale),
             lse.data_ptr() if lse is not None else None,
-            workspace.data_ptr(), workspace.numel(), _stream_handle(q.device))
+            workspace.data_ptr() if workspace is not None else None, workspace_bytes,
+            _stream_handle(q.device))
     _lib.check(status, "dsa_bsa_fwd")
     return (out, lse) if return_lse else out
 

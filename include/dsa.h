@@ -49,13 +49,16 @@ const char* dsa_last_error(void);
  *                skipped; a row with no key blocks yields zeros.
  *   scale: softmax scale (d^-1/2 for softmax_scale=None).
  *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
- *   workspace: device scratch, 16-byte aligned, that receives the transposed V
- *                for this call, plus (when it holds dsa_bsa_workspace_bytes_block()
- *                bytes) the fp32 partials of query blocks in the last round of
- *                workgroups, which then run as 2..8 key ranges merged by a second
- *                launch; at least the transposed V's bytes (the function's value
- *                less 68,157,440).  Contents need no initialisation and are dead
- *                after the call.
+ *   workspace: optional device scratch (NULL with workspace_bytes == 0, or
+ *                16-byte aligned) for the fp32 partials of the query blocks in
+ *                the last, partial round of workgroups (two per CU of the
+ *                stream's device), which then run as 2..8 key ranges merged by
+ *                a second launch.  The split takes at most workspace_bytes /
+ *                66,560 partials (128 x 130 fp32 each) and at most 1,024; with
+ *                less room (none: unsplit) the result can differ in the last
+ *                bits, since the fp32 accumulation order differs.  Contents
+ *                need no initialisation and are dead after the call.  V is read
+ *                in place; no transposed copy is made.
  * Keys past kv_tokens in a partial last block are masked.
  */
 int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, const int64_t* strides,
@@ -64,17 +67,16 @@ int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, const int6
                 const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* Workspace bytes for dsa_bsa_fwd with 128-token blocks: the transposed V
- * (batch * heads * head_dim * kv_tokens rounded up to 128, in bf16), rounded
- * up to 256 bytes, plus 68,157,440 bytes for the split partials (1,024
- * workgroups of 128 x 130 fp32); 0 for invalid sizes.  No counterpart in the
- * reference, whose FlexAttention allocates internally. */
+/* Workspace bytes that let dsa_bsa_fwd with 128-token blocks split its last
+ * round as far as it ever does: 68,157,440 (1,024 partials of 128 x 130
+ * fp32) when the key range holds at least 16 blocks (two parts of at least 8
+ * key blocks each), else 0 (the call never splits, e.g. over 512 text
+ * tokens); 0 for invalid sizes.  No counterpart in the reference, whose
+ * FlexAttention allocates internally. */
 size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
                                int32_t head_dim);
 
-/* The same for any block_size in 1..128, whose transposed V holds batch *
- * heads * head_dim * 64 * (key blocks * (block_size > 64 ? 2 : 1)) bf16
- * values; 0 for invalid sizes. */
+/* The same for any block_size in 1..128 (key blocks of block_size tokens). */
 size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_tokens,
                                      int32_t head_dim, int32_t block_size);
 

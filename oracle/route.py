@@ -53,17 +53,19 @@ def sample_indices(tokens, block_size, samples):
     return block_ids[:, None] * block_size + local, sizes
 
 
-def sampled_block_mass(q, k, block_size, samples, scale=None, bf16_scores=True):
+def sampled_block_mass(q, k, block_size, samples, scale=None, bf16_scores=True,
+                       query_blocks=None):
     """Sampled estimate of per-(head, q-block, k-block) attention mass.
 
     q, k: [1, T, H, D] arrays (values already representable in the input
     dtype).  With ``bf16_scores`` the scores are rounded to bfloat16 after the
     dot product and again after the scale multiply, as a bf16 matmul followed
     by a bf16 multiply does (flex.py:245); the softmax runs on float64 here
-    (float32 in the reference).  Returns mass [H, blocks, blocks] float64.
+    (float32 in the reference).  Returns mass [H, blocks, blocks] float64, or,
+    with ``query_blocks`` (a list of query-block ids), only those rows:
+    [H, len(query_blocks), blocks].  Every row is a softmax over all sampled
+    keys, so a row does not depend on which other rows are evaluated.
     """
-    q = np.asarray(q, dtype=np.float64)
-    k = np.asarray(k, dtype=np.float64)
     if q.shape[0] != 1 or q.shape[1] != k.shape[1]:
         raise ValueError("sampled route update supports batch-1 self-attention")
     if samples <= 0 or samples > block_size:
@@ -71,8 +73,10 @@ def sampled_block_mass(q, k, block_size, samples, scale=None, bf16_scores=True):
     tokens, heads, head_dim = q.shape[1:]
     indices, sizes = sample_indices(tokens, block_size, samples)
     blocks = indices.shape[0]
-    sampled_q = q[0, indices.reshape(-1)].transpose(1, 0, 2)  # [H, blocks*S, D]
-    sampled_k = k[0, indices.reshape(-1)].transpose(1, 0, 2)
+    q_indices = indices if query_blocks is None else indices[np.asarray(query_blocks)]
+    # Only the sampled tokens are converted to float64.
+    sampled_q = np.asarray(q[0, q_indices.reshape(-1)], dtype=np.float64).transpose(1, 0, 2)
+    sampled_k = np.asarray(k[0, indices.reshape(-1)], dtype=np.float64).transpose(1, 0, 2)
     log_weights = np.log(
         (sizes.astype(np.float32) / np.float32(samples)).astype(np.float32)).astype(np.float32)
     log_weights = np.repeat(log_weights, samples).astype(np.float64)
@@ -88,7 +92,8 @@ def sampled_block_mass(q, k, block_size, samples, scale=None, bf16_scores=True):
     logits -= logits.max(-1, keepdims=True)
     weights = np.exp(logits)
     probabilities = weights / weights.sum(-1, keepdims=True)
-    return probabilities.reshape(heads, blocks, samples, blocks, samples).sum(-1).mean(2)
+    rows = q_indices.shape[0]
+    return probabilities.reshape(heads, rows, samples, blocks, samples).sum(-1).mean(2)
 
 
 def _fixed(row):

@@ -37,14 +37,18 @@ def test_header_symbols_are_exported_and_bound(lib):
 
 def test_version_and_workspace_size(lib):
     assert lib.dsa_version() == 1
-    # 2 x 12 heads x 128 dims x 32,760 tokens padded to 32,768, bf16, then
-    # room for 1,024 split partials of 128 x (128 + 2) fp32.
+    # The workspace holds only the split partials of the last round: 1,024
+    # workgroups of 128 x (128 + 2) fp32, when the key range can be split
+    # (at least 16 key blocks, 2 parts of 8); V is read in place.
     split = 1024 * (128 * 128 + 256) * 4
-    assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == 2 * 12 * 128 * 32768 * 2 + split
-    # 72-token blocks: 10 key blocks of two 64-key halves; one 1-token block
-    # still takes one 64-key half.
-    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 720, 128, 72) == 128 * 1280 * 2 + split
-    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 1, 128, 1) == 128 * 64 * 2 + split
+    assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == split
+    assert lib.dsa_bsa_workspace_bytes(1, 40, 57600, 128) == split
+    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 16 * 72, 128, 72) == split
+    # Key ranges too short to split need none: 512 text tokens (4 blocks),
+    # 10 blocks of 72 tokens, one 1-token block.
+    assert lib.dsa_bsa_workspace_bytes(1, 12, 512, 128) == 0
+    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 720, 128, 72) == 0
+    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 1, 128, 1) == 0
     assert lib.dsa_bsa_workspace_bytes(0, 12, 10, 128) == 0
 
 
@@ -60,8 +64,12 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 64, 128,
                              None, None, 1, 0.1, None, fake, 1 << 20, None)
     assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
+    misaligned = ctypes.c_void_p(24)
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, None, fake, 16, None)
+                             None, None, 1, 0.1, None, misaligned, 1 << 20, None)
+    assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 128, 128,
+                             None, None, 1, 0.1, None, None, 1 << 20, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
     status = lib.dsa_route_select(fake, None, 4, 2100, 0.5, 0.95, 1, 0, fake, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "2048" in _lib.last_error()

@@ -1,0 +1,263 @@
+"""Parity at the full BASELINE shapes: the timed config-2 launch, the config-3
+sampled mass, and a config-4 DiT block and denoising loop.
+
+Config 2 and 3 inputs come from bench.py's own generators (clustered Q/K with
+one centroid per 128-token block, N(0,1) V, per-head Bernoulli(0.625) routes
+plus the diagonal and the 29 frame-0 sink columns), so the launch checked here
+is the launch bench.py times: 57,600 tokens x 40 heads, [B,T,H,D] views of
+BHSD storage, the default workspace (room for the split partials), and hence
+the split of the last partial round of workgroups and its merge.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import route as R
+from oracle.attention import block_sparse_attention, summarize
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MIN_COSINE = 0.9995
+
+
+@pytest.fixture(scope="module")
+def config2(cuda_device):
+    from dit_sparse_atten_amd import ops
+    q, k, v = bench.clustered_inputs(cuda_device)
+    route = bench.bernoulli_route(cuda_device)
+    csr = ops.route_to_csr(route)
+    out, lse = ops.bsa_fwd(q, k, v, csr, return_lse=True)
+    torch.cuda.synchronize()
+    yield q, k, v, route, out, lse
+    del q, k, v, route, out, lse
+    torch.cuda.empty_cache()
+
+
+def test_config2_timed_launch_matches_oracle(cuda_device, config2):
+    """256 (head, query block) rows of the exact config-2 launch, including
+    every row of the split last round (head 39, query blocks 370-449 on a
+    256-CU MI355X), against the float64 closed form; LSE of the split rows;
+    the whole output finite.  Reference: flex.py:379-399."""
+    q, k, v, route, out, lse = config2
+    assert bool(torch.isfinite(out).all())
+    rows = bench.parity_rows(cuda_device)
+    tail = bench.tail_rows(cuda_device)
+    assert len(rows) >= 256 and set(tail) <= set(rows)
+    route_cpu = route.cpu().numpy()
+    by_head = {}
+    for head, q_block in rows:
+        by_head.setdefault(head, []).append(q_block)
+    got_all, want_all = [], []
+    for head, q_blocks in sorted(by_head.items()):
+        qn, kn, vn = (x[:, :, head:head + 1].float().cpu().numpy() for x in (q, k, v))
+        expected, expected_lse = block_sparse_attention(
+            qn, kn, vn, route_cpu[head:head + 1], 128, rows=[(0, 0, qb) for qb in q_blocks])
+        got = out[:, :, head:head + 1].float().cpu().numpy()
+        for qb in q_blocks:
+            sl = slice(qb * 128, (qb + 1) * 128)
+            got_all.append(got[0, sl, 0])
+            want_all.append(expected[0, sl, 0])
+        tail_blocks = [qb for h, qb in tail if h == head]
+        if tail_blocks:
+            got_lse = lse[0, head].cpu().numpy()
+            for qb in tail_blocks:
+                sl = slice(qb * 128, (qb + 1) * 128)
+                np.testing.assert_allclose(got_lse[sl], expected_lse[0, 0, sl], atol=1e-3,
+                                           rtol=1e-4)
+    metrics = summarize(np.concatenate(got_all), np.concatenate(want_all))
+    assert metrics["max_absolute_error"] <= MAX_ABS, metrics
+    assert metrics["cosine_similarity"] >= MIN_COSINE, metrics
+    np.testing.assert_allclose(np.concatenate(got_all), np.concatenate(want_all), atol=5e-3,
+                               rtol=3e-2)
+
+
+def test_config2_bench_parity_check_agrees(cuda_device, config2):
+    """bench.py's float32 device restatement (its config.parity field) passes
+    the same bar on the same launch."""
+    q, k, v, route, out, _ = config2
+    parity = bench.attention_parity(q, k, v, route, out, bench.parity_rows(cuda_device))
+    assert parity["output_finite"]
+    assert parity["max_absolute_error"] <= MAX_ABS, parity
+    assert parity["cosine_similarity"] >= MIN_COSINE, parity
+
+
+# Relative bound of the sampled mass.  The kernel's fp32 dot products and the
+# oracle's float64 ones round to bf16 identically except when a score lies
+# within fp32 noise of a bf16 rounding boundary; such a score then moves by one
+# bf16 ulp (2^-8 relative, about 4% in exp for |score| ~ 11), which moves the
+# few entries it dominates.  Entries above 1e-5 must agree within 1e-3
+# relative at the 99.9th percentile and within 5e-2 everywhere.
+MASS_FLOOR = 1e-5
+MASS_RTOL_P999 = 1e-3
+MASS_RTOL_MAX = 5e-2
+
+
+@pytest.mark.parametrize("tokens,heads", [(57600, 40), (57563, 4)])
+def test_config3_sampled_mass_full_scale(cuda_device, tokens, heads):
+    """Config 3: 57,600 tokens x 40 heads, S = 16 (450 blocks, 7,200 sampled
+    keys per head: 112 full 64-key tiles and a half tile at the end of the
+    key sweep), every key block of 24 query blocks per head including the
+    first and last, against the oracle's float64 softmax; and a partial last
+    block (57,563 tokens: 91 tokens, log(91/16) weight).  Rows sum to 1.
+    Reference: flex.py:205-251."""
+    from dit_sparse_atten_amd import ops
+    generator = torch.Generator(device=cuda_device).manual_seed(0)
+    blocks = math.ceil(tokens / 128)
+
+    def clustered():
+        noise = torch.randn((1, heads, tokens, 128), device=cuda_device, generator=generator)
+        centroid = torch.randn((1, heads, blocks, 128), device=cuda_device,
+                               generator=generator)
+        group = torch.arange(tokens, device=cuda_device) // 128
+        return (0.5 * noise + centroid[:, :, group]).to(torch.bfloat16).transpose(1, 2)
+
+    q, k = clustered(), clustered()
+    mass = ops.sampled_block_mass(q, k, 128, 16)
+    torch.cuda.synchronize()
+    assert mass.shape == (heads, blocks, blocks)
+    np.testing.assert_allclose(mass.sum(-1).cpu().numpy(), 1.0, atol=1e-5)
+    pick = np.random.default_rng(tokens).choice(np.arange(1, blocks - 1), 22, replace=False)
+    query_blocks = [0, blocks - 1] + sorted(int(x) for x in pick)
+    qn, kn = q.float().cpu().numpy(), k.float().cpu().numpy()
+    del q, k
+    expected = np.concatenate([
+        R.sampled_block_mass(qn[:, :, h0:h0 + 4], kn[:, :, h0:h0 + 4], 128, 16,
+                             query_blocks=query_blocks)
+        for h0 in range(0, heads, 4)])
+    got = mass[:, query_blocks].cpu().numpy().astype(np.float64)
+    big = expected > MASS_FLOOR
+    relative = np.abs(got - expected)[big] / expected[big]
+    stats = {"entries": int(big.sum()), "p999": float(np.quantile(relative, 0.999)),
+             "max": float(relative.max()),
+             "small_max_abs": float(np.abs(got - expected)[~big].max(initial=0.0))}
+    assert stats["p999"] <= MASS_RTOL_P999, stats
+    assert stats["max"] <= MASS_RTOL_MAX, stats
+    assert stats["small_max_abs"] <= MASS_FLOOR, stats
+
+
+def _block_rows_fp32(model, blk, x, ctx, temb6, grid, rows):
+    """float32 restatement of one WanDiT block (wan_dit.WanDiT._block) on the
+    token rows ``rows``: the keys and values of the self-attention come from
+    every token; the queries, the attention (a float32 softmax over all 57,600
+    keys, chunked by head), the cross-attention over the text tokens and the
+    feed-forward from the sampled rows only."""
+    import torch.nn.functional as F
+
+    from tests.golden.inputs import apply_rope, wan_rope_angles
+    c = model.config
+    heads, head_dim = c.heads, c.head_dim
+    f32 = lambda pair: (pair[0].float(), pair[1].float())  # noqa: E731
+    xf = x[0].float()
+    mod = blk["table"] + temb6
+    angles = wan_rope_angles(grid).to(x.device)
+
+    def rms(t, w):
+        return t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + c.eps) * w
+
+    def rope(t, a):
+        return apply_rope(t.view(1, -1, heads, head_dim).double(), a).float().reshape(t.shape)
+
+    def attend(qr, kr, vr):
+        qr, kr, vr = (t.view(t.shape[0], heads, head_dim) for t in (qr, kr, vr))
+        out = []
+        for h in range(heads):
+            scores = qr[:, h] @ kr[:, h].t().contiguous() * head_dim ** -0.5
+            out.append(torch.softmax(scores, dim=-1) @ vr[:, h].contiguous())
+        return torch.stack(out, dim=1).reshape(qr.shape[0], c.dim)
+
+    h = F.layer_norm(xf, (c.dim,), eps=c.eps) * (1 + mod[1]) + mod[0]
+    k = rope(rms(F.linear(h, *f32(blk["k"])), blk["norm_k"]), angles)
+    v = F.linear(h, *f32(blk["v"]))
+    q = rope(rms(F.linear(h[rows], *f32(blk["q"])), blk["norm_q"]), angles[rows])
+    xr = xf[rows] + mod[2] * F.linear(attend(q, k, v), *f32(blk["o"]))
+    del k, v, h
+    h = F.layer_norm(xr, (c.dim,), blk["norm2_w"], blk["norm2_b"], eps=c.eps)
+    cf = ctx[0].float()
+    cq = rms(F.linear(h, *f32(blk["cq"])), blk["cnorm_q"])
+    ck = rms(F.linear(cf, *f32(blk["ck"])), blk["cnorm_k"])
+    cv = F.linear(cf, *f32(blk["cv"]))
+    xr = xr + F.linear(attend(cq, ck, cv), *f32(blk["co"]))
+    h = F.layer_norm(xr, (c.dim,), eps=c.eps) * (1 + mod[4]) + mod[3]
+    ffn = F.linear(F.gelu(F.linear(h, *f32(blk["ffn1"])), approximate="tanh"), *f32(blk["ffn2"]))
+    return xr + mod[5] * ffn
+
+
+def _cosine(a, b):
+    a, b = a.double().reshape(-1), b.double().reshape(-1)
+    return float(a @ b / (a.norm() * b.norm()))
+
+
+def test_config4_block_at_full_shape(cuda_device):
+    """One block of the config-4 model at its real shape (dim 1536, 12 heads,
+    57,600 tokens of the 16x45x80 grid, 512 text tokens) through the dense
+    backend, against the float32 restatement on 256 sampled tokens: the block
+    output and the block's increment to the residual stream."""
+    from dit_sparse_atten_amd.attention_backends import context
+    from dit_sparse_atten_amd.attention_backends.dense import DenseBackend
+    from dit_sparse_atten_amd.wan_dit import WanDiT, WanDiTConfig
+    context.reset_runtime_state()
+    model = WanDiT(WanDiTConfig(layers=1), device=cuda_device, seed=11)
+    gen = torch.Generator(device=cuda_device).manual_seed(21)
+    grid = (16, 45, 80)
+    x = torch.randn(1, 57600, 1536, device=cuda_device, generator=gen).bfloat16()
+    ctx = model.embed_text(torch.randn(1, 512, 4096, device=cuda_device, generator=gen)
+                           .bfloat16())
+    temb6 = torch.randn(6, 1536, device=cuda_device, generator=gen) * 0.5
+    blk = model.blocks[0]
+    out = model._block(x.clone(), blk, ctx, temb6, model._cos_sin(grid), DenseBackend())
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all())
+    rows = torch.randperm(57600, generator=torch.Generator().manual_seed(5))[:256]
+    rows = rows.to(cuda_device)
+    want = _block_rows_fp32(model, blk, x, ctx, temb6, grid, rows)
+    got = out[0, rows].float()
+    base = x[0, rows].float()
+    assert _cosine(got, want) >= 0.999
+    assert _cosine(got - base, want - base) >= 0.999
+    context.reset_runtime_state()
+
+
+@pytest.mark.parametrize("threshold,expected", [
+    (0.58, {"first_layer_dense": 10, "sampled_bootstrap": 58, "dense_dispatch": 232,
+            "sampled_update": 0, "sparse_reuse": 0}),
+    (None, {"first_layer_dense": 10, "sampled_bootstrap": 58, "dense_dispatch": 0,
+            "sampled_update": 58, "sparse_reuse": 232}),
+])
+def test_config4_denoising_loop_at_full_shape(cuda_device, threshold, expected):
+    """Config 4: the 30-layer Wan2.1-1.3B-shaped model, 5 steps x CFG pair at
+    57,600 tokens with 512 x 4096 text, through the flex_reuse hybrid the
+    bench times (sampled bootstrap with prefetch, sampled update every 2
+    steps, 16 samples, persistence .5, target .95, keep .625, 1x16 Morton
+    micro-tiles), with dense dispatch at 0.58 and without it.  Random
+    projections give diffuse attention, so every route reaches the cap and,
+    at 0.58, dispatches dense.  Phase counts, released routes, finite latents."""
+    from dit_sparse_atten_amd.attention_backends import context
+    from dit_sparse_atten_amd.attention_backends.flex import FlexReuseBackend, FlexReuseConfig
+    from dit_sparse_atten_amd.wan_dit import WanDiT, denoise
+    context.reset_runtime_state()
+    model = WanDiT(device=cuda_device, seed=11)
+    gen = torch.Generator(device=cuda_device).manual_seed(12)
+    latents = torch.randn(1, 16, 16, 90, 160, device=cuda_device, generator=gen).bfloat16()
+    cond = torch.randn(1, 512, 4096, device=cuda_device, generator=gen).bfloat16()
+    uncond = torch.randn(1, 512, 4096, device=cuda_device, generator=gen).bfloat16()
+    backend = FlexReuseBackend(FlexReuseConfig(
+        bootstrap_mode="sampled", prefetch_sampled_bootstrap=True, sampled_update_interval=2,
+        prefetch_sampled_update=False, route_samples=16, route_persistence=0.5,
+        mass_target=0.95, keep=0.625, dense_route_threshold=threshold, total_steps=5,
+        spatial_reorder=True))
+    out = denoise(model, backend, latents, cond, uncond, steps=5)
+    torch.cuda.synchronize()
+    assert out.shape == latents.shape
+    assert bool(torch.isfinite(out.float()).all())
+    counts = backend.phase_counts
+    for phase, count in expected.items():
+        assert counts[phase] == count, (phase, counts)
+    summary = backend.profile_summary()
+    assert summary["released_routes"] == 58 and not backend.state
+    assert summary["dense_dispatched_routes"] == (58 if threshold else 0)
+    context.reset_runtime_state()

@@ -168,6 +168,25 @@ def test_sampled_mass_matches_reference_golden(case):
     np.testing.assert_allclose(mass.sum(-1), 1.0, atol=1e-9)
 
 
+def test_sampled_mass_query_block_subset_equals_full_rows():
+    """The row-restricted form (used at full config-3 scale) returns exactly
+    the selected rows of the full computation, in the order asked for, and
+    still matches the reference golden on them."""
+    data = _load("sampled_mass")
+    tokens, heads, dim, block, samples, bf16, seed = (
+        int(x) for x in data["bf16_partial_s16__params"])
+    q, k, _ = clustered_qkv(tokens, heads, dim, group=block, seed=seed, dtype=torch.bfloat16)
+    qn, kn = q.float().numpy(), k.float().numpy()
+    full = R.sampled_block_mass(qn, kn, block, samples)
+    blocks = full.shape[1]
+    subset = [blocks - 1, 0, blocks // 2]
+    rows = R.sampled_block_mass(qn, kn, block, samples, query_blocks=subset)
+    assert rows.shape == (heads, len(subset), blocks)
+    np.testing.assert_array_equal(rows, full[:, subset])
+    np.testing.assert_allclose(rows, data["bf16_partial_s16__mass"][:, subset],
+                               atol=2e-3, rtol=2e-3)
+
+
 def test_full_sampling_matches_exact_block_mass():
     """tests/test_flex_backend.py:43-53: samples == block gives exact / block."""
     rng = np.random.default_rng(4)
