@@ -37,6 +37,7 @@
 //  * the last, partial round of query blocks may run as 2..8 key ranges each
 //    (choose_split), whose fp32 partials bsa_merge_kernel combines.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "bsa_tiles.h"
@@ -561,15 +562,24 @@ __global__ void __launch_bounds__(256) bsa_merge_kernel(BsaParams p) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-// Workgroup slots (two attention workgroups per CU) of the device `stream`
-// belongs to (the current device for the null stream), cached per device.
-int device_slots(hipStream_t stream) {
-  static int slots[64] = {0};
+constexpr int kMaxDevices = 64;
+
+// The device `stream` belongs to (the current device for the null stream), or
+// -1 when it cannot be told.
+int stream_device(hipStream_t stream) {
   int device = -1;
   if (stream == nullptr || hipStreamGetDevice(stream, &device) != hipSuccess) {
-    if (hipGetDevice(&device) != hipSuccess) return 0;
+    if (hipGetDevice(&device) != hipSuccess) return -1;
   }
-  if (device < 0 || device >= 64) return 0;
+  return device >= 0 && device < kMaxDevices ? device : -1;
+}
+
+// Workgroup slots (two attention workgroups per CU) of the stream's device,
+// cached per device.
+int device_slots(hipStream_t stream) {
+  static int slots[kMaxDevices] = {0};
+  const int device = stream_device(stream);
+  if (device < 0) return 0;
   if (slots[device] == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
@@ -726,6 +736,41 @@ int launch(BsaParams p, float* part, int64_t part_groups, hipStream_t stream, co
 
 }  // namespace
 
+// Split partials of dsa_bsa_fwd_noalloc: room for kMaxPartGroups partials
+// (68,157,440 bytes).  Every device the library runs on holds its own copy
+// until the process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns on that device (scratch_on).
+static __device__ __align__(256) float scratch[kMaxPartGroups * kPartFloats];
+
+namespace {
+
+std::mutex g_scratch_lock;
+float* g_scratch[kMaxDevices] = {};
+
+// Device address of `device`'s scratch array, resolved once per device with
+// that device current.
+int scratch_on(int device, float** out, const char* who) {
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch[device] == nullptr) {
+    int current = -1;
+    if (hipGetDevice(&current) != hipSuccess)
+      return dsa::set_error(DSA_ELAUNCH, "%s: no current HIP device", who);
+    if (current != device && hipSetDevice(device) != hipSuccess)
+      return dsa::set_error(DSA_ELAUNCH, "%s: cannot select device %d", who, device);
+    void* address = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (current != device) (void)hipSetDevice(current);
+    if (err != hipSuccess || address == nullptr)
+      return dsa::set_error(DSA_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                            who, device, hipGetErrorString(err));
+    g_scratch[device] = static_cast<float*>(address);
+  }
+  *out = g_scratch[device];
+  return DSA_OK;
+}
+
+}  // namespace
+
 extern "C" size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads,
                                                 int32_t kv_tokens, int32_t head_dim,
                                                 int32_t block_size) {
@@ -757,4 +802,27 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
     return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: workspace must be 16-byte aligned");
   return launch(p, static_cast<float*>(workspace), (int64_t)(workspace_bytes / kPartBytes),
                 stream, "dsa_bsa_fwd");
+}
+
+extern "C" int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
+                                   const int64_t* strides, int32_t batch, int32_t q_tokens,
+                                   int32_t kv_tokens, int32_t heads, int32_t head_dim,
+                                   int32_t block_size, const int32_t* row_ptr,
+                                   const int32_t* col_idx, int32_t route_batches, float scale,
+                                   float* lse, hipStream_t stream) {
+  dsa::clear_error();
+  BsaParams p;
+  const int status = prepare(q, k, v, o, strides, batch, q_tokens, kv_tokens, heads, head_dim,
+                             block_size, row_ptr, col_idx, route_batches, scale, lse,
+                             "dsa_bsa_fwd_noalloc", &p);
+  if (status != DSA_OK) return status;
+  const int device = stream_device(stream);
+  if (device < 0)
+    return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd_noalloc: cannot tell the stream's device");
+  float* part = nullptr;
+  const int found = scratch_on(device, &part, "dsa_bsa_fwd_noalloc");
+  if (found != DSA_OK) return found;
+  // The split never takes more than the array holds, so no call size needs
+  // more scratch than kMaxPartGroups partials.
+  return launch(p, part, kMaxPartGroups, stream, "dsa_bsa_fwd_noalloc");
 }

@@ -81,6 +81,26 @@ size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_to
                                      int32_t head_dim, int32_t block_size);
 
 /*
+ * dsa_bsa_fwd without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  Same arguments,
+ * semantics and results as dsa_bsa_fwd given a workspace of
+ * dsa_bsa_workspace_bytes_block() bytes; it calls no hipMalloc / hipFree.  The
+ * split partials live in a library-owned device array of 68,157,440 bytes
+ * (1,024 partials of 128 x 130 fp32), one per device the library runs on,
+ * held until the process ends; the split never needs more, so no call size
+ * is refused for want of scratch.  Every call on a device shares that
+ * device's array: calls that overlap on one device (on different streams)
+ * race; calls ordered on one stream do not.  Nothing in the array needs
+ * clearing: a call writes every partial it reads.
+ */
+int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
+                        const int64_t* strides, int32_t batch, int32_t q_tokens,
+                        int32_t kv_tokens, int32_t heads, int32_t head_dim, int32_t block_size,
+                        const int32_t* row_ptr, const int32_t* col_idx, int32_t route_batches,
+                        float scale, float* lse, hipStream_t stream);
+
+/*
  * Sampled block-mass estimate for one batch-1 self-attention call.
  * Replaces `_sampled_block_mass` (attention_backends/flex.py:205-251):
  * `samples` evenly spaced tokens per block, scores rounded like a bf16 matmul
