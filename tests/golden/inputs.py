@@ -98,3 +98,25 @@ def rope_qkv(grid, batch, heads, head_dim=128, seed=0, dtype=torch.bfloat16):
     q, k, v = (torch.randn(shape, generator=generator) for _ in range(3))
     angles = wan_rope_angles(grid, head_dim)
     return apply_rope(q, angles).to(dtype), apply_rope(k, angles).to(dtype), v.to(dtype)
+
+
+def block_mass_like(heads, blocks, seed, centroid_dim=4, sharpness=16.0):
+    """Softmax-shaped non-negative block mass [heads, blocks, blocks] float32
+    with the structure of a sampled block mass: per block a query and a key
+    centroid c ~ U(-1, 1)^centroid_dim, score s = <c_q, c_k> (summed in a fixed
+    order), mass = 2^-16 max(0, 1 + s / sharpness)^16 (0.5 + u), u ~ U[0, 1),
+    i.e. roughly exp(16 s / sharpness) with per-entry noise, entries below 1.
+    Built from the torch CPU generator's uniform draws with elementwise fp32
+    adds, multiplies and a clamp only, so every machine reproduces it bit for
+    bit (no exp, no reduction)."""
+    generator = torch.Generator().manual_seed(seed)
+    cq = torch.rand((heads, blocks, 1, centroid_dim), generator=generator) * 2 - 1
+    ck = torch.rand((heads, 1, blocks, centroid_dim), generator=generator) * 2 - 1
+    noise = torch.rand((heads, blocks, blocks), generator=generator) + 0.5
+    score = cq[..., 0] * ck[..., 0]
+    for j in range(1, centroid_dim):
+        score = score + cq[..., j] * ck[..., j]
+    t = torch.clamp_min(score * (1.0 / sharpness) + 1.0, 0.0)
+    for _ in range(4):
+        t = t * t
+    return t * noise * (2.0 ** -16)

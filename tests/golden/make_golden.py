@@ -5,7 +5,8 @@ Only functions whose exact output no reference test or closed form pins are
 run here:
   * flex._top_mass_route        tie order / fp32 rounding of sum and cumsum
   * flex._sampled_block_mass    sample-index choice and log-weights
-  * FlexReuseBackend._sampled_route   persistence prior + selection
+  * FlexReuseBackend._sampled_route   persistence prior + selection, also at
+    config-3 scale on a reproducible mass (route_config3.npz)
   * spatial.build_spatial_layout      Morton order and majority-vote neighbours
   * sparse.MatrixSparseBackend  config-0 bootstrap route, mass and outputs
   * sparse.MatrixSparseBackend  four steps per policy (reuse / all / directional):
@@ -31,7 +32,8 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parents[1]))
 REFERENCE = Path(os.environ.get("DSA_REFERENCE", "/root/reference"))
 
-from tests.golden.inputs import clustered_qkv, random_route, route_mass  # noqa: E402
+from tests.golden.inputs import (  # noqa: E402
+    block_mass_like, clustered_qkv, random_route, route_mass)
 
 
 def _reference_modules():
@@ -106,6 +108,58 @@ def sampled_route_fixture(flex):
     mass = flex._sampled_block_mass(q, k, 128, samples=16)
     _save("sampled_route", seed=np.array([7, 8]), previous=previous.numpy(),
           mass=mass.numpy(), route=result["route"].numpy())
+
+
+def route_summary(route):
+    """Per-row (count, sum of selected indices, sum of their squares) of a
+    boolean route [..., K]: a compact fingerprint of every row's selection."""
+    route = np.asarray(route, dtype=bool)
+    index = np.arange(route.shape[-1], dtype=np.int64)
+    return (route.sum(-1).astype(np.int16), (route * index).sum(-1).astype(np.int32),
+            (route * index * index).sum(-1).astype(np.int64))
+
+
+def route_config3_fixture(flex):
+    """The reference's sampled-route selection at config-3 scale (40 heads x
+    450 x 450, target .95, keep .625, 29-block first-frame sink of the
+    16x45x80 grid): FlexReuseBackend._sampled_route on a reproducible
+    softmax-shaped mass (inputs.block_mass_like), without a previous route
+    (bootstrap) and with one (persistence prior 0.5).  The mass is injected in
+    place of _sampled_block_mass; everything after it (prior, _top_mass_route,
+    sink) is the reference's own code.  Stored as per-row fingerprints."""
+    heads, blocks, seed, sharpness, previous_seed = 40, 450, 31, 4.0, 32
+    mass = block_mass_like(heads, blocks, seed, sharpness=sharpness)
+    previous = random_route(heads, blocks, previous_seed)
+    backend = flex.FlexReuseBackend(flex.FlexReuseConfig(
+        route_samples=16, mass_target=0.95, keep=0.625, route_persistence=0.5))
+    original_mass, original_top = flex._sampled_block_mass, flex._top_mass_route
+    selected_from = []
+
+    def recording_top_mass_route(primed, target, keep):
+        selected_from.append(primed.clone())  # the mass the reference selects from
+        return original_top(primed, target, keep)
+
+    flex._sampled_block_mass = lambda *args, **kwargs: mass.clone()
+    flex._top_mass_route = recording_top_mass_route
+    try:
+        arrays = {"params": np.array([heads, blocks, seed, sharpness, previous_seed])}
+        dummy = torch.zeros(1, blocks * 128, heads, 1)
+        for name, prev in (("bootstrap", None), ("prior", previous)):
+            selected_from.clear()
+            state = {"route": prev, "grid": (16, 45, 80), "layout": None}
+            route = backend._sampled_route(state, dummy, dummy, None)["route"].numpy()
+            count, index_sum, square_sum = route_summary(route)
+            arrays[f"{name}__count"] = count
+            arrays[f"{name}__index_sum"] = index_sum
+            arrays[f"{name}__square_sum"] = square_sum
+            # Sum of the selected values (sink columns included) in float64: a
+            # selection that differs only in which of several equal values it
+            # took at the boundary (torch's unstable argsort) has the same sum.
+            primed = selected_from[-1].double().numpy()
+            arrays[f"{name}__value_sum"] = (primed * route).sum(-1)
+    finally:
+        flex._sampled_block_mass, flex._top_mass_route = original_mass, original_top
+    _save("route_config3", **arrays)
 
 
 def spatial_fixture(spatial):
@@ -239,6 +293,7 @@ def main():
     top_mass_fixture(flex)
     sampled_mass_fixture(flex)
     sampled_route_fixture(flex)
+    route_config3_fixture(flex)
     spatial_fixture(spatial)
     sparse_config0_fixture(context, sparse)
     routing_fixture(routing, spatial)
