@@ -20,6 +20,10 @@ DSA_EINVAL = -1
 DSA_EUNSUPPORTED = -2
 DSA_ELAUNCH = -3
 
+# Element types of the attention inputs (DSA_DTYPE_* in dsa.h).
+DSA_DTYPE_BF16 = 0
+DSA_DTYPE_F16 = 1
+
 _c_int = ctypes.c_int32
 _c_i64 = ctypes.c_int64
 _c_float = ctypes.c_float
@@ -31,7 +35,7 @@ SIGNATURES = {
     "dsa_version": (_c_int, ()),
     "dsa_last_error": (ctypes.c_char_p, ()),
     "dsa_bsa_fwd": (_c_int, (
-        _c_ptr, _c_ptr, _c_ptr, _c_ptr,          # q, k, v, o
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,  # q, k, v, o, dtype
         ctypes.POINTER(_c_i64),                    # strides[12]
         _c_int, _c_int, _c_int, _c_int, _c_int,    # batch, q_tokens, kv_tokens, heads, head_dim
         _c_int,                                    # block_size
@@ -40,7 +44,7 @@ SIGNATURES = {
         _c_ptr, _c_size, _c_ptr,                   # workspace, workspace_bytes, stream
     )),
     "dsa_bsa_fwd_noalloc": (_c_int, (
-        _c_ptr, _c_ptr, _c_ptr, _c_ptr,          # q, k, v, o
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,  # q, k, v, o, dtype
         ctypes.POINTER(_c_i64),                    # strides[12]
         _c_int, _c_int, _c_int, _c_int, _c_int,    # batch, q_tokens, kv_tokens, heads, head_dim
         _c_int,                                    # block_size
@@ -50,17 +54,20 @@ SIGNATURES = {
     "dsa_bsa_workspace_bytes": (_c_size, (_c_int, _c_int, _c_int, _c_int)),
     "dsa_bsa_workspace_bytes_block": (_c_size, (_c_int, _c_int, _c_int, _c_int, _c_int)),
     "dsa_sampled_mass": (_c_int, (
-        _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
+        _c_ptr, _c_ptr, _c_int,                    # q, k, dtype
+        ctypes.POINTER(_c_i64),                    # strides[4]
         _c_int, _c_int, _c_int, _c_int, _c_int,    # tokens, heads, head_dim, block, samples
         _c_float, _c_ptr, _c_ptr,                  # scale, mass, stream
     )),
     "dsa_block_mass": (_c_int, (
-        _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
+        _c_ptr, _c_ptr, _c_int,                    # q, k, dtype
+        ctypes.POINTER(_c_i64),                    # strides[4]
         _c_int, _c_int, _c_int, _c_int,            # tokens, heads, head_dim, block
         _c_ptr, _c_i64, _c_float, _c_ptr, _c_ptr,  # lse, lse_head_stride, scale, mass, stream
     )),
     "dsa_tile_stats": (_c_int, (
-        _c_ptr, _c_ptr, ctypes.POINTER(_c_i64),    # q, k, strides[4]
+        _c_ptr, _c_ptr, _c_int,                    # q, k, dtype
+        ctypes.POINTER(_c_i64),                    # strides[4]
         _c_int, _c_int, _c_int, _c_int, _c_int,    # tokens, heads, head_dim, tile_h, tile_w
         _c_ptr, _c_i64, _c_ptr, _c_ptr, _c_float,  # lse, lse_head_stride, row_ptr, col_idx, scale
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # mass, mass_f16, centroids q_y q_x k_y k_x

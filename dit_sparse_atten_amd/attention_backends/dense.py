@@ -1,8 +1,9 @@
 """Dense attention backend on the libdsa block-sparse kernel with a full route.
 
 Mirrors ``DenseBackend`` of the reference (attention_backends/dense.py:12-48):
-same name, call signature, dtype handling (compute in ``dtype``, return the
-caller's dtype) and output layout (contiguous [B, T, H, D]).  The reference
+same name, call signature, dtype handling (compute in ``dtype``, bfloat16 or
+float16, and return the caller's dtype; float32 compute raises ValueError, as
+every libdsa backend does) and output layout (contiguous [B, T, H, D]).  The reference
 calls SDPA; here the same hand-written HIP kernel as the sparse path runs with
 every key block listed, so dense and sparse numerics agree by construction.
 """
@@ -42,8 +43,7 @@ class DenseBackend:
             raise NotImplementedError("The dense backend does not implement causal attention")
         if dropout_p:
             raise NotImplementedError("The dense backend does not implement attention dropout")
-        if dtype != torch.bfloat16:
-            raise ValueError(f"The libdsa attention kernels compute in bfloat16, not {dtype}")
+        ops.dtype_code(dtype)  # bfloat16 or float16, else ValueError
         output_dtype = q.dtype
         q = q.to(dtype)
         k = k.to(dtype)

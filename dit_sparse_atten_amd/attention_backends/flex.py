@@ -185,8 +185,6 @@ class FlexReuseBackend:
             raise ValueError("route_exploration_fraction must be in [0, 1]")
         if c.directional_update and not c.spatial_reorder:
             raise ValueError("directional_update requires spatial_reorder")
-        if c.route_samples > 32 or c.route_samples & (c.route_samples - 1):
-            raise ValueError("route_samples must be a power of two <= 32 on the libdsa kernels")
         self.dense = DenseBackend()
         self.state = {}
         self.route_streams = {}

@@ -183,8 +183,12 @@ class MatrixSparseBackend:
 
     def _sparse_attention(self, q, k, v, scale, layout):
         c = self.config
+        # The reference computes in the input dtype; so do the kernels, for
+        # bfloat16 and float16 (float32 raises ValueError, as in every
+        # libdsa backend).
+        ops.dtype_code(q.dtype)
         output_dtype = q.dtype
-        q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+        k, v = k.to(q.dtype), v.to(q.dtype)
         # Jointly permuting Q/K/V is attention-equivalent; it only changes
         # which tokens form a tile.
         q, k, v = layout.to_tile_major(q, k, v)

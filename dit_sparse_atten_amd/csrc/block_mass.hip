@@ -1,4 +1,4 @@
-// Exact block attention mass for gfx950 (MI355X).
+// Exact block attention mass for gfx950 (MI355X), bf16 or fp16 Q/K.
 //
 // Replaces `_block_attention_mass` / `_exact_block_mass_kernel` of the
 // reference (attention_backends/flex.py:96-202):
@@ -10,7 +10,7 @@
 // Design: one 4-wave workgroup per (head, 128-query block) walks every key
 // block once.  K streams through LDS in 64-key half-tiles (the same
 // buffer->LDS staging as the forward kernel); S^T = K Q^T on
-// v_mfma_f32_32x32x16_bf16 leaves each lane with one query row, so
+// v_mfma_f32_32x32x16_bf16 (or _f16) leaves each lane with one query row, so
 // p = exp2(s * scale * log2(e) - lse * log2(e)) needs no max and no exchange.
 // Each lane sums its probabilities per key block; a wave reduction and a
 // fixed-order sum of the four wave partials (through LDS, double-buffered by
@@ -27,8 +27,8 @@ using dsa::kKStage;
 using dsa::kRowBytes;
 
 struct BlockMassParams {
-  const __bf16* q;
-  const __bf16* k;
+  const void* q;  // element type T of the kernel instance
+  const void* k;
   const float* lse;  // [heads, tokens] (token stride 1, head stride lse_sh)
   float* mass;       // [heads, blocks, blocks]
   int64_t q_st, q_sh, k_st, k_sh, lse_sh;
@@ -39,7 +39,9 @@ struct BlockMassParams {
 constexpr float kLog2e = 1.4426950408889634f;
 
 
+template <typename T>
 __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
+  typedef dsa::Elem<T> E;
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ float part[2][4];
@@ -57,15 +59,15 @@ __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
   const int tq = qb * 128 + wave * 32 + qi;
   const bool row_ok = tq < p.tokens;
   const int tq_c = row_ok ? tq : p.tokens - 1;
-  const __bf16* qrow = p.q + h * p.q_sh + (int64_t)tq_c * p.q_st;
-  dsa_bf16x8 qf[8];
+  const T* qrow = static_cast<const T*>(p.q) + h * p.q_sh + (int64_t)tq_c * p.q_st;
+  typename E::x8 qf[8];
 #pragma unroll
   for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
+    qf[dc] = *reinterpret_cast<const typename E::x8*>(qrow + dc * 16 + g * 8);
   // Rows past the sequence end get lse = +inf, so every p of theirs is 0.
   const float lse2 = row_ok ? p.lse[h * p.lse_sh + tq] * kLog2e : INFINITY;
 
-  const __bf16* kbase = p.k + h * p.k_sh;
+  const T* kbase = static_cast<const T*>(p.k) + h * p.k_sh;
   int koff[4];
   dsa::k_tile_offsets(wave, lane, p.k_st, koff);
   auto issue = [&](int key0, unsigned char* dst) __attribute__((always_inline)) {
@@ -100,9 +102,9 @@ __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
       const int row = kt * 32 + qi;
 #pragma unroll
       for (int dc = 0; dc < 8; ++dc) {
-        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
+        const typename E::x8 a = *reinterpret_cast<const typename E::x8*>(
             cur + row * kRowBytes + dsa::k2_swz(row, dc * 2 + g) * 16);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], sacc, 0, 0, 0);
+        sacc = E::mfma32(a, qf[dc], sacc);
       }
       if (valid < kHalfKeys) {
 #pragma unroll
@@ -137,13 +139,16 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 }  // namespace
 
-extern "C" int dsa_block_mass(const void* q, const void* k, const int64_t* strides,
+extern "C" int dsa_block_mass(const void* q, const void* k, int32_t dtype, const int64_t* strides,
                               int32_t tokens, int32_t heads, int32_t head_dim,
                               int32_t block_size, const float* lse, int64_t lse_head_stride,
                               float scale, float* mass, hipStream_t stream) {
   dsa::clear_error();
   if (!q || !k || !strides || !lse || !mass)
     return dsa::set_error(DSA_EINVAL, "dsa_block_mass: null pointer argument");
+  if (dtype != DSA_BF16 && dtype != DSA_F16)
+    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_block_mass: dtype %d unsupported (bf16 or fp16)",
+                          dtype);
   if (tokens <= 0 || heads <= 0)
     return dsa::set_error(DSA_EINVAL, "dsa_block_mass: tokens and heads must be positive");
   if (head_dim != dsa::kHeadDim)
@@ -174,8 +179,8 @@ extern "C" int dsa_block_mass(const void* q, const void* k, const int64_t* strid
     return dsa::set_error(DSA_EINVAL, "dsa_block_mass: grid too large");
 
   BlockMassParams p;
-  p.q = static_cast<const __bf16*>(q);
-  p.k = static_cast<const __bf16*>(k);
+  p.q = q;
+  p.k = k;
   p.lse = lse;
   p.mass = mass;
   p.q_st = strides[0]; p.q_sh = strides[1];
@@ -185,6 +190,9 @@ extern "C" int dsa_block_mass(const void* q, const void* k, const int64_t* strid
   p.heads = heads;
   p.blocks = blocks;
   p.scale_log2 = scale * kLog2e;
-  hipLaunchKernelGGL(block_mass_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p);
+  if (dtype == DSA_F16)
+    hipLaunchKernelGGL(block_mass_kernel<_Float16>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(block_mass_kernel<__bf16>, dim3((unsigned)grid), dim3(256), 0, stream, p);
   return dsa::check_launch("dsa_block_mass");
 }

@@ -1,0 +1,688 @@
+// Block-sparse attention forward for gfx950 (MI355X): bf16 or fp16 in/out,
+// fp32 softmax.  The kernel templates shared by bsa_fwd.hip (bf16 instances
+// and the C-ABI entry points) and bsa_fwd_f16.hip (fp16 instances).
+//
+// Replaces the FlexAttention call of the reference backend
+// (attention_backends/flex.py:379-399 `_flex_output`, kernel options
+// flex.py:360-364) and its dense SDPA fallback (attention_backends/dense.py:14-48).
+//
+// Semantics per (batch b, head h, query row t):
+//   O[b,t,h,:] = softmax_k( scale * <Q[b,t,h,:], K[b,k,h,:]> ) @ V[b,k,h,:]
+// where k ranges over the tokens of every key block listed in the CSR row of
+// (route batch, h, t / 128).  Without a CSR every key block is listed (dense
+// fallback).  Keys past `kv_tokens` in a partial last block are masked.
+//
+// Design (per 128-row query block, one 4-wave workgroup, two per CU):
+//  * wave w owns query rows 32w..32w+31; S^T = K Q^T uses
+//    v_mfma_f32_32x32x16_bf16 (or _f16) so each lane's accumulators belong to one query
+//    row (row max / sum stay in registers, one cross-half exchange) and P^T
+//    leaves the accumulators already in the B-operand layout of O^T = V^T P^T;
+//  * keys stream as 64-key half-tiles of K and V, double-buffered in LDS by
+//    direct buffer->LDS loads issued one half-tile ahead; the two stages are
+//    distinct LDS objects so reads of one never wait on the DMA into the
+//    other, and rows past the sequence end read as zeros (buffer range check);
+//  * V is staged row-major like K, straight from the caller's tensor; the
+//    V^T A-operand fragments of O^T = V^T P^T come out of that stage through
+//    gfx950's transposing LDS read (ds_read_b64_tr_b16: in each 16-lane
+//    group, lane j receives element j % 4 of the 8 bytes that lane
+//    4 r + j / 4 addresses, r = 0..3), so no transposed copy of V exists;
+//    each lane addresses the 4-key quads in the order 0, 2, 1, 3 (the key
+//    order of the P^T slots);
+//  * online softmax with a lazily moved reference max (rescale only when a
+//    score exceeds it by 2^8); row sums add the fp32 P in plain VALU adds
+//    (v_dot2 would contend with the matrix core for issue); the row max and
+//    the final row sum pair lanes l and l ^ 32 with v_permlane32_swap;
+//  * query / key blocks of 1..128 tokens (the matrix-sparse backend's spatial
+//    tiles): routed whole blocks of 65..127 keys stream the row's kept blocks
+//    as one gathered key sequence (kGather), and routed blocks of at most 64
+//    tokens run 2-wave workgroups (kWaves);
+//  * the last, partial round of query blocks may run as 2..8 key ranges each
+//    (choose_split), whose fp32 partials bsa_merge_kernel combines.
+#pragma once
+
+#include <algorithm>
+#include <type_traits>
+
+#include "bsa_tiles.h"
+
+namespace bsa {
+
+struct BsaParams {
+  const void* q;  // element type T of the kernel instance
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int64_t q_sb, q_st, q_sh;
+  int64_t k_sb, k_st, k_sh;
+  int64_t v_sb, v_st, v_sh;
+  int64_t o_sb, o_st, o_sh;
+  const int32_t* row_ptr;  // null: every key block (dense)
+  const int32_t* col_idx;
+  int32_t batch, heads, q_tokens, kv_tokens, q_blocks, kv_blocks, route_batches;
+  int32_t block;     // tokens per query block and per key block (1..128)
+  int32_t block_pad; // gathered stream: key slots per block (block rounded up to 8)
+  float scale;       // softmax scale applied to <q, k>
+  float scale_log2;  // scale * log2(e)
+  // Split tail: workgroups from split_from on each compute one of `parts` key
+  // ranges of query block split_from + (wg - split_from) / parts and leave
+  // their unnormalised partial in `part` for bsa_merge_kernel.
+  int32_t split_from;
+  int32_t parts;
+  float* part;
+};
+
+// One split partial: O [128 rows][128 dims] relative to the row's reference
+// max, then m (log2 units of the scaled scores) and l per row, in fp32.
+constexpr int kPartFloats = 128 * 128 + 2 * 128;
+constexpr int kMaxPartGroups = 1024;  // split workgroups per call (two rounds of 512 slots)
+
+using dsa::kHeadDim;
+using dsa::kRowBytes;
+using dsa::kHalfKeys;
+using dsa::kKStage;
+using dsa::k2_swz;
+using dsa::k_tile_rsrc;
+using dsa::lds_load16;
+using dsa::make_rsrc;
+typedef dsa::const_i32 dsa_const_i32;
+
+constexpr float kRescaleLog2 = 8.0f;  // move the max once p could exceed 2^8
+
+// V stage [64 keys][128 dims], row-major like K: the 16-byte chunk c of key
+// row r sits at chunk position c ^ v_swz_mask(r), masks 0, 6, 10, 12 for
+// r & 3 = 0..3.  One transposed read of a 16-lane group touches 4 consecutive
+// key rows x 32 bytes (two chunks); these masks give the 4 rows' segments
+// distinct bank groups, for 32 as for 64 four-byte banks per clock.
+__device__ __forceinline__ int v_swz_mask(int r) { return (0xCA60 >> (4 * (r & 3))) & 15; }
+__device__ __forceinline__ int v_swz(int r, int c) { return c ^ v_swz_mask(r); }
+
+// ds_read_b64_tr_b16 at an LDS address, as four 16-bit elements of type T.
+template <typename T>
+__device__ __forceinline__ typename dsa::Elem<T>::x4 lds_read_tr(const unsigned char* lds) {
+  const dsa_i16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) dsa_i16x4*)(lds));
+  return __builtin_bit_cast(typename dsa::Elem<T>::x4, raw);
+}
+
+// kRouted: key blocks from the CSR row (false: every key block, dense).
+// kNh: 64-key half-tiles per key block (2 for blocks of 65..128 keys, else 1).
+// kSkip: some half-tile of every block holds at most 32 valid keys (block
+// sizes 65..96, or at most 32), so those steps run one 32-key sub-tile.
+// kGather (routed, whole blocks of 65..127 keys): the row's kept blocks are
+// concatenated, each padded to block_pad keys, and streamed as 64-key chunks,
+// so a 72-key block costs 72 key slots instead of 64 + 32.  Row r of a
+// chunk's K and V stages holds stream position r, so the S^T, P^T and V^T
+// lane layouts are those of the plain stream.
+//
+// kWaves: waves per workgroup, 32 query rows each (4; 2 for routed blocks of
+// at most 64 tokens, whose rows two waves cover: smaller workgroups spread
+// over the four SIMDs instead of leaving two waves per workgroup idle).
+template <typename T, bool kRouted, int kNh, bool kSkip, bool kGather = false, int kWaves = 4>
+__global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
+    bsa_fwd_kernel(BsaParams p) {
+  typedef dsa::Elem<T> E;
+  typedef typename E::x8 x8;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_v1[kKStage];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5;
+  const int qi = lane & 31;
+
+  // Dense: each XCD takes a contiguous range of (b, h) rows, whose workgroups
+  // stream the same keys in lock step through that XCD's L2.  Routed: blocks
+  // stay in launch order, which the hardware deals round-robin over the XCDs,
+  // so every XCD gets an eighth of every head; routes whose keep differs from
+  // head to head (spatially local attention keeps from 0.2 to 0.65 per head)
+  // would otherwise leave the XCDs holding the dense heads working alone
+  // (5.7% of an end-to-end sparse step; 0.6% the other way on i.i.d. routes).
+  const int wg = (int)blockIdx.x;
+  const bool split = wg >= p.split_from;
+  int work, part = 0;
+  if (split) {
+    const int t = wg - p.split_from;
+    work = p.split_from + t / p.parts;
+    part = t % p.parts;
+  } else {
+    work = kRouted ? wg : dsa::xcd_remap(wg, p.split_from);
+  }
+  const int qb = work % p.q_blocks;
+  const int bh = work / p.q_blocks;
+  const int h = bh % p.heads;
+  const int b = bh / p.heads;
+
+  int start = 0, end = p.kv_blocks;
+  if (kRouted) {
+    const dsa_const_i32 rp = (dsa_const_i32)p.row_ptr;
+    const int rb = p.route_batches == 1 ? 0 : b;
+    const int64_t row = ((int64_t)rb * p.heads + h) * p.q_blocks + qb;
+    start = rp[row];
+    end = rp[row + 1];
+  }
+  if (split) {  // key part `part` of the row's blocks
+    const int n = end - start;
+    end = start + (int)((int64_t)n * (part + 1) / p.parts);
+    start = start + (int)((int64_t)n * part / p.parts);
+  }
+  const dsa_const_i32 cidx = (dsa_const_i32)p.col_idx;
+  const int nblk = end - start;
+
+  // Rows past the block (blocks shorter than 128) or the sequence are
+  // computed on a clamped row and never stored; waves wholly past the block
+  // only stage their share of K/V.
+  const int local_row = wave * 32 + qi;
+  const int tq = qb * p.block + local_row;
+  const bool row_ok = local_row < p.block && tq < p.q_tokens;
+  const bool wave_active = wave * 32 < p.block;
+  const int tq_c = tq < p.q_tokens ? tq : p.q_tokens - 1;
+  const T* qrow = static_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh + (int64_t)tq_c * p.q_st;
+  x8 qf[8];
+#pragma unroll
+  for (int dc = 0; dc < 8; ++dc)
+    qf[dc] = *reinterpret_cast<const x8*>(qrow + dc * 16 + g * 8);
+
+  const T* kbase = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh;
+  const T* vbase = static_cast<const T*>(p.v) + b * p.v_sb + h * p.v_sh;
+  // Each wave stages kSlices of the 16 1-KB slices of a K or V stage.
+  static_assert(kWaves == 4 || (kWaves == 2 && !kGather), "2-wave groups: plain stream only");
+  constexpr int kSlices = 16 / kWaves;
+  // Per-lane source offsets (elements) relative to the half-tile's first key.
+  int koff[kSlices], voff[kSlices];
+#pragma unroll
+  for (int j = 0; j < kSlices; ++j) {
+    const int idx = (wave * kSlices + j) * 64 + lane;
+    const int row = idx >> 4;
+    koff[j] = row * (int)p.k_st + k2_swz(row, idx & 15) * 8;
+    voff[j] = row * (int)p.v_st + v_swz(row, idx & 15) * 8;
+  }
+
+  // V^T fragment reads: lane (g, i = lane % 32) of the PV product needs dims
+  // 32 dt + i of the 16-key group's quads (2 g) and (2 g + 1) in slot order,
+  // i.e. key rows 4 g + r and 8 + 4 g + r (r = 0..3; the quad order 0, 2, 1, 3
+  // of the P^T slots).  In its 16-lane group, lane 4 r + c addresses key row
+  // 4 g + r, dims 32 dt + 16 ((lane >> 4) & 1) + 4 c .. + 3; the transposed
+  // read hands every lane its own dim of the 4 rows.  Byte offsets per dt.
+  int vfrag[4];
+  {
+    const int lam = lane & 15, r = lam >> 2, c = lam & 3;
+    const int row = 4 * g + r;
+    const int sub = 2 * ((lane >> 4) & 1) + (c >> 1);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+      vfrag[dt] = row * kRowBytes + v_swz(row, 4 * dt + sub) * 16 + (c & 1) * 8;
+  }
+
+  auto block_of = [&](int j) -> int {
+    const int it = start + j;
+    const int kb = kRouted ? cidx[it] : it;
+    return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
+  };
+
+  // Stages half-tile `half` of key block kb (an invalid block stages block 0,
+  // which is then fully masked).
+  auto issue = [&](int kb, int half, unsigned char* kdst, unsigned char* vdst) {
+    const int kbc = kb < 0 ? 0 : kb;
+    const int key0 = kbc * p.block + half * kHalfKeys;
+    const __amdgpu_buffer_rsrc_t k_rsrc = k_tile_rsrc(kbase, p.k_st, key0, p.kv_tokens);
+    const __amdgpu_buffer_rsrc_t v_rsrc = k_tile_rsrc(vbase, p.v_st, key0, p.kv_tokens);
+#pragma unroll
+    for (int j = 0; j < kSlices; ++j)
+      lds_load16(k_rsrc, kdst + (wave * kSlices + j) * 1024, koff[j] * 2, 0);
+#pragma unroll
+    for (int j = 0; j < kSlices; ++j)
+      lds_load16(v_rsrc, vdst + (wave * kSlices + j) * 1024, voff[j] * 2, 0);
+  };
+  // Stages the 64-key chunk that starts `o0` slots into stream block kb0 and
+  // runs on into kb1 (the blocks are in range; pad and tail slots load
+  // whatever they address, or zeros past the end, and are masked).
+  const __amdgpu_buffer_rsrc_t k_all_rsrc = make_rsrc(
+      kbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.k_st * 2 + kRowBytes));
+  const __amdgpu_buffer_rsrc_t v_all_rsrc = make_rsrc(
+      vbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.v_st * 2 + kRowBytes));
+  auto issue_gather = [&](int kb0, int kb1, int o0, unsigned char* kdst, unsigned char* vdst)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = (wave * 4 + j) * 4 + (lane >> 4);  // stream position o0 + row
+      const int o = o0 + row;
+      const bool first = o < p.block_pad;
+      const uint32_t token =
+          (uint32_t)((first ? kb0 : kb1) * p.block + (first ? o : o - p.block_pad));
+      lds_load16(k_all_rsrc, kdst + (wave * 4 + j) * 1024,
+                 token * (uint32_t)(p.k_st * 2) + (uint32_t)(k2_swz(row, lane & 15) * 16), 0);
+      lds_load16(v_all_rsrc, vdst + (wave * 4 + j) * 1024,
+                 token * (uint32_t)(p.v_st * 2) + (uint32_t)(v_swz(row, lane & 15) * 16), 0);
+    }
+  };
+  // Valid keys of half-tile `half` of block kb (0 for an invalid block).
+  auto valid_of = [&](int kb, int half) -> int {
+    if (kb < 0) return 0;
+    const int key0 = kb * p.block + half * kHalfKeys;
+    int valid = min(kHalfKeys, p.block - half * kHalfKeys);
+    return min(valid, p.kv_tokens - key0);
+  };
+
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  dsa_f32x16 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+
+  // NKT: 32-key sub-tiles of the half-tile that hold valid keys (2, or 1 when
+  // at most 32 are valid: the last half of a 65..96-key block, or a block of
+  // at most 32 keys), so empty sub-tiles cost neither MFMAs nor softmax work.
+  // Gathered stream: `invalid` has bit p set when stream position p of the
+  // chunk is a pad slot, past the row's last key or in an out-of-range block;
+  // accumulator r of lane half g holds position 32 kt + 8 (r >> 2) + 4 g + (r & 3).
+  auto compute = [&](const unsigned char* kt_lds, const unsigned char* v_lds, int valid,
+                     uint64_t invalid, auto nkt_c) __attribute__((always_inline)) {
+    constexpr int NKT = decltype(nkt_c)::value;
+    dsa_f32x16 sacc[NKT];
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+#pragma unroll
+    for (int dc = 0; dc < 8; ++dc) {
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) {
+        const int row = kt * 32 + qi;
+        const x8 a = *reinterpret_cast<const x8*>(
+            kt_lds + row * kRowBytes + k2_swz(row, dc * 2 + g) * 16);
+        sacc[kt] = E::mfma32(a, qf[dc], sacc[kt]);
+      }
+    }
+    if constexpr (kGather) {
+      if (invalid != 0) {
+        const uint64_t mine = invalid >> (4 * g);
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
+          const uint32_t bits = (uint32_t)(mine >> (32 * kt));
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (bits & (1u << (8 * (r >> 2) + (r & 3)))) sacc[kt][r] = -INFINITY;
+        }
+      }
+    } else if (valid < NKT * 32) {
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= valid) sacc[kt][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+    mx = dsa::pair32_max(mx);
+    const float mx2 = mx * p.scale_log2;
+    const bool up = mx2 > m_run + kRescaleLog2;
+    if (__any(up)) {
+      const float alpha = up ? __builtin_amdgcn_exp2f(m_run - mx2) : 1.0f;
+      m_run = up ? mx2 : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    x8 pf[2 * NKT];
+    float sum0 = 0.f, sum1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2 * NKT; ++j) {
+      const int kt = j >> 1, hf = j & 1;
+#pragma unroll
+      for (int t = 0; t < 8; t += 2) {
+        const float p0 =
+            __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t], p.scale_log2, -m_use));
+        const float p1 =
+            __builtin_amdgcn_exp2f(fmaf(sacc[kt][hf * 8 + t + 1], p.scale_log2, -m_use));
+        const dsa_f32x2 two = {p0, p1};
+        const typename E::x2 pb = __builtin_convertvector(two, typename E::x2);
+        sum0 += p0;
+        sum1 += p1;
+        pf[j][t] = pb[0];
+        pf[j][t + 1] = pb[1];
+      }
+    }
+    l_run += sum0 + sum1;
+#pragma unroll
+    for (int j = 0; j < 2 * NKT; ++j) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        // Key rows 16 j + 4 g + r (slots 0..3) and 16 j + 8 + 4 g + r (4..7).
+        const unsigned char* at = v_lds + vfrag[dt] + j * 16 * kRowBytes;
+        const typename E::x4 lo = lds_read_tr<T>(at);
+        const typename E::x4 hi = lds_read_tr<T>(at + 8 * kRowBytes);
+        const x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        oacc[dt] = E::mfma32(a, pf[j], oacc[dt]);
+      }
+    }
+  };
+
+  // One pipelined step: wait for the current stage, prefetch the next
+  // half-tile (next_kb == -2: none), then compute on the current one
+  // (skip_c: this step may hold at most 32 valid keys).
+  auto step = [&](int kb, int half, int next_kb, int next_half, const unsigned char* kc,
+                  const unsigned char* vc, unsigned char* kn, unsigned char* vn,
+                  auto skip_c) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (next_kb != -2) issue(next_kb, next_half, kn, vn);
+    if (wave_active) {
+      const int valid = valid_of(kb, half);
+      if (decltype(skip_c)::value && valid <= 32)
+        compute(kc, vc, valid, 0ull, std::integral_constant<int, 1>{});
+      else
+        compute(kc, vc, valid, 0ull, std::integral_constant<int, 2>{});
+    }
+  };
+  // Gathered stream step: chunk at slot o0 of stream block j0 (whose block
+  // index is kb0; kb0 < 0 or kb1 < 0: out of range), `left` valid stream
+  // slots from the chunk start to the row's last key; next_kb0 == -2: no
+  // next chunk.
+  auto step_gather = [&](int kb0, int kb1, int o0, int left, int next_kb0, int next_kb1,
+                         int next_o0, const unsigned char* kc, const unsigned char* vc,
+                         unsigned char* kn, unsigned char* vn) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (next_kb0 != -2)
+      issue_gather(next_kb0 < 0 ? 0 : next_kb0, next_kb1 < 0 ? 0 : next_kb1, next_o0, kn, vn);
+    if (wave_active) {
+      const int second = p.block_pad - o0;  // first slot of block kb1
+      uint64_t invalid = 0;
+      if (left < 64) invalid = ~0ull << left;
+      if (p.block_pad > p.block) {
+        const int lo = max(p.block - o0, 0);
+        const int hi = min(second, 64);
+        if (lo < hi)
+          invalid |= (hi == 64 ? ~0ull : (1ull << hi) - 1) & ~((1ull << lo) - 1);
+      }
+      if (kb0 < 0) invalid |= second >= 64 ? ~0ull : (1ull << second) - 1;
+      if (kb1 < 0 && second < 64) invalid |= ~0ull << second;
+      if (left <= 32)
+        compute(kc, vc, 0, invalid, std::integral_constant<int, 1>{});
+      else
+        compute(kc, vc, 0, invalid, std::integral_constant<int, 2>{});
+    }
+  };
+  const std::bool_constant<false> no_skip;
+  const std::bool_constant<kSkip> may_skip;
+
+  if (kGather && nblk > 0) {
+    // Stream block j: CSR entry j clamped to the row (slots past the row's
+    // last key are masked), -1 when out of range.
+    auto gblock = [&](int j) -> int {
+      const int kb = cidx[start + (j < nblk ? j : nblk - 1)];
+      return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
+    };
+    const int bp = p.block_pad;
+    const int total = (nblk - 1) * bp + p.block;  // slots up to the row's last key
+    const int chunks = (total + 63) >> 6;
+    int j0 = 0, o0 = 0;
+    int kb0 = gblock(0), kb1 = gblock(1);
+    issue_gather(kb0 < 0 ? 0 : kb0, kb1 < 0 ? 0 : kb1, 0, lds_k0, lds_v0);
+    for (int c = 0; c < chunks; c += 2) {
+      int j1 = j0, o1 = o0 + 64;
+      if (o1 >= bp) { o1 -= bp; ++j1; }
+      const bool more1 = c + 1 < chunks;
+      const int kb0n = more1 ? gblock(j1) : -2, kb1n = more1 ? gblock(j1 + 1) : -2;
+      step_gather(kb0, kb1, o0, total - c * 64, kb0n, kb1n, o1, lds_k0, lds_v0, lds_k1,
+                  lds_v1);
+      if (!more1) break;
+      int j2 = j1, o2 = o1 + 64;
+      if (o2 >= bp) { o2 -= bp; ++j2; }
+      const bool more2 = c + 2 < chunks;
+      const int kb0m = more2 ? gblock(j2) : -2, kb1m = more2 ? gblock(j2 + 1) : -2;
+      step_gather(kb0n, kb1n, o1, total - (c + 1) * 64, kb0m, kb1m, o2, lds_k1, lds_v1,
+                  lds_k0, lds_v0);
+      j0 = j2; o0 = o2; kb0 = kb0m; kb1 = kb1m;
+    }
+  } else if (!kGather && nblk > 0) {
+    int kb = block_of(0);
+    issue(kb, 0, lds_k0, lds_v0);
+    if (kNh == 2) {
+      // The first half of a 65..128-key block always holds 64 keys (short
+      // only at the sequence end, which the masked two-sub-tile path covers).
+      for (int j = 0; j < nblk; ++j) {
+        const int kb_after = j + 1 < nblk ? block_of(j + 1) : -2;
+        step(kb, 0, kb, 1, lds_k0, lds_v0, lds_k1, lds_v1, no_skip);
+        step(kb, 1, kb_after, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip);
+        kb = kb_after;
+      }
+    } else {
+      for (int j = 0; j < nblk; j += 2) {
+        const int kb1 = j + 1 < nblk ? block_of(j + 1) : -2;
+        step(kb, 0, kb1, 0, lds_k0, lds_v0, lds_k1, lds_v1, may_skip);
+        if (kb1 == -2) break;
+        const int kb2 = j + 2 < nblk ? block_of(j + 2) : -2;
+        step(kb1, 0, kb2, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip);
+        kb = kb2;
+      }
+    }
+  }
+
+  const float l_tot = dsa::pair32_sum(l_run);
+  if (split) {
+    if (row_ok) {
+      float* po = p.part + (int64_t)(wg - p.split_from) * kPartFloats;
+      float* prow = po + local_row * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const dsa_f32x4 v4 = {oacc[dt][rr * 4 + 0], oacc[dt][rr * 4 + 1],
+                                oacc[dt][rr * 4 + 2], oacc[dt][rr * 4 + 3]};
+          *reinterpret_cast<dsa_f32x4*>(prow + dt * 32 + rr * 8 + g * 4) = v4;
+        }
+      if (g == 0) {
+        po[128 * 128 + local_row] = m_run;
+        po[128 * 128 + 128 + local_row] = l_tot;
+      }
+    }
+    return;
+  }
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (row_ok) {
+    T* orow = static_cast<T*>(p.o) + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const dsa_f32x2 lo = {oacc[dt][rr * 4 + 0] * inv, oacc[dt][rr * 4 + 1] * inv};
+        const dsa_f32x2 hi = {oacc[dt][rr * 4 + 2] * inv, oacc[dt][rr * 4 + 3] * inv};
+        const typename E::x2 blo = __builtin_convertvector(lo, typename E::x2);
+        const typename E::x2 bhi = __builtin_convertvector(hi, typename E::x2);
+        const typename E::x4 v4 = {blo[0], blo[1], bhi[0], bhi[1]};
+        *reinterpret_cast<typename E::x4*>(orow + dt * 32 + rr * 8 + g * 4) = v4;
+      }
+    if (p.lse && g == 0) {
+      p.lse[((int64_t)b * p.heads + h) * p.q_tokens + tq] =
+          l_tot > 0.f ? m_run * 0.6931471805599453f + logf(l_tot) : -INFINITY;
+    }
+  }
+}
+
+// Combines the `parts` partials of each split query block: with M the largest
+// row max, O = sum_i O_i 2^(m_i - M) / sum_i l_i 2^(m_i - M) and
+// LSE = M ln 2 + ln(sum_i l_i 2^(m_i - M)).  Two threads per row, 64 dims each.
+template <typename T>
+__global__ void __launch_bounds__(256) bsa_merge_kernel(BsaParams p) {
+  const int item = blockIdx.x;
+  const int work = p.split_from + item;
+  const int qb = work % p.q_blocks;
+  const int bh = work / p.q_blocks;
+  const int h = bh % p.heads;
+  const int b = bh / p.heads;
+  const int r = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const int tq = qb * p.block + r;
+  if (r >= p.block || tq >= p.q_tokens) return;
+  const float* base = p.part + (int64_t)item * p.parts * kPartFloats;
+  float m_max = -INFINITY;
+  for (int i = 0; i < p.parts; ++i) m_max = fmaxf(m_max, base[i * kPartFloats + 128 * 128 + r]);
+  float w[8];
+  float l = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    w[i] = 0.f;
+    if (i < p.parts) {
+      const float m_i = base[i * kPartFloats + 128 * 128 + r];
+      w[i] = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m_max);
+      l = fmaf(w[i], base[i * kPartFloats + 128 * 128 + 128 + r], l);
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* orow = static_cast<T*>(p.o) + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
+  for (int c = half * 8; c < half * 8 + 8; ++c) {  // 8-dim chunks of this thread's 64
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i >= p.parts) break;
+      const float* src = base + i * kPartFloats + r * kHeadDim + c * 8;
+      const dsa_f32x4 a = *reinterpret_cast<const dsa_f32x4*>(src);
+      const dsa_f32x4 bq = *reinterpret_cast<const dsa_f32x4*>(src + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[e] = fmaf(w[i], a[e], acc[e]);
+        acc[4 + e] = fmaf(w[i], bq[e], acc[4 + e]);
+      }
+    }
+    typename dsa::Elem<T>::x8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = (T)(acc[e] * inv);
+    *reinterpret_cast<typename dsa::Elem<T>::x8*>(orow + c * 8) = out;
+  }
+  if (p.lse && half == 0)
+    p.lse[((int64_t)b * p.heads + h) * p.q_tokens + tq] =
+        l > 0.f ? m_max * 0.6931471805599453f + logf(l) : -INFINITY;
+}
+
+inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+constexpr int kMaxDevices = 64;
+
+// The device `stream` belongs to (the current device for the null stream), or
+// -1 when it cannot be told.
+inline int stream_device(hipStream_t stream) {
+  int device = -1;
+  if (stream == nullptr || hipStreamGetDevice(stream, &device) != hipSuccess) {
+    if (hipGetDevice(&device) != hipSuccess) return -1;
+  }
+  return device >= 0 && device < kMaxDevices ? device : -1;
+}
+
+// Workgroup slots (two attention workgroups per CU) of the stream's device,
+// cached per device.
+inline int device_slots(hipStream_t stream) {
+  static int slots[kMaxDevices] = {0};
+  const int device = stream_device(stream);
+  if (device < 0) return 0;
+  if (slots[device] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+      return 0;
+    slots[device] = 2 * cus;
+  }
+  return slots[device];
+}
+
+// Split of the last round: the last k of n query blocks each run as `parts`
+// key ranges, chosen to minimise the predicted time in rounds of one
+// workgroup's time, (n - k) / slots + ceil(parts k / slots) / parts, over k =
+// n mod slots (or that plus one round) and 2..max_parts parts, at most
+// max_groups split workgroups.  Returns k (0: no split).
+inline int choose_split(int64_t n, int slots, int max_parts, int64_t max_groups, int* parts) {
+  *parts = 1;
+  if (slots <= 0 || n <= 0 || max_parts < 2) return 0;
+  const int64_t rem = n % slots;
+  if (rem == 0) return 0;
+  double best = (double)((n + slots - 1) / slots) - 0.05;  // split only for a clear gain
+  int best_k = 0;
+  for (int extra = 0; extra <= 1; ++extra) {
+    const int64_t k = rem + (int64_t)extra * slots;
+    if (k > n) break;
+    for (int pp = 2; pp <= max_parts; ++pp) {
+      if (k * pp > max_groups) break;
+      const double t = (double)((n - k) / slots) +
+                       (double)((k * pp + slots - 1) / slots) / (double)pp;
+      if (t < best) {
+        best = t;
+        best_k = (int)k;
+        *parts = pp;
+      }
+    }
+  }
+  if (best_k == 0) *parts = 1;
+  return best_k;
+}
+
+// Parts a split query block may take: at least 8 key blocks per part of the
+// whole key range (short ranges, such as 512 text tokens, gain less than the
+// merge costs), at most 8.
+inline int max_parts_for(int32_t kv_blocks) { return std::min(8, kv_blocks / 8); }
+
+constexpr size_t kPartBytes = sizeof(float) * kPartFloats;
+
+// Routed calls take the gathered key stream when every key block is whole and
+// holds 65..127 keys and its 8-rounded size is below the plain layout's slots
+// per block (64 + 32 up to 96 keys, else 128), and the whole K and V
+// sequences of one head each span < 2 GiB (one buffer resource addresses each).
+inline bool use_gather(int32_t block, int32_t kv_tokens, int64_t k_token_stride,
+                int64_t v_token_stride) {
+  if (block <= kHalfKeys || block >= 2 * kHalfKeys || kv_tokens % block != 0) return false;
+  const int32_t pad = (block + 7) & ~7;
+  const int32_t plain = block - kHalfKeys <= 32 ? kHalfKeys + 32 : 2 * kHalfKeys;
+  if (pad >= plain) return false;
+  const int64_t stride = std::max(k_token_stride, v_token_stride);
+  return ((int64_t)kv_tokens + 8) * stride * 2 + kRowBytes <= 0x7fffffff;
+}
+
+// Validates the arguments of an attention call and fills `p` (without the
+// split fields).  Returns DSA_OK or the error status.
+template <typename T>
+int launch_typed(BsaParams p, float* part, int64_t part_groups, hipStream_t stream,
+                 const char* who) {
+  const int64_t grid = (int64_t)p.batch * p.heads * p.q_blocks;
+  int parts = 1;
+  const int split = choose_split(grid, device_slots(stream), max_parts_for(p.kv_blocks),
+                                 std::min<int64_t>(part_groups, kMaxPartGroups), &parts);
+  p.split_from = (int32_t)(grid - split);
+  p.parts = parts;
+  p.part = part;
+  const dim3 blocks((unsigned)(grid - split + (int64_t)split * parts)), threads(256),
+      two_waves(128);
+  const int32_t nh = p.block > kHalfKeys ? 2 : 1;
+  // Blocks whose last half-tile holds 1..32 keys run it as one sub-tile.
+  const int rem = p.block % kHalfKeys;
+  const bool skip = rem != 0 && rem <= 32;
+  auto four = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p); };
+  auto two = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, two_waves, 0, stream, p); };
+  if (p.row_ptr && use_gather(p.block, p.kv_tokens, p.k_st, p.v_st)) {
+    four(bsa_fwd_kernel<T, true, 2, true, true>);
+  } else if (p.row_ptr) {
+    if (nh == 2) skip ? four(bsa_fwd_kernel<T, true, 2, true>) : four(bsa_fwd_kernel<T, true, 2, false>);
+    else skip ? two(bsa_fwd_kernel<T, true, 1, true, false, 2>)
+              : two(bsa_fwd_kernel<T, true, 1, false, false, 2>);
+  } else {
+    if (nh == 2) skip ? four(bsa_fwd_kernel<T, false, 2, true>) : four(bsa_fwd_kernel<T, false, 2, false>);
+    else skip ? four(bsa_fwd_kernel<T, false, 1, true>) : four(bsa_fwd_kernel<T, false, 1, false>);
+  }
+  if (split > 0)
+    hipLaunchKernelGGL(bsa_merge_kernel<T>, dim3((unsigned)split), dim3(256), 0, stream, p);
+  return dsa::check_launch(who);
+}
+
+}  // namespace bsa
+
+// fp16 instances (bsa_fwd_f16.hip).
+int bsa_launch_f16(bsa::BsaParams p, float* part, int64_t part_groups, hipStream_t stream,
+                   const char* who);

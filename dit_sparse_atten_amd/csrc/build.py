@@ -24,8 +24,10 @@ OBJECTS = PACKAGE / "_build"
 SOURCES = (
     "dsa_api.hip",
     "bsa_fwd.hip",
+    "bsa_fwd_f16.hip",
     "block_mass.hip",
     "tile_stats.hip",
+    "sampled_mass.hip",
     "route.hip",
     "routing.hip",
     "tile_route.hip",

@@ -25,8 +25,41 @@ typedef float dsa_f32x4 __attribute__((ext_vector_type(4)));
 typedef float dsa_f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t dsa_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t dsa_u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 dsa_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 dsa_f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 dsa_f16x2 __attribute__((ext_vector_type(2)));
+typedef short dsa_i16x4 __attribute__((ext_vector_type(4)));
+
+// Input element types (the dtype codes of dsa.h).
+#define DSA_BF16 0
+#define DSA_F16 1
 
 namespace dsa {
+
+// The 16-bit input types share one MFMA shape (32x32x16, fp32 accumulate)
+// and one LDS layout; Elem<T> names the vector types and the matrix op.
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<__bf16> {
+  typedef dsa_bf16x8 x8;
+  typedef dsa_bf16x4 x4;
+  typedef dsa_bf16x2 x2;
+  static __device__ __forceinline__ dsa_f32x16 mfma32(x8 a, x8 b, dsa_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Elem<_Float16> {
+  typedef dsa_f16x8 x8;
+  typedef dsa_f16x4 x4;
+  typedef dsa_f16x2 x2;
+  static __device__ __forceinline__ dsa_f32x16 mfma32(x8 a, x8 b, dsa_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
 
 // Records an error message for dsa_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...);

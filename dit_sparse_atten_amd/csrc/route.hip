@@ -1,8 +1,8 @@
-// Sampled route update for gfx950: block-mass estimate, persistence prior,
-// top-mass selection, first-frame sink and CSR construction.
+// Sampled route update for gfx950: persistence prior, top-mass selection,
+// first-frame sink and CSR construction.
 //
-// Replaces attention_backends/flex.py:
-//   _sampled_block_mass   205-251  -> sampled_mass_kernel (one fused launch)
+// Replaces attention_backends/flex.py (the sampled mass itself,
+// _sampled_block_mass 205-251, is sampled_mass.hip):
 //   prior + _top_mass_route + _add_first_frame_sink
 //                         83-94, 535-548, 550-566 -> route_select_kernel
 //   _pack_route / _build_block_mask (KV direction)
@@ -27,222 +27,6 @@ using dsa::wave_sum_i64;
 
 constexpr int kHeadDim = 128;
 constexpr float kLog2e = 1.4426950408889634f;
-
-// ---------------------------------------------------------------------------
-// Sampled block mass
-// ---------------------------------------------------------------------------
-
-struct MassParams {
-  const __bf16* q;
-  const __bf16* k;
-  float* mass;  // [heads, blocks, blocks]
-  int64_t q_st, q_sh, k_st, k_sh;
-  int32_t tokens, heads, blocks, block_size;
-  float scale;        // score scale (d^-1/2 unless given)
-  float logw_full;    // log(block_size / samples)
-  float logw_last;    // log(size of the last block / samples)
-};
-
-// Token index of sampled slot j (block j / S, sample j % S), flex.py:224-231.
-template <int S>
-__device__ __forceinline__ int sampled_token(int j, int tokens, int block_size) {
-  const int blk = j / S;
-  const int s = j % S;
-  int size = tokens - blk * block_size;
-  size = size < block_size ? size : block_size;
-  int local = ((2 * s + 1) * size) / (2 * S);
-  local = local < size - 1 ? local : size - 1;
-  return blk * block_size + local;
-}
-
-// bf16 rounding (round to nearest even) of two fp32 values, returned as fp32.
-__device__ __forceinline__ void round_bf16_pair(float a, float b, float& ra, float& rb) {
-  const dsa_f32x2 two = {a, b};
-  const dsa_bf16x2 h = __builtin_convertvector(two, dsa_bf16x2);
-  const uint32_t bits = __builtin_bit_cast(uint32_t, h);
-  ra = __builtin_bit_cast(float, bits << 16);
-  rb = __builtin_bit_cast(float, bits & 0xFFFF0000u);
-}
-
-// One workgroup (4 waves x 32 sampled queries) scans every sampled key twice:
-// sweep 1 builds each query's log-sum-exp, sweep 2 sums the normalised
-// probabilities per (query block, key block).  The sampled score matrix is
-// never written to memory.  The scan is VALU-bound (the per-score rounding
-// and softmax work outweighs the 32x32x16 MFMAs several times), so scores
-// are rounded in pairs, the log2(e) scale and log-weight fold into one fma,
-// the max runs over the rounded scores, and only the tile holding the
-// sequence's last sampled keys pays the per-score tail checks.  Sampled key
-// rows are gathered straight into LDS (buffer loads with a per-lane row
-// offset), double-buffered one 64-key tile ahead of the compute.
-template <int S>
-__global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
-  constexpr int kTileKeys = 64;
-  constexpr int KBS = 32 / S;  // key blocks covered by one 32-key sub-tile
-  __shared__ __attribute__((aligned(1024))) unsigned char st0[kTileKeys * 256];
-  __shared__ __attribute__((aligned(1024))) unsigned char st1[kTileKeys * 256];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 5;
-  const int qi = lane & 31;
-  const int h = blockIdx.y;
-  const int ns = p.blocks * S;
-  const int tiles = (ns + kTileKeys - 1) / kTileKeys;
-  const int q0 = blockIdx.x * 128 + wave * 32;  // first sampled query of this wave
-
-  int qs = q0 + qi;
-  qs = qs < ns ? qs : ns - 1;
-  const __bf16* qrow =
-      p.q + h * p.q_sh + (int64_t)sampled_token<S>(qs, p.tokens, p.block_size) * p.q_st;
-  dsa_bf16x8 qf[8];
-#pragma unroll
-  for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
-
-  // The head's K rows as one raw buffer (the host keeps them within 2^31 bytes).
-  const __bf16* kbase = p.k + h * p.k_sh;
-  const __amdgpu_buffer_rsrc_t k_rsrc =
-      dsa::make_rsrc(kbase, (uint32_t)(((int64_t)(p.tokens - 1) * p.k_st + kHeadDim) * 2));
-  // This lane's 4 chunks of tile t: LDS slot idx = (wave * 4 + j) * 64 + lane
-  // holds chunk (idx & 15) ^ (row & 15) of tile row idx >> 4.
-  auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
-    const int kt0 = t * kTileKeys;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int idx = (wave * 4 + j) * 64 + lane;
-      const int row = idx >> 4;
-      const int c = (idx & 15) ^ (row & 15);
-      int key = kt0 + row;
-      key = key < ns ? key : ns - 1;
-      const uint32_t off = (uint32_t)(
-          ((int64_t)sampled_token<S>(key, p.tokens, p.block_size) * p.k_st + c * 8) * 2);
-      dsa::lds_load16(k_rsrc, dst + (wave * 4 + j) * 1024, off, 0);
-    }
-  };
-
-  const int last_block = p.blocks - 1;
-  const float c_full = p.logw_full * kLog2e;
-  const float c_last = p.logw_last * kLog2e;
-  // Tiles before this one hold only full, in-range key blocks.
-  const int first_tail_tile = (last_block * S) / kTileKeys;
-  float m2 = -INFINITY, l2 = 0.f, lse2 = 0.f;
-
-  auto compute = [&](const unsigned char* lds_k, int t, int sweep) __attribute__((always_inline)) {
-    const int kt0 = t * kTileKeys;
-    const bool tail = t >= first_tail_tile;
-#pragma unroll
-    for (int sub = 0; sub < kTileKeys / 32; ++sub) {
-      dsa_f32x16 acc;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-#pragma unroll
-      for (int dc = 0; dc < 8; ++dc) {
-        const int key = sub * 32 + qi;
-        const int c = dc * 2 + g;
-        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
-            lds_k + key * 256 + ((c ^ (key & 15)) << 4));
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], acc, 0, 0, 0);
-      }
-      // Score = bf16(bf16(q.k) * scale), as a bf16 matmul and a bf16 scale
-      // multiply; the softmax input in log2 units is score * log2e + c with
-      // c = log(block size / S) * log2e.
-      float sc[16], cw[16];
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float a0, a1;
-        round_bf16_pair(acc[r], acc[r + 1], a0, a1);
-        round_bf16_pair(a0 * p.scale, a1 * p.scale, sc[r], sc[r + 1]);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) cw[r] = c_full;
-      if (tail) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = kt0 + sub * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          cw[r] = j / S == last_block ? c_last : c_full;
-          if (j >= ns) sc[r] = -INFINITY;
-        }
-      }
-      if (sweep == 0) {
-        // Running max of x = score * log2e + c (log2e > 0: c_last differs
-        // from c_full only in the tail).
-        float mx = m2;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaf(sc[r], kLog2e, cw[r]));
-        float sum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          sum += __builtin_amdgcn_exp2f(fmaf(sc[r], kLog2e, cw[r] - mx));
-        l2 = l2 * __builtin_amdgcn_exp2f(m2 - mx) + sum;
-        m2 = mx;
-      } else {
-        float pk[KBS];
-#pragma unroll
-        for (int b = 0; b < KBS; ++b) pk[b] = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int local = 8 * (r >> 2) + 4 * g + (r & 3);
-          pk[local / S] += __builtin_amdgcn_exp2f(fmaf(sc[r], kLog2e, cw[r] - lse2));
-        }
-        // Sum over the S query lanes of each query block and both halves.
-#pragma unroll
-        for (int b = 0; b < KBS; ++b) {
-#pragma unroll
-          for (int m = 1; m < S; m <<= 1) pk[b] += __shfl_xor(pk[b], m);
-          pk[b] += __shfl_xor(pk[b], 32);
-        }
-        if (g == 0 && (qi % S) == 0) {
-          const int qs_first = q0 + qi;
-          if (qs_first < ns) {
-            const int qb = qs_first / S;
-            float* out = p.mass + ((int64_t)h * p.blocks + qb) * p.blocks;
-#pragma unroll
-            for (int b = 0; b < KBS; ++b) {
-              const int kb = (kt0 + sub * 32) / S + b;
-              if (kb < p.blocks) out[kb] = pk[b] * (1.0f / S);
-            }
-          }
-        }
-      }
-    }
-  };
-
-  // Step: wait for the current tile (and every older memory operation),
-  // barrier (all waves' loads landed; every wave done with the other stage),
-  // prefetch the next tile into the other stage, compute the current one.
-  auto step = [&](int t, int sweep, int next_t, const unsigned char* cur,
-                  unsigned char* nxt) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (next_t >= 0) issue(next_t, nxt);
-    compute(cur, t, sweep);
-  };
-
-  for (int sweep = 0; sweep < 2; ++sweep) {
-    issue(0, st0);
-    for (int t = 0; t < tiles; t += 2) {
-      step(t, sweep, t + 1 < tiles ? t + 1 : -1, st0, st1);
-      if (t + 1 >= tiles) break;
-      step(t + 1, sweep, t + 2 < tiles ? t + 2 : -1, st1, st0);
-    }
-    if (sweep == 0) {  // each query's log-sum-exp (log2 units)
-      // Lanes l and l ^ 32 hold the two halves of one query's keys; both get
-      // the same total (the pair's two terms in one fixed order, so a
-      // contracted fma rounds alike in both lanes).
-      const auto ms = __builtin_amdgcn_permlane32_swap(__float_as_uint(m2), __float_as_uint(m2),
-                                                       false, false);
-      const auto ls = __builtin_amdgcn_permlane32_swap(__float_as_uint(l2), __float_as_uint(l2),
-                                                       false, false);
-      const float ma = __uint_as_float(ms[0]), mb = __uint_as_float(ms[1]);
-      const float mx = fmaxf(ma, mb);
-      const float tot = __uint_as_float(ls[0]) * __builtin_amdgcn_exp2f(ma - mx) +
-                        __uint_as_float(ls[1]) * __builtin_amdgcn_exp2f(mb - mx);
-      lse2 = mx + __builtin_log2f(tot);
-      __syncthreads();  // every wave done with st0/st1 before sweep 2 refills st0
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Top-mass selection: one wave per (head, query-block) row, K <= 64 * kPer
@@ -451,61 +235,6 @@ __global__ void __launch_bounds__(256) pack_rows_kernel(const uint8_t* route, in
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 }  // namespace
-
-extern "C" int dsa_sampled_mass(const void* q, const void* k, const int64_t* strides,
-                                int32_t tokens, int32_t heads, int32_t head_dim,
-                                int32_t block_size, int32_t samples, float scale, float* mass,
-                                hipStream_t stream) {
-  dsa::clear_error();
-  if (!q || !k || !mass || !strides)
-    return dsa::set_error(DSA_EINVAL, "dsa_sampled_mass: null pointer");
-  if (tokens <= 0 || heads <= 0 || block_size <= 0)
-    return dsa::set_error(DSA_EINVAL, "dsa_sampled_mass: tokens/heads/block must be positive");
-  if (head_dim != kHeadDim)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_sampled_mass: head_dim %d unsupported (128)",
-                          head_dim);
-  if (samples <= 0 || samples > block_size)
-    return dsa::set_error(DSA_EINVAL, "route_samples must be in [1, block_size]");
-  if (samples > 32 || (samples & (samples - 1)) != 0)
-    return dsa::set_error(DSA_EUNSUPPORTED,
-                          "dsa_sampled_mass: samples must be a power of two <= 32 (got %d)",
-                          samples);
-  if (!(scale > 0.f)) return dsa::set_error(DSA_EINVAL, "dsa_sampled_mass: scale must be > 0");
-  if (!aligned16(q) || !aligned16(k))
-    return dsa::set_error(DSA_EINVAL, "dsa_sampled_mass: q/k must be 16-byte aligned");
-  for (int i = 0; i < 4; ++i)
-    if (strides[i] % 8 != 0 || strides[i] < 0)
-      return dsa::set_error(DSA_EINVAL,
-                            "dsa_sampled_mass: stride %d not a non-negative multiple of 8", i);
-  if (((int64_t)(tokens - 1) * strides[2] + kHeadDim) * 2 > 0x7fffffff)
-    return dsa::set_error(DSA_EUNSUPPORTED,
-                          "dsa_sampled_mass: one head's K rows must span < 2 GiB");
-  MassParams p;
-  p.q = static_cast<const __bf16*>(q);
-  p.k = static_cast<const __bf16*>(k);
-  p.mass = mass;
-  p.q_st = strides[0]; p.q_sh = strides[1]; p.k_st = strides[2]; p.k_sh = strides[3];
-  p.tokens = tokens;
-  p.heads = heads;
-  p.block_size = block_size;
-  p.blocks = (tokens + block_size - 1) / block_size;
-  p.scale = scale;
-  // fp32 log of an fp32 quotient, as torch's (sizes.float() / samples).log().
-  const int last = tokens - (p.blocks - 1) * block_size;
-  p.logw_full = logf((float)block_size / (float)samples);
-  p.logw_last = logf((float)last / (float)samples);
-  const int ns = p.blocks * samples;
-  const dim3 grid((unsigned)((ns + 127) / 128), (unsigned)heads);
-  switch (samples) {
-    case 1: hipLaunchKernelGGL(sampled_mass_kernel<1>, grid, dim3(256), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL(sampled_mass_kernel<2>, grid, dim3(256), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL(sampled_mass_kernel<4>, grid, dim3(256), 0, stream, p); break;
-    case 8: hipLaunchKernelGGL(sampled_mass_kernel<8>, grid, dim3(256), 0, stream, p); break;
-    case 16: hipLaunchKernelGGL(sampled_mass_kernel<16>, grid, dim3(256), 0, stream, p); break;
-    default: hipLaunchKernelGGL(sampled_mass_kernel<32>, grid, dim3(256), 0, stream, p); break;
-  }
-  return dsa::check_launch("dsa_sampled_mass");
-}
 
 extern "C" int dsa_route_select(const float* mass, const uint8_t* previous, int32_t rows,
                                 int32_t keys, float rho, float target, int32_t cap,

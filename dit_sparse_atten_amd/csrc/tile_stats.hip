@@ -48,8 +48,8 @@ constexpr int kMaxTiles = 2048;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct TileStatsParams {
-  const __bf16* q;
-  const __bf16* k;
+  const void* q;  // element type T of the kernel instance
+  const void* k;
   const float* lse;
   const int32_t* row_ptr;  // null: every key tile
   const int32_t* col_idx;
@@ -73,8 +73,9 @@ __device__ __forceinline__ float axis_offset(int i, int length) {
 }
 
 // kWaves: waves per workgroup, one per 32 query rows of the tile (2..4).
-template <bool kRouted, int kNh, bool kGather = false, int kWaves = 4>
+template <typename T, bool kRouted, int kNh, bool kGather = false, int kWaves = 4>
 __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsParams p) {
+  typedef dsa::Elem<T> E;
   constexpr int kThreads = kWaves * 64;
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
@@ -106,11 +107,11 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
   const bool row_ok = local_row < p.tile && tq < p.tokens;
   const bool wave_active = wave * 32 < p.tile;
   const int tq_c = tq < p.tokens ? tq : p.tokens - 1;
-  const __bf16* qrow = p.q + h * p.q_sh + (int64_t)tq_c * p.q_st;
-  dsa_bf16x8 qf[8];
+  const T* qrow = static_cast<const T*>(p.q) + h * p.q_sh + (int64_t)tq_c * p.q_st;
+  typename E::x8 qf[8];
 #pragma unroll
   for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const dsa_bf16x8*>(qrow + dc * 16 + g * 8);
+    qf[dc] = *reinterpret_cast<const typename E::x8*>(qrow + dc * 16 + g * 8);
   const float lse2 = row_ok ? p.lse[h * p.lse_sh + tq] * kLog2e : INFINITY;
 
   int start = 0, end = p.tiles;
@@ -126,7 +127,7 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
   };
   const int ntile = end - start;
 
-  const __bf16* kbase = p.k + h * p.k_sh;
+  const T* kbase = static_cast<const T*>(p.k) + h * p.k_sh;
   int koff[4];
   dsa::k_tile_offsets(wave, lane, p.k_st, koff);
   auto issue = [&](int kt, int half, unsigned char* dst) __attribute__((always_inline)) {
@@ -192,9 +193,9 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
       const int row = kk * 32 + qi;
 #pragma unroll
       for (int dc = 0; dc < 8; ++dc) {
-        const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
+        const typename E::x8 a = *reinterpret_cast<const typename E::x8*>(
             cur + row * kRowBytes + dsa::k2_swz(row, dc * 2 + g) * 16);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], sacc, 0, 0, 0);
+        sacc = E::mfma32(a, qf[dc], sacc);
       }
 #pragma unroll
       for (int quad = 0; quad < 4; ++quad) {
@@ -270,9 +271,9 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
         const int row = kk * 32 + qi;
 #pragma unroll
         for (int dc = 0; dc < 8; ++dc) {
-          const dsa_bf16x8 a = *reinterpret_cast<const dsa_bf16x8*>(
+          const typename E::x8 a = *reinterpret_cast<const typename E::x8*>(
               cur + row * kRowBytes + dsa::k2_swz(row, dc * 2 + g) * 16);
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], sacc, 0, 0, 0);
+          sacc = E::mfma32(a, qf[dc], sacc);
         }
 #pragma unroll
         for (int quad = 0; quad < 4; ++quad) {
@@ -398,9 +399,45 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
+template <typename T>
+void launch_tile_stats(const TileStatsParams& p, bool routed, bool gather, hipStream_t stream) {
+  const int32_t tile = p.tile;
+  const dim3 blocks((unsigned)((int64_t)p.heads * p.tiles)), threads(256);
+  if (gather && tile <= 96) {
+    const dim3 three(192);
+    if (routed)
+      hipLaunchKernelGGL((tile_stats_kernel<T, true, 2, true, 3>), blocks, three, 0, stream, p);
+    else
+      hipLaunchKernelGGL((tile_stats_kernel<T, false, 2, true, 3>), blocks, three, 0, stream, p);
+  } else if (gather) {
+    if (routed)
+      hipLaunchKernelGGL((tile_stats_kernel<T, true, 2, true, 4>), blocks, threads, 0, stream, p);
+    else
+      hipLaunchKernelGGL((tile_stats_kernel<T, false, 2, true, 4>), blocks, threads, 0, stream, p);
+  } else if (tile > 96) {
+    if (routed)
+      hipLaunchKernelGGL((tile_stats_kernel<T, true, 2>), blocks, threads, 0, stream, p);
+    else
+      hipLaunchKernelGGL((tile_stats_kernel<T, false, 2>), blocks, threads, 0, stream, p);
+  } else if (tile > kHalfKeys) {
+    if (routed)
+      hipLaunchKernelGGL((tile_stats_kernel<T, true, 2, false, 3>), blocks, dim3(192), 0, stream, p);
+    else
+      hipLaunchKernelGGL((tile_stats_kernel<T, false, 2, false, 3>), blocks, dim3(192), 0, stream, p);
+  } else {
+    // Two waves even for tiles of at most 32 tokens (one of them then only
+    // stages K): one-wave workgroups, four per CU, leave too few waves to
+    // hide the dense pass's latency.
+    if (routed)
+      hipLaunchKernelGGL((tile_stats_kernel<T, true, 1, false, 2>), blocks, dim3(128), 0, stream, p);
+    else
+      hipLaunchKernelGGL((tile_stats_kernel<T, false, 1, false, 2>), blocks, dim3(128), 0, stream, p);
+  }
+}
+
 }  // namespace
 
-extern "C" int dsa_tile_stats(const void* q, const void* k, const int64_t* strides,
+extern "C" int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const int64_t* strides,
                               int32_t tokens, int32_t heads, int32_t head_dim, int32_t tile_h,
                               int32_t tile_w, const float* lse, int64_t lse_head_stride,
                               const int32_t* row_ptr, const int32_t* col_idx, float scale,
@@ -410,6 +447,9 @@ extern "C" int dsa_tile_stats(const void* q, const void* k, const int64_t* strid
   dsa::clear_error();
   if (!q || !k || !strides || !lse || !mass)
     return dsa::set_error(DSA_EINVAL, "dsa_tile_stats: null pointer argument");
+  if (dtype != DSA_BF16 && dtype != DSA_F16)
+    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_tile_stats: dtype %d unsupported (bf16 or fp16)",
+                          dtype);
   if ((row_ptr == nullptr) != (col_idx == nullptr))
     return dsa::set_error(DSA_EINVAL, "dsa_tile_stats: row_ptr and col_idx must both be set");
   if (tokens <= 0 || heads <= 0)
@@ -445,8 +485,8 @@ extern "C" int dsa_tile_stats(const void* q, const void* k, const int64_t* strid
     return dsa::set_error(DSA_EINVAL, "dsa_tile_stats: grid too large");
 
   TileStatsParams p;
-  p.q = static_cast<const __bf16*>(q);
-  p.k = static_cast<const __bf16*>(k);
+  p.q = q;
+  p.k = k;
   p.lse = lse;
   p.row_ptr = row_ptr;
   p.col_idx = col_idx;
@@ -467,40 +507,13 @@ extern "C" int dsa_tile_stats(const void* q, const void* k, const int64_t* strid
   p.tile_w = tile_w;
   p.tile_pad = (tile + 7) & ~7;
   p.scale_log2 = scale * kLog2e;
-  const dim3 blocks((unsigned)grid), threads(256);
   const bool routed = row_ptr != nullptr;
   const int32_t plain_slots = tile - kHalfKeys <= 32 ? kHalfKeys + 32 : 2 * kHalfKeys;
   const bool gather = tile > kHalfKeys && tile < 2 * kHalfKeys && p.tile_pad < plain_slots &&
                       ((int64_t)tokens + 8) * strides[2] * 2 + kRowBytes <= 0x7fffffff;
-  if (gather && tile <= 96) {
-    const dim3 three(192);
-    if (routed)
-      hipLaunchKernelGGL((tile_stats_kernel<true, 2, true, 3>), blocks, three, 0, stream, p);
-    else
-      hipLaunchKernelGGL((tile_stats_kernel<false, 2, true, 3>), blocks, three, 0, stream, p);
-  } else if (gather) {
-    if (routed)
-      hipLaunchKernelGGL((tile_stats_kernel<true, 2, true, 4>), blocks, threads, 0, stream, p);
-    else
-      hipLaunchKernelGGL((tile_stats_kernel<false, 2, true, 4>), blocks, threads, 0, stream, p);
-  } else if (tile > 96) {
-    if (routed)
-      hipLaunchKernelGGL((tile_stats_kernel<true, 2>), blocks, threads, 0, stream, p);
-    else
-      hipLaunchKernelGGL((tile_stats_kernel<false, 2>), blocks, threads, 0, stream, p);
-  } else if (tile > kHalfKeys) {
-    if (routed)
-      hipLaunchKernelGGL((tile_stats_kernel<true, 2, false, 3>), blocks, dim3(192), 0, stream, p);
-    else
-      hipLaunchKernelGGL((tile_stats_kernel<false, 2, false, 3>), blocks, dim3(192), 0, stream, p);
-  } else {
-    // Two waves even for tiles of at most 32 tokens (one of them then only
-    // stages K): one-wave workgroups, four per CU, leave too few waves to
-    // hide the dense pass's latency.
-    if (routed)
-      hipLaunchKernelGGL((tile_stats_kernel<true, 1, false, 2>), blocks, dim3(128), 0, stream, p);
-    else
-      hipLaunchKernelGGL((tile_stats_kernel<false, 1, false, 2>), blocks, dim3(128), 0, stream, p);
-  }
+  if (dtype == DSA_F16)
+    launch_tile_stats<_Float16>(p, routed, gather, stream);
+  else
+    launch_tile_stats<__bf16>(p, routed, gather, stream);
   return dsa::check_launch("dsa_tile_stats");
 }

@@ -26,13 +26,27 @@ def _require_cuda(name, tensor):
         raise ValueError(f"{name} must be a CUDA (HIP) tensor; libdsa has no CPU path")
 
 
-def _kernel_view(name, tensor):
-    """Return a [B,T,H,D] bf16 view the kernel can read (copying only if needed)."""
+# The 16-bit element types the kernels compute in (dtype codes of dsa.h).
+KERNEL_DTYPES = {torch.bfloat16: _lib.DSA_DTYPE_BF16, torch.float16: _lib.DSA_DTYPE_F16}
+
+
+def dtype_code(dtype):
+    """The libdsa dtype code of a torch dtype; ValueError for any other than
+    bfloat16 and float16 (the kernels have no float32 path)."""
+    if dtype not in KERNEL_DTYPES:
+        raise ValueError(f"libdsa computes in bfloat16 or float16, not {dtype}")
+    return KERNEL_DTYPES[dtype]
+
+
+def _kernel_view(name, tensor, dtype=None):
+    """Return a [B,T,H,D] 16-bit view the kernel can read (copying only if
+    needed); ``dtype``, when given, is the element type every operand must share."""
     _require_cuda(name, tensor)
     if tensor.ndim != 4:
         raise ValueError(f"{name} must have shape [batch, tokens, heads, head_dim]")
-    if tensor.dtype != torch.bfloat16:
-        raise ValueError(f"{name} must be bfloat16, got {tensor.dtype}")
+    dtype_code(tensor.dtype)
+    if dtype is not None and tensor.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} like q, got {tensor.dtype}")
     ok = (
         tensor.stride(3) == 1
         and all(stride % 8 == 0 for stride in tensor.stride()[:3])
@@ -103,14 +117,15 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     block and per key block that the route addresses: 128 for ``flex_reuse``,
     the spatial tile size for the matrix-sparse backend.
 
-    q: [B,Tq,H,128], k/v: [B,Tk,H,128] bf16 on a HIP device, any strides with a
-    contiguous head dim.  Returns O [B,Tq,H,128] bf16 (contiguous unless
-    ``out`` is given) and, with ``return_lse``, the natural-log LSE [B,H,Tq] fp32.
+    q: [B,Tq,H,128], k/v: [B,Tk,H,128], all bf16 or all fp16 (the compute
+    type), on a HIP device, any strides with a contiguous head dim.  Returns O
+    [B,Tq,H,128] in that type (contiguous unless ``out`` is given) and, with
+    ``return_lse``, the natural-log LSE [B,H,Tq] fp32.
     """
     lib = _lib.load()
     q = _kernel_view("q", q)
-    k = _kernel_view("k", k)
-    v = _kernel_view("v", v)
+    k = _kernel_view("k", k, q.dtype)
+    v = _kernel_view("v", v, q.dtype)
     batch, q_tokens, heads, head_dim = q.shape
     if k.shape[0] != batch or v.shape[0] != batch or k.shape[2] != heads or v.shape[2] != heads:
         raise ValueError("q, k and v must agree on batch and heads")
@@ -124,11 +139,10 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     if scale is None:
         scale = head_dim ** -0.5
     if out is None:
-        out = torch.empty((batch, q_tokens, heads, head_dim), dtype=torch.bfloat16,
-                          device=q.device)
+        out = torch.empty((batch, q_tokens, heads, head_dim), dtype=q.dtype, device=q.device)
     else:
         _require_cuda("out", out)
-        if out.shape != (batch, q_tokens, heads, head_dim) or out.dtype != torch.bfloat16:
+        if out.shape != (batch, q_tokens, heads, head_dim) or out.dtype != q.dtype:
             raise ValueError("out has the wrong shape or dtype")
     lse = None
     if return_lse:
@@ -161,7 +175,7 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
                  if workspace_bytes else None)
     with torch.cuda.device(q.device):
         status = lib.dsa_bsa_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), strides,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dtype_code(q.dtype), strides,
             batch, q_tokens, kv_tokens, heads, head_dim, block_size,
             row_ptr.data_ptr() if row_ptr is not None else None,
             col_idx.data_ptr() if col_idx is not None else None,
@@ -192,7 +206,7 @@ def sampled_block_mass(q, k, block_size, samples=2, scale=None):
     if samples <= 0 or samples > block_size:
         raise ValueError("route_samples must be in [1, block_size]")
     q = _kernel_view("q", q)
-    k = _kernel_view("k", k)
+    k = _kernel_view("k", k, q.dtype)
     _, tokens, heads, head_dim = q.shape
     if scale is None:
         scale = head_dim ** -0.5
@@ -201,7 +215,7 @@ def sampled_block_mass(q, k, block_size, samples=2, scale=None):
     strides = _lib.int64_array([q.stride(1), q.stride(2), k.stride(1), k.stride(2)])
     with torch.cuda.device(q.device):
         status = lib.dsa_sampled_mass(
-            q.data_ptr(), k.data_ptr(), strides, tokens, heads, head_dim, block_size,
+            q.data_ptr(), k.data_ptr(), dtype_code(q.dtype), strides, tokens, heads, head_dim, block_size,
             samples, float(scale), mass.data_ptr(), _stream_handle(q.device))
     _lib.check(status, "dsa_sampled_mass")
     return mass
@@ -222,7 +236,7 @@ def block_mass(q, k, lse, block_size=128, scale=None):
     if block_size != 128:
         raise ValueError("The exact mass kernel currently requires block_size=128")
     q = _kernel_view("q", q)
-    k = _kernel_view("k", k)
+    k = _kernel_view("k", k, q.dtype)
     _, tokens, heads, head_dim = q.shape
     _require_cuda("lse", lse)
     if lse.dtype != torch.float32:
@@ -242,7 +256,7 @@ def block_mass(q, k, lse, block_size=128, scale=None):
     strides = _lib.int64_array([q.stride(1), q.stride(2), k.stride(1), k.stride(2)])
     with torch.cuda.device(q.device):
         status = lib.dsa_block_mass(
-            q.data_ptr(), k.data_ptr(), strides, tokens, heads, head_dim, block_size,
+            q.data_ptr(), k.data_ptr(), dtype_code(q.dtype), strides, tokens, heads, head_dim, block_size,
             lse.data_ptr(), lse.stride(0), float(scale), mass.data_ptr(),
             _stream_handle(q.device))
     _lib.check(status, "dsa_block_mass")
@@ -264,7 +278,7 @@ def tile_stats(q, k, lse, tile_shape, csr=None, scale=None, centroids=True):
     if q.shape[0] != 1 or q.shape[1] != k.shape[1]:
         raise ValueError("tile statistics support batch-1 self-attention")
     q = _kernel_view("q", q)
-    k = _kernel_view("k", k)
+    k = _kernel_view("k", k, q.dtype)
     _, tokens, heads, head_dim = q.shape
     tile_h, tile_w = (int(x) for x in tile_shape)
     tile = tile_h * tile_w
@@ -297,7 +311,7 @@ def tile_stats(q, k, lse, tile_shape, csr=None, scale=None, centroids=True):
     strides = _lib.int64_array([q.stride(1), q.stride(2), k.stride(1), k.stride(2)])
     with torch.cuda.device(q.device):
         status = lib.dsa_tile_stats(
-            q.data_ptr(), k.data_ptr(), strides, tokens, heads, head_dim, tile_h, tile_w,
+            q.data_ptr(), k.data_ptr(), dtype_code(q.dtype), strides, tokens, heads, head_dim, tile_h, tile_w,
             lse.data_ptr(), lse.stride(0),
             row_ptr.data_ptr() if row_ptr is not None else None,
             col_idx.data_ptr() if col_idx is not None else None, float(scale),

@@ -32,8 +32,13 @@ int dsa_version(void);
 /* Message of the last failed call on the calling thread ("" if none). */
 const char* dsa_last_error(void);
 
+/* Element types of the attention inputs (the `dtype` arguments). */
+#define DSA_DTYPE_BF16 0
+#define DSA_DTYPE_F16 1
+
 /*
- * Block-sparse attention forward, bf16 in / bf16 out, fp32 online softmax.
+ * Block-sparse attention forward, bf16 or fp16 in and out (dtype), fp32 online
+ * softmax; the matrix products run in the input type with fp32 accumulation.
  * Replaces FlexAttention over a BlockMask (attention_backends/flex.py:379-399
  * `_flex_output`, flex.py:360-376) and, with row_ptr == col_idx == NULL, dense
  * SDPA (attention_backends/dense.py:14-48).
@@ -61,9 +66,9 @@ const char* dsa_last_error(void);
  *                in place; no transposed copy is made.
  * Keys past kv_tokens in a partial last block are masked.
  */
-int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, const int64_t* strides,
-                int32_t batch, int32_t q_tokens, int32_t kv_tokens, int32_t heads,
-                int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
+int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, int32_t dtype,
+                const int64_t* strides, int32_t batch, int32_t q_tokens, int32_t kv_tokens,
+                int32_t heads, int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
                 const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
                 void* workspace, size_t workspace_bytes, hipStream_t stream);
 
@@ -94,27 +99,29 @@ size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_to
  * race; calls ordered on one stream do not.  Nothing in the array needs
  * clearing: a call writes every partial it reads.
  */
-int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
+int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                         const int64_t* strides, int32_t batch, int32_t q_tokens,
                         int32_t kv_tokens, int32_t heads, int32_t head_dim, int32_t block_size,
                         const int32_t* row_ptr, const int32_t* col_idx, int32_t route_batches,
                         float scale, float* lse, hipStream_t stream);
 
 /*
- * Sampled block-mass estimate for one batch-1 self-attention call.
- * Replaces `_sampled_block_mass` (attention_backends/flex.py:205-251):
- * `samples` evenly spaced tokens per block, scores rounded like a bf16 matmul
- * and bf16 scale multiply, fp32 softmax over all sampled keys plus
- * log(block size / samples), mass[h, qb, kb] = mean over query samples of the
- * sum over key samples.  strides[4]: q (t, h), k (t, h) in elements.
- * samples: power of two <= min(32, block_size).  mass: [heads, blocks, blocks].
+ * Sampled block-mass estimate for one batch-1 self-attention call, bf16 or
+ * fp16 Q/K (dtype).  Replaces `_sampled_block_mass`
+ * (attention_backends/flex.py:205-251): `samples` evenly spaced tokens per
+ * block, scores rounded like a matmul and a scale multiply in the input type,
+ * fp32 softmax over all sampled keys plus log(block size / samples),
+ * mass[h, qb, kb] = mean over query samples of the sum over key samples.
+ * strides[4]: q (t, h), k (t, h) in elements.  samples: 1..block_size;
+ * block_size <= 128.  mass: [heads, blocks, blocks], deterministic.
  */
-int dsa_sampled_mass(const void* q, const void* k, const int64_t* strides, int32_t tokens,
-                     int32_t heads, int32_t head_dim, int32_t block_size, int32_t samples,
-                     float scale, float* mass, hipStream_t stream);
+int dsa_sampled_mass(const void* q, const void* k, int32_t dtype, const int64_t* strides,
+                     int32_t tokens, int32_t heads, int32_t head_dim, int32_t block_size,
+                     int32_t samples, float scale, float* mass, hipStream_t stream);
 
 /*
- * Exact block attention mass of one batch-1 self-attention call.
+ * Exact block attention mass of one batch-1 self-attention call, bf16 or fp16
+ * Q/K (dtype).
  * Replaces `_block_attention_mass` and its Triton `_exact_block_mass_kernel`
  * (attention_backends/flex.py:96-202): mass[h, qb, kb] = sum over the valid
  * query tokens t of block qb and key tokens s of block kb of
@@ -124,13 +131,14 @@ int dsa_sampled_mass(const void* q, const void* k, const int64_t* strides, int32
  * elements.  head_dim 128, block_size 128.  mass: [heads, blocks, blocks],
  * every entry written (no initialisation needed); deterministic.
  */
-int dsa_block_mass(const void* q, const void* k, const int64_t* strides, int32_t tokens,
+int dsa_block_mass(const void* q, const void* k, int32_t dtype, const int64_t* strides,
+                   int32_t tokens,
                    int32_t heads, int32_t head_dim, int32_t block_size, const float* lse,
                    int64_t lse_head_stride, float scale, float* mass, hipStream_t stream);
 
 /*
  * Spatial-tile attention statistics of one batch-1 self-attention call over
- * tile-major tokens (tile_h * tile_w <= 128 tokens per tile, tokens a whole
+ * tile-major tokens, bf16 or fp16 Q/K (dtype) (tile_h * tile_w <= 128 tokens per tile, tokens a whole
  * number of tiles, at most 2048 tiles).  Replaces the statistics of the
  * matrix-sparse backend: `_dense_route` (attention_backends/sparse.py:184-233)
  * with row_ptr == col_idx == NULL, `sparse_chunk` (sparse.py:718-750) with the
@@ -142,7 +150,8 @@ int dsa_block_mass(const void* q, const void* k, const int64_t* strides, int32_t
  * centroids moment / max(mass, 1e-12) in fp16 (each optional).  Cells a CSR
  * row does not list are written as zeros; a row must not repeat a tile.
  */
-int dsa_tile_stats(const void* q, const void* k, const int64_t* strides, int32_t tokens,
+int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const int64_t* strides,
+                   int32_t tokens,
                    int32_t heads, int32_t head_dim, int32_t tile_h, int32_t tile_w,
                    const float* lse, int64_t lse_head_stride, const int32_t* row_ptr,
                    const int32_t* col_idx, float scale, float* mass, void* mass_f16,

@@ -42,6 +42,12 @@ def to_bf16(values):
     return rounded.astype(np.uint32).view(np.float32)
 
 
+def to_fp16(values):
+    """Round float32 values to float16 (round-to-nearest-even, overflow to
+    inf), kept as float32."""
+    return np.asarray(values, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
 def sample_indices(tokens, block_size, samples):
     """Token indices sampled per block: [blocks, samples] (flex.py:221-231)."""
     blocks = -(-tokens // block_size)
@@ -54,14 +60,16 @@ def sample_indices(tokens, block_size, samples):
 
 
 def sampled_block_mass(q, k, block_size, samples, scale=None, bf16_scores=True,
-                       query_blocks=None):
+                       query_blocks=None, score_dtype=None):
     """Sampled estimate of per-(head, q-block, k-block) attention mass.
 
     q, k: [1, T, H, D] arrays (values already representable in the input
-    dtype).  With ``bf16_scores`` the scores are rounded to bfloat16 after the
-    dot product and again after the scale multiply, as a bf16 matmul followed
-    by a bf16 multiply does (flex.py:245); the softmax runs on float64 here
-    (float32 in the reference).  Returns mass [H, blocks, blocks] float64, or,
+    dtype).  The scores are rounded to the input dtype after the dot product
+    and again after the scale multiply, as a matmul and a multiply in that
+    dtype do (flex.py:245): ``score_dtype`` "bf16" or "fp16", or None for
+    float32 inputs (no rounding); without ``score_dtype``, ``bf16_scores``
+    selects "bf16" or None.  The softmax runs on float64 here (float32 in the
+    reference).  Returns mass [H, blocks, blocks] float64, or,
     with ``query_blocks`` (a list of query-block ids), only those rows:
     [H, len(query_blocks), blocks].  Every row is a softmax over all sampled
     keys, so a row does not depend on which other rows are evaluated.
@@ -83,9 +91,11 @@ def sampled_block_mass(q, k, block_size, samples, scale=None, bf16_scores=True,
     if scale is None:
         scale = head_dim ** -0.5
     scores = np.einsum("hqd,hkd->hqk", sampled_q, sampled_k)
-    if bf16_scores:
-        scores = to_bf16(scores.astype(np.float32))
-        scores = to_bf16((scores * np.float32(scale)).astype(np.float32)).astype(np.float64)
+    rounding = score_dtype if score_dtype is not None else ("bf16" if bf16_scores else None)
+    if rounding is not None:
+        rounder = {"bf16": to_bf16, "fp16": to_fp16}[rounding]
+        scores = rounder(scores.astype(np.float32))
+        scores = rounder((scores * np.float32(scale)).astype(np.float32)).astype(np.float64)
     else:
         scores = (scores.astype(np.float32) * np.float32(scale)).astype(np.float64)
     logits = scores + log_weights[None, None]

@@ -83,7 +83,13 @@ def sampled_mass_fixture(flex):
         "fp32_partial_s16": (1000, 3, 64, 128, 16, torch.float32),
         "bf16_s16": (1024, 2, 128, 128, 16, torch.bfloat16),
         "bf16_partial_s16": (300, 2, 128, 128, 16, torch.bfloat16),
+        "f16_partial_s16": (1000, 3, 128, 128, 16, torch.float16),
+        "bf16_partial_s12": (1000, 3, 128, 128, 12, torch.bfloat16),
+        "bf16_partial_s48": (1000, 2, 128, 128, 48, torch.bfloat16),
     }
+    codes = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+    # params: tokens, heads, head_dim, block, samples, dtype (0 fp32, 1 bf16,
+    # 2 fp16), seed.
     for index, (name, (tokens, heads, dim, block, samples, dtype)) in enumerate(specs.items()):
         q, k, _ = clustered_qkv(tokens, heads, dim, group=block, seed=100 + index, dtype=dtype)
         mass = flex._sampled_block_mass(q, k, block, samples=samples)
@@ -91,7 +97,7 @@ def sampled_mass_fixture(flex):
                                                 k.double().sum().item()])
         arrays[f"{name}__mass"] = mass.numpy()
         arrays[f"{name}__params"] = np.array(
-            [tokens, heads, dim, block, samples, int(dtype == torch.bfloat16), 100 + index])
+            [tokens, heads, dim, block, samples, codes[dtype], 100 + index])
     _save("sampled_mass", **arrays)
 
 

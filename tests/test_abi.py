@@ -54,28 +54,34 @@ def test_version_and_workspace_size(lib):
 
 def test_invalid_arguments_are_reported_before_any_launch(lib):
     strides = _lib.int64_array([8] * 12)
-    status = lib.dsa_bsa_fwd(None, None, None, None, strides, 1, 128, 128, 1, 128, 128,
+    status = lib.dsa_bsa_fwd(None, None, None, None, 0, strides, 1, 128, 128, 1, 128, 128,
                              None, None, 1, 0.1, None, None, 0, None)
     assert status == _lib.DSA_EINVAL
     assert "null" in _lib.last_error()
     with pytest.raises(ValueError, match="null"):
         _lib.check(status, "dsa_bsa_fwd")
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 64, 128,
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 64, 128,
                              None, None, 1, 0.1, None, fake, 1 << 20, None)
     assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
     misaligned = ctypes.c_void_p(24)
-    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 128, 128,
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
                              None, None, 1, 0.1, None, misaligned, 1 << 20, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
-    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, strides, 1, 128, 128, 1, 128, 128,
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
                              None, None, 1, 0.1, None, None, 1 << 20, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
     status = lib.dsa_route_select(fake, None, 4, 2100, 0.5, 0.95, 1, 0, fake, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "2048" in _lib.last_error()
-    status = lib.dsa_sampled_mass(fake, fake, _lib.int64_array([8] * 4), 1024, 2, 128, 128, 3,
-                                  0.1, fake, None)
-    assert status == _lib.DSA_EUNSUPPORTED and "power of two" in _lib.last_error()
+    status = lib.dsa_sampled_mass(fake, fake, 0, _lib.int64_array([8] * 4), 1024, 2, 128, 128,
+                                  129, 0.1, fake, None)
+    assert status == _lib.DSA_EINVAL and "route_samples" in _lib.last_error()
+    status = lib.dsa_sampled_mass(fake, fake, 2, _lib.int64_array([8] * 4), 1024, 2, 128, 128,
+                                  16, 0.1, fake, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "dtype" in _lib.last_error()
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 7, strides, 1, 128, 128, 1, 128, 128,
+                             None, None, 1, 0.1, None, None, 0, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "dtype" in _lib.last_error()
     status = lib.dsa_permute_rows(4, None, None, None, None, None, 1, 1, 1, 16, None)
     assert status == _lib.DSA_EINVAL
 
@@ -83,12 +89,12 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
 def test_exact_and_routing_entry_points_validate_first(lib):
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     strides = _lib.int64_array([8] * 4)
-    status = lib.dsa_block_mass(fake, fake, strides, 256, 2, 64, 128, fake, 256, 0.1, fake, None)
+    status = lib.dsa_block_mass(fake, fake, 0, strides, 256, 2, 64, 128, fake, 256, 0.1, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
-    status = lib.dsa_block_mass(fake, fake, strides, 256, 2, 128, 128, fake, 100, 0.1, fake,
+    status = lib.dsa_block_mass(fake, fake, 0, strides, 256, 2, 128, 128, fake, 100, 0.1, fake,
                                 None)
     assert status == _lib.DSA_EINVAL and "lse" in _lib.last_error()
-    status = lib.dsa_block_mass(fake, fake, strides, 256, 2, 128, 128, fake, 256, -1.0, fake,
+    status = lib.dsa_block_mass(fake, fake, 0, strides, 256, 2, 128, 128, fake, 256, -1.0, fake,
                                 None)
     assert status == _lib.DSA_EINVAL and "scale" in _lib.last_error()
     status = lib.dsa_frontier_mask(fake, 2, 2100, fake, fake, None, None)
@@ -111,12 +117,12 @@ def test_exact_and_routing_entry_points_validate_first(lib):
 def test_tile_stats_validates_first(lib):
     fake = ctypes.c_void_p(16)
     strides = _lib.int64_array([8] * 4)
-    status = lib.dsa_tile_stats(fake, fake, strides, 1024, 2, 128, 12, 12, fake, 1024, None,
+    status = lib.dsa_tile_stats(fake, fake, 0, strides, 1024, 2, 128, 12, 12, fake, 1024, None,
                                 None, 0.1, fake, None, None, None, None, None, None)
     assert status == _lib.DSA_EUNSUPPORTED and "128" in _lib.last_error()
-    status = lib.dsa_tile_stats(fake, fake, strides, 1000, 2, 128, 8, 8, fake, 1000, None,
+    status = lib.dsa_tile_stats(fake, fake, 0, strides, 1000, 2, 128, 8, 8, fake, 1000, None,
                                 None, 0.1, fake, None, None, None, None, None, None)
     assert status == _lib.DSA_EINVAL and "whole" in _lib.last_error()
-    status = lib.dsa_tile_stats(fake, fake, strides, 1024, 2, 128, 8, 8, fake, 1024, fake,
+    status = lib.dsa_tile_stats(fake, fake, 0, strides, 1024, 2, 128, 8, 8, fake, 1024, fake,
                                 None, 0.1, fake, None, None, None, None, None, None)
     assert status == _lib.DSA_EINVAL

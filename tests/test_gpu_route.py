@@ -26,28 +26,62 @@ def ops():
     return module
 
 
-@pytest.mark.parametrize("case", ["bf16_s16", "bf16_partial_s16"])
+@pytest.mark.parametrize("case", ["bf16_s16", "bf16_partial_s16", "f16_partial_s16",
+                                  "bf16_partial_s12", "bf16_partial_s48"])
 def test_sampled_mass_matches_reference_golden(ops, cuda_device, case):
+    """The reference's own _sampled_block_mass outputs: bf16 and fp16 inputs
+    (scores rounded in the input type), partial last blocks, 16, 12 and 48
+    samples per block."""
+    from tests.test_oracle_route import GOLDEN_DTYPES
     data = _load("sampled_mass")
-    tokens, heads, dim, block, samples, bf16, seed = (int(x) for x in data[f"{case}__params"])
-    q, k, _ = clustered_qkv(tokens, heads, dim, group=block, seed=seed, dtype=torch.bfloat16)
+    tokens, heads, dim, block, samples, code, seed = (int(x) for x in data[f"{case}__params"])
+    dtype, score_dtype = GOLDEN_DTYPES[code]
+    q, k, _ = clustered_qkv(tokens, heads, dim, group=block, seed=seed, dtype=dtype)
     mass = ops.sampled_block_mass(q.to(cuda_device), k.to(cuda_device), block, samples)
     torch.cuda.synchronize()
     got = mass.cpu().numpy()
     np.testing.assert_allclose(got, data[f"{case}__mass"], atol=2e-3, rtol=2e-3)
-    oracle = R.sampled_block_mass(q.float().numpy(), k.float().numpy(), block, samples)
+    oracle = R.sampled_block_mass(q.float().numpy(), k.float().numpy(), block, samples,
+                                  score_dtype=score_dtype)
     np.testing.assert_allclose(got, oracle, atol=2e-3, rtol=2e-3)
     np.testing.assert_allclose(got.sum(-1), 1.0, atol=1e-5)
 
 
-@pytest.mark.parametrize("samples", [1, 2, 4, 8, 16, 32])
-def test_sampled_mass_sample_counts(ops, cuda_device, samples):
+@pytest.mark.parametrize("samples", [1, 2, 3, 4, 5, 8, 12, 16, 24, 32, 33, 48, 64, 100, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sampled_mass_sample_counts(ops, cuda_device, samples, dtype):
+    """Any sample count 1..block (flex.py:219-231 accepts 1..block_size):
+    powers of two up to 32 directly, other counts padded to the next power of
+    two, 64 and 128 with block sums across waves; partial last block."""
     tokens, heads, block = 1000, 3, 128
-    q, k, _ = clustered_qkv(tokens, heads, 128, group=block, seed=samples, dtype=torch.bfloat16)
+    q, k, _ = clustered_qkv(tokens, heads, 128, group=block, seed=samples, dtype=dtype)
     got = ops.sampled_block_mass(q.to(cuda_device), k.to(cuda_device), block, samples)
     torch.cuda.synchronize()
-    oracle = R.sampled_block_mass(q.float().numpy(), k.float().numpy(), block, samples)
+    oracle = R.sampled_block_mass(q.float().numpy(), k.float().numpy(), block, samples,
+                                  score_dtype="bf16" if dtype == torch.bfloat16 else "fp16")
     np.testing.assert_allclose(got.cpu().numpy(), oracle, atol=2e-3, rtol=2e-3)
+    np.testing.assert_allclose(got.sum(-1).cpu().numpy(), 1.0, atol=1e-5)
+    # Deterministic: block sums have a fixed order, without atomics.
+    again = ops.sampled_block_mass(q.to(cuda_device), k.to(cuda_device), block, samples)
+    assert torch.equal(again, got)
+
+
+def test_full_sampling_at_block_128_matches_exact_block_mass(ops, cuda_device):
+    """samples == block == 128 (the reference's identity, test_flex_backend.py:
+    43-53, at the production block size): mass = exact mass / block, up to
+    the bf16 rounding of the scores."""
+    tokens, heads, block = 128 * 6, 2, 128
+    generator = torch.Generator().manual_seed(6)
+    q = torch.randn(1, tokens, heads, 128, generator=generator).to(torch.bfloat16)
+    k = torch.randn(1, tokens, heads, 128, generator=generator).to(torch.bfloat16)
+    got = ops.sampled_block_mass(q.to(cuda_device), k.to(cuda_device), block, block)
+    torch.cuda.synchronize()
+    scores = np.einsum("bqhd,bkhd->bhqk", q.double().numpy(), k.double().numpy()) / math.sqrt(128)
+    probabilities = np.exp(scores - scores.max(-1, keepdims=True))
+    probabilities /= probabilities.sum(-1, keepdims=True)
+    blocks = tokens // block
+    exact = probabilities[0].reshape(heads, blocks, block, blocks, block).sum((2, 4))
+    np.testing.assert_allclose(got.cpu().numpy(), exact / block, atol=3e-3, rtol=3e-2)
 
 
 def test_full_sampling_matches_exact_block_mass(ops, cuda_device):

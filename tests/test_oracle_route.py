@@ -16,6 +16,9 @@ from tests.golden.inputs import block_mass_like, clustered_qkv, random_route
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 MARGIN_ULP = 4.0
+# dtype code of the sampled_mass fixture -> (input dtype, score rounding).
+GOLDEN_DTYPES = {0: (torch.float32, None), 1: (torch.bfloat16, "bf16"),
+                 2: (torch.float16, "fp16")}
 
 
 def _load(name):
@@ -155,15 +158,15 @@ def test_prior_is_exact_closed_form_on_dyadic_rows():
 @pytest.mark.parametrize("case", _cases(_load("sampled_mass")))
 def test_sampled_mass_matches_reference_golden(case):
     data = _load("sampled_mass")
-    tokens, heads, dim, block, samples, bf16, seed = (int(x) for x in data[f"{case}__params"])
-    dtype = torch.bfloat16 if bf16 else torch.float32
+    tokens, heads, dim, block, samples, code, seed = (int(x) for x in data[f"{case}__params"])
+    dtype, score_dtype = GOLDEN_DTYPES[code]
     q, k, _ = clustered_qkv(tokens, heads, dim, group=block, seed=seed, dtype=dtype)
     np.testing.assert_allclose(
         [q.double().sum().item(), k.double().sum().item()], data[f"{case}__checksum"])
     mass = R.sampled_block_mass(q.float().numpy(), k.float().numpy(), block, samples,
-                                bf16_scores=bool(bf16))
+                                score_dtype=score_dtype, bf16_scores=False)
     expected = data[f"{case}__mass"]
-    tolerance = 2e-3 if bf16 else 2e-6
+    tolerance = 2e-3 if score_dtype else 2e-6
     np.testing.assert_allclose(mass, expected, atol=tolerance, rtol=tolerance)
     np.testing.assert_allclose(mass.sum(-1), 1.0, atol=1e-9)
 
@@ -173,7 +176,7 @@ def test_sampled_mass_query_block_subset_equals_full_rows():
     the selected rows of the full computation, in the order asked for, and
     still matches the reference golden on them."""
     data = _load("sampled_mass")
-    tokens, heads, dim, block, samples, bf16, seed = (
+    tokens, heads, dim, block, samples, _, seed = (
         int(x) for x in data["bf16_partial_s16__params"])
     q, k, _ = clustered_qkv(tokens, heads, dim, group=block, seed=seed, dtype=torch.bfloat16)
     qn, kn = q.float().numpy(), k.float().numpy()
