@@ -76,30 +76,33 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
   return DSA_OK;
 }
 
-// Launches the attention of a prepared call.  `part` holds room for
-// `part_groups` split partials (0: the call runs unsplit).
-int launch(int32_t dtype, BsaParams p, float* part, int64_t part_groups, hipStream_t stream,
+// Launches the attention of a prepared call on `scratch_bytes` of scratch
+// (launch order, then split partials; see launch_typed).
+int launch(int32_t dtype, BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
            const char* who) {
-  return dtype == DSA_F16 ? bsa_launch_f16(p, part, part_groups, stream, who)
-                          : launch_typed<__bf16>(p, part, part_groups, stream, who);
+  return dtype == DSA_F16 ? bsa_launch_f16(p, scratch, scratch_bytes, stream, who)
+                          : launch_typed<__bf16>(p, scratch, scratch_bytes, stream, who);
 }
 
 }  // namespace
 
-// Split partials of dsa_bsa_fwd_noalloc: room for kMaxPartGroups partials
-// (68,157,440 bytes).  Every device the library runs on holds its own copy
-// until the process ends; host code reaches it only through the address
-// hipGetSymbolAddress returns on that device (scratch_on).
-static __device__ __align__(256) float scratch[kMaxPartGroups * kPartFloats];
+// Scratch of dsa_bsa_fwd_noalloc: the launch order of up to kMaxOrderItems
+// work items (1 MiB), then kMaxPartGroups split partials (68,157,440 bytes).
+// Every device the library runs on holds its own copy until the process
+// ends; host code reaches it only through the address hipGetSymbolAddress
+// returns on that device (scratch_on).
+constexpr size_t kScratchBytes = (size_t)kMaxOrderItems * sizeof(int32_t) +
+                                 (size_t)kMaxPartGroups * kPartBytes;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {
 
 std::mutex g_scratch_lock;
-float* g_scratch[kMaxDevices] = {};
+void* g_scratch[kMaxDevices] = {};
 
 // Device address of `device`'s scratch array, resolved once per device with
 // that device current.
-int scratch_on(int device, float** out, const char* who) {
+int scratch_on(int device, void** out, const char* who) {
   std::lock_guard<std::mutex> guard(g_scratch_lock);
   if (g_scratch[device] == nullptr) {
     int current = -1;
@@ -113,7 +116,7 @@ int scratch_on(int device, float** out, const char* who) {
     if (err != hipSuccess || address == nullptr)
       return dsa::set_error(DSA_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s",
                             who, device, hipGetErrorString(err));
-    g_scratch[device] = static_cast<float*>(address);
+    g_scratch[device] = address;
   }
   *out = g_scratch[device];
   return DSA_OK;
@@ -127,7 +130,10 @@ extern "C" size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads,
   if (batch <= 0 || heads <= 0 || kv_tokens <= 0 || head_dim <= 0) return 0;
   if (block_size <= 0 || block_size > 128) return 0;
   const int32_t kv_blocks = (kv_tokens + block_size - 1) / block_size;
-  return max_parts_for(kv_blocks) >= 2 ? (size_t)kMaxPartGroups * kPartBytes : 0;
+  // Routed calls are self-attention (q_tokens == kv_tokens): batch x heads x
+  // kv_blocks work items to order.
+  const size_t order = order_bytes((int64_t)batch * heads * kv_blocks, kv_blocks);
+  return order + (max_parts_for(kv_blocks) >= 2 ? (size_t)kMaxPartGroups * kPartBytes : 0);
 }
 
 extern "C" size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
@@ -150,8 +156,7 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
   if (status != DSA_OK) return status;
   if (workspace_bytes > 0 && (!workspace || !aligned16(workspace)))
     return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: workspace must be 16-byte aligned");
-  return launch(dtype, p, static_cast<float*>(workspace), (int64_t)(workspace_bytes / kPartBytes),
-                stream, "dsa_bsa_fwd");
+  return launch(dtype, p, workspace, workspace ? workspace_bytes : 0, stream, "dsa_bsa_fwd");
 }
 
 extern "C" int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
@@ -169,10 +174,11 @@ extern "C" int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, 
   const int device = stream_device(stream);
   if (device < 0)
     return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd_noalloc: cannot tell the stream's device");
-  float* part = nullptr;
-  const int found = scratch_on(device, &part, "dsa_bsa_fwd_noalloc");
+  void* area = nullptr;
+  const int found = scratch_on(device, &area, "dsa_bsa_fwd_noalloc");
   if (found != DSA_OK) return found;
-  // The split never takes more than the array holds, so no call size needs
-  // more scratch than kMaxPartGroups partials.
-  return launch(dtype, p, part, kMaxPartGroups, stream, "dsa_bsa_fwd_noalloc");
+  // Calls of more work items than the order region holds run in launch
+  // order, as dsa_bsa_fwd does; the split never takes more partials than the
+  // array holds.  So no call size needs more scratch than this.
+  return launch(dtype, p, area, kScratchBytes, stream, "dsa_bsa_fwd_noalloc");
 }

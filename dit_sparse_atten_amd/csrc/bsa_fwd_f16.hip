@@ -4,7 +4,7 @@
 // parallel.
 #include "bsa_kernel.h"
 
-int bsa_launch_f16(bsa::BsaParams p, float* part, int64_t part_groups, hipStream_t stream,
+int bsa_launch_f16(bsa::BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
                    const char* who) {
-  return bsa::launch_typed<_Float16>(p, part, part_groups, stream, who);
+  return bsa::launch_typed<_Float16>(p, scratch, scratch_bytes, stream, who);
 }

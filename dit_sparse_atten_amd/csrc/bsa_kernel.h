@@ -59,6 +59,7 @@ struct BsaParams {
   int64_t o_sb, o_st, o_sh;
   const int32_t* row_ptr;  // null: every key block (dense)
   const int32_t* col_idx;
+  const int32_t* order;    // routed: work item of each launch slot (null: identity)
   int32_t batch, heads, q_tokens, kv_tokens, q_blocks, kv_blocks, route_batches;
   int32_t block;     // tokens per query block and per key block (1..128)
   int32_t block_pad; // gathered stream: key slots per block (block rounded up to 8)
@@ -135,22 +136,24 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   const int qi = lane & 31;
 
   // Dense: each XCD takes a contiguous range of (b, h) rows, whose workgroups
-  // stream the same keys in lock step through that XCD's L2.  Routed: blocks
-  // stay in launch order, which the hardware deals round-robin over the XCDs,
-  // so every XCD gets an eighth of every head; routes whose keep differs from
-  // head to head (spatially local attention keeps from 0.2 to 0.65 per head)
-  // would otherwise leave the XCDs holding the dense heads working alone
-  // (5.7% of an end-to-end sparse step; 0.6% the other way on i.i.d. routes).
+  // stream the same keys in lock step through that XCD's L2.  Routed: slots
+  // are dealt round-robin over the XCDs, so every XCD gets an eighth of every
+  // head (routes whose keep differs from head to head, 0.2 to 0.65 per head
+  // under spatially local attention, would otherwise leave the XCDs holding
+  // the dense heads working alone), and `order` (launch_order_kernel) puts
+  // each head's rows longest first, so the workgroups resident side by side
+  // run rows of similar length and stay in step through the L2.
   const int wg = (int)blockIdx.x;
   const bool split = wg >= p.split_from;
-  int work, part = 0;
+  int slot = wg, part = 0;
   if (split) {
     const int t = wg - p.split_from;
-    work = p.split_from + t / p.parts;
+    slot = p.split_from + t / p.parts;
     part = t % p.parts;
-  } else {
-    work = kRouted ? wg : dsa::xcd_remap(wg, p.split_from);
   }
+  int work = slot;
+  if (kRouted && p.order) work = ((dsa_const_i32)p.order)[slot];
+  else if (!kRouted && !split) work = dsa::xcd_remap(wg, p.split_from);
   const int qb = work % p.q_blocks;
   const int bh = work / p.q_blocks;
   const int h = bh % p.heads;
@@ -512,13 +515,66 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   }
 }
 
+// Launch order of a routed call: within each (batch, head) group its query
+// blocks by key-block count descending, ties by index ascending (a stable
+// sort), so the workgroups that run side by side walk rows of similar length
+// and stay in step through the L2 (a same-box A/B at config 2: 40.54 against
+// 41.50 ms).  One workgroup per group: a bitonic sort of (count + 1) << 32 |
+// ~index keys in LDS, padding keys 0 last.
+constexpr int kMaxOrderBlocks = 8192;     // query blocks per (batch, head) group
+constexpr int64_t kMaxOrderItems = 262144;  // work items per call (1 MiB of order)
+
+// Internal linkage: each translation unit that launches it has its own copy.
+static __global__ void __launch_bounds__(256) launch_order_kernel(const int32_t* row_ptr,
+                                                           int32_t* order, int32_t heads,
+                                                           int32_t q_blocks,
+                                                           int32_t route_batches, int32_t n) {
+  __shared__ uint64_t keys[kMaxOrderBlocks];
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.x;
+  const int rb = route_batches == 1 ? 0 : bh / heads;
+  const int32_t* rp = row_ptr + ((int64_t)rb * heads + bh % heads) * q_blocks;
+  for (int i = tid; i < n; i += 256) {
+    uint64_t key = 0;
+    if (i < q_blocks)
+      key = ((uint64_t)(uint32_t)(rp[i + 1] - rp[i] + 1) << 32) | (uint32_t)~(uint32_t)i;
+    keys[i] = key;
+  }
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      dsa::lds_barrier();
+      for (int i = tid; i < n / 2; i += 256) {
+        const int lo = 2 * stride * (i / stride) + (i % stride);
+        const int hi = lo + stride;
+        const bool descending = (lo & size) == 0;
+        const uint64_t a = keys[lo], b = keys[hi];
+        if ((a < b) == descending) {
+          keys[lo] = b;
+          keys[hi] = a;
+        }
+      }
+    }
+  }
+  dsa::lds_barrier();
+  const int32_t base = bh * q_blocks;
+  for (int i = tid; i < q_blocks; i += 256)
+    order[base + i] = base + (int32_t)~(uint32_t)keys[i];
+}
+
+// Bytes of the launch order of a routed call of `items` work items (0 when
+// the call is not ordered), rounded up to 256.
+inline size_t order_bytes(int64_t items, int32_t q_blocks) {
+  if (items > kMaxOrderItems || q_blocks > kMaxOrderBlocks) return 0;
+  return ((size_t)items * sizeof(int32_t) + 255) & ~(size_t)255;
+}
+
 // Combines the `parts` partials of each split query block: with M the largest
 // row max, O = sum_i O_i 2^(m_i - M) / sum_i l_i 2^(m_i - M) and
 // LSE = M ln 2 + ln(sum_i l_i 2^(m_i - M)).  Two threads per row, 64 dims each.
 template <typename T>
 __global__ void __launch_bounds__(256) bsa_merge_kernel(BsaParams p) {
   const int item = blockIdx.x;
-  const int work = p.split_from + item;
+  const int work = p.order ? p.order[p.split_from + item] : p.split_from + item;
   const int qb = work % p.q_blocks;
   const int bh = work / p.q_blocks;
   const int h = bh % p.heads;
@@ -646,12 +702,29 @@ inline bool use_gather(int32_t block, int32_t kv_tokens, int64_t k_token_stride,
   return ((int64_t)kv_tokens + 8) * stride * 2 + kRowBytes <= 0x7fffffff;
 }
 
-// Validates the arguments of an attention call and fills `p` (without the
-// split fields).  Returns DSA_OK or the error status.
+// Launches a prepared call.  `scratch` (null when `scratch_bytes` is 0)
+// holds, for a routed call, the launch order first (order_bytes, when there
+// is room for it), then the split partials of the last round.
 template <typename T>
-int launch_typed(BsaParams p, float* part, int64_t part_groups, hipStream_t stream,
+int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
                  const char* who) {
   const int64_t grid = (int64_t)p.batch * p.heads * p.q_blocks;
+  size_t used = 0;
+  p.order = nullptr;
+  if (p.row_ptr) {
+    const size_t need = order_bytes(grid, p.q_blocks);
+    if (need > 0 && scratch_bytes >= need) {
+      int32_t* order = static_cast<int32_t*>(scratch);
+      p.order = order;
+      used = need;
+      int n = 2;
+      while (n < p.q_blocks) n <<= 1;
+      hipLaunchKernelGGL(launch_order_kernel, dim3((unsigned)(p.batch * p.heads)), dim3(256), 0,
+                         stream, p.row_ptr, order, p.heads, p.q_blocks, p.route_batches, n);
+    }
+  }
+  float* part = reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + used);
+  const int64_t part_groups = (int64_t)((scratch_bytes - used) / kPartBytes);
   int parts = 1;
   const int split = choose_split(grid, device_slots(stream), max_parts_for(p.kv_blocks),
                                  std::min<int64_t>(part_groups, kMaxPartGroups), &parts);
@@ -684,5 +757,5 @@ int launch_typed(BsaParams p, float* part, int64_t part_groups, hipStream_t stre
 }  // namespace bsa
 
 // fp16 instances (bsa_fwd_f16.hip).
-int bsa_launch_f16(bsa::BsaParams p, float* part, int64_t part_groups, hipStream_t stream,
+int bsa_launch_f16(bsa::BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
                    const char* who);

@@ -243,7 +243,8 @@ def test_gathered_key_stream_at_720p_tile_shape(cuda_device):
 def test_split_last_round_matches_unsplit(cuda_device, monkeypatch, routed):
     """With room for the split partials the last round of query blocks runs
     as key ranges merged by a second launch (here 128 blocks of 64-block rows:
-    all of them, in 4 parts); without a workspace the call runs unsplit.  Both
+    all of them, in 4 parts), routed rows in longest-first launch order;
+    without a workspace the call runs unsplit in plain launch order.  Both
     match the closed form, and each other closely."""
     from dit_sparse_atten_amd import _lib
     from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
