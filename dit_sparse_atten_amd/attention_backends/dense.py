@@ -39,8 +39,6 @@ class DenseBackend:
         del q_lens, k_lens, deterministic, version
         if window_size != (-1, -1):
             raise NotImplementedError("The dense backend only supports global attention")
-        if causal:
-            raise NotImplementedError("The dense backend does not implement causal attention")
         if dropout_p:
             raise NotImplementedError("The dense backend does not implement attention dropout")
         ops.dtype_code(dtype)  # bfloat16 or float16, else ValueError
@@ -50,7 +48,7 @@ class DenseBackend:
         v = v.to(dtype)
         if q_scale is not None:
             q = q * q_scale
-        output = ops.bsa_fwd(q, k, v, scale=softmax_scale)
+        output = ops.bsa_fwd(q, k, v, scale=softmax_scale, causal=causal)
         return output.to(output_dtype)
 
 

@@ -33,6 +33,7 @@ struct BlockMassParams {
   float* mass;       // [heads, blocks, blocks]
   int64_t q_st, q_sh, k_st, k_sh, lse_sh;
   int32_t tokens, heads, blocks;
+  int32_t head_dim;  // 8..128, a multiple of 8
   float scale_log2;  // scale * log2(e)
 };
 
@@ -61,15 +62,13 @@ __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
   const int tq_c = row_ok ? tq : p.tokens - 1;
   const T* qrow = static_cast<const T*>(p.q) + h * p.q_sh + (int64_t)tq_c * p.q_st;
   typename E::x8 qf[8];
-#pragma unroll
-  for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const typename E::x8*>(qrow + dc * 16 + g * 8);
+  dsa::load_q_fragments(qrow, g, p.head_dim, qf);
   // Rows past the sequence end get lse = +inf, so every p of theirs is 0.
   const float lse2 = row_ok ? p.lse[h * p.lse_sh + tq] * kLog2e : INFINITY;
 
   const T* kbase = static_cast<const T*>(p.k) + h * p.k_sh;
-  int koff[4];
-  dsa::k_tile_offsets(wave, lane, p.k_st, koff);
+  uint32_t koff[4];
+  dsa::k_tile_offsets(wave, lane, p.k_st, p.head_dim, koff);
   auto issue = [&](int key0, unsigned char* dst) __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rsrc = dsa::k_tile_rsrc(kbase, p.k_st, key0, p.tokens);
 #pragma unroll
@@ -151,8 +150,9 @@ extern "C" int dsa_block_mass(const void* q, const void* k, int32_t dtype, const
                           dtype);
   if (tokens <= 0 || heads <= 0)
     return dsa::set_error(DSA_EINVAL, "dsa_block_mass: tokens and heads must be positive");
-  if (head_dim != dsa::kHeadDim)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_block_mass: head_dim %d unsupported (128 only)",
+  if (head_dim <= 0 || head_dim > dsa::kHeadDim || head_dim % 8 != 0)
+    return dsa::set_error(DSA_EUNSUPPORTED,
+                          "dsa_block_mass: head_dim %d unsupported (a multiple of 8 up to 128)",
                           head_dim);
   if (block_size != 128)
     return dsa::set_error(DSA_EUNSUPPORTED,
@@ -189,6 +189,7 @@ extern "C" int dsa_block_mass(const void* q, const void* k, int32_t dtype, const
   p.tokens = tokens;
   p.heads = heads;
   p.blocks = blocks;
+  p.head_dim = head_dim;
   p.scale_log2 = scale * kLog2e;
   if (dtype == DSA_F16)
     hipLaunchKernelGGL(block_mass_kernel<_Float16>, dim3((unsigned)grid), dim3(256), 0, stream, p);

@@ -18,17 +18,21 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
             const int64_t* strides,
             int32_t batch, int32_t q_tokens, int32_t kv_tokens, int32_t heads,
             int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
-            const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
-            const char* who, BsaParams* p) {
+            const int32_t* col_idx, int32_t route_batches, float scale, int32_t causal,
+            float* lse, const char* who, BsaParams* p) {
   if (!q || !k || !v || !o || !strides)
     return dsa::set_error(DSA_EINVAL, "%s: null tensor or stride pointer", who);
   if (dtype != DSA_BF16 && dtype != DSA_F16)
     return dsa::set_error(DSA_EUNSUPPORTED, "%s: dtype %d unsupported (bf16 or fp16)", who, dtype);
   if (batch <= 0 || heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
     return dsa::set_error(DSA_EINVAL, "%s: batch/heads/tokens must be positive", who);
-  if (head_dim != kHeadDim)
-    return dsa::set_error(DSA_EUNSUPPORTED, "%s: head_dim %d unsupported (128 only)", who,
-                          head_dim);
+  if (head_dim <= 0 || head_dim > kHeadDim || head_dim % 8 != 0)
+    return dsa::set_error(DSA_EUNSUPPORTED,
+                          "%s: head_dim %d unsupported (a multiple of 8 up to 128)", who, head_dim);
+  if (causal != 0 && causal != 1)
+    return dsa::set_error(DSA_EINVAL, "%s: causal must be 0 or 1", who);
+  if (causal && row_ptr)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: causal attention takes no block route", who);
   if (block_size <= 0 || block_size > 128)
     return dsa::set_error(DSA_EUNSUPPORTED, "%s: block_size %d unsupported (1..128)", who,
                           block_size);
@@ -71,6 +75,8 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
   p->route_batches = row_ptr ? route_batches : 1;
   p->block = block_size;
   p->block_pad = (block_size + 7) & ~7;
+  p->head_dim = head_dim;
+  p->causal = causal;
   p->scale = scale;
   p->scale_log2 = scale * 1.4426950408889634f;
   return DSA_OK;
@@ -146,12 +152,12 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
                            int32_t kv_tokens, int32_t heads, int32_t head_dim,
                            int32_t block_size, const int32_t* row_ptr,
                            const int32_t* col_idx, int32_t route_batches, float scale,
-                           float* lse, void* workspace, size_t workspace_bytes,
+                           int32_t causal, float* lse, void* workspace, size_t workspace_bytes,
                            hipStream_t stream) {
   dsa::clear_error();
   BsaParams p;
   const int status = prepare(q, k, v, o, dtype, strides, batch, q_tokens, kv_tokens, heads, head_dim,
-                             block_size, row_ptr, col_idx, route_batches, scale, lse,
+                             block_size, row_ptr, col_idx, route_batches, scale, causal, lse,
                              "dsa_bsa_fwd", &p);
   if (status != DSA_OK) return status;
   if (workspace_bytes > 0 && (!workspace || !aligned16(workspace)))
@@ -164,11 +170,11 @@ extern "C" int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, 
                                    int32_t kv_tokens, int32_t heads, int32_t head_dim,
                                    int32_t block_size, const int32_t* row_ptr,
                                    const int32_t* col_idx, int32_t route_batches, float scale,
-                                   float* lse, hipStream_t stream) {
+                                   int32_t causal, float* lse, hipStream_t stream) {
   dsa::clear_error();
   BsaParams p;
   const int status = prepare(q, k, v, o, dtype, strides, batch, q_tokens, kv_tokens, heads, head_dim,
-                             block_size, row_ptr, col_idx, route_batches, scale, lse,
+                             block_size, row_ptr, col_idx, route_batches, scale, causal, lse,
                              "dsa_bsa_fwd_noalloc", &p);
   if (status != DSA_OK) return status;
   const int device = stream_device(stream);

@@ -62,6 +62,8 @@ struct BsaParams {
   const int32_t* order;    // routed: work item of each launch slot (null: identity)
   int32_t batch, heads, q_tokens, kv_tokens, q_blocks, kv_blocks, route_batches;
   int32_t block;     // tokens per query block and per key block (1..128)
+  int32_t head_dim;  // 8..128, a multiple of 8; dims past it are zero in the stages
+  int32_t causal;    // dense only: query t attends keys k <= t
   int32_t block_pad; // gathered stream: key slots per block (block rounded up to 8)
   float scale;       // softmax scale applied to <q, k>
   float scale_log2;  // scale * log2(e)
@@ -160,6 +162,11 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   const int b = bh / p.heads;
 
   int start = 0, end = p.kv_blocks;
+  if (!kRouted && p.causal) {
+    // Keys up to the block's last query row (query t sees keys k <= t).
+    const int last_row = min(qb * p.block + p.block, p.q_tokens) - 1;
+    end = min(p.kv_blocks, last_row / p.block + 1);
+  }
   if (kRouted) {
     const dsa_const_i32 rp = (dsa_const_i32)p.row_ptr;
     const int rb = p.route_batches == 1 ? 0 : b;
@@ -185,23 +192,23 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   const int tq_c = tq < p.q_tokens ? tq : p.q_tokens - 1;
   const T* qrow = static_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh + (int64_t)tq_c * p.q_st;
   x8 qf[8];
-#pragma unroll
-  for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const x8*>(qrow + dc * 16 + g * 8);
+  dsa::load_q_fragments(qrow, g, p.head_dim, qf);
 
   const T* kbase = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh;
   const T* vbase = static_cast<const T*>(p.v) + b * p.v_sb + h * p.v_sh;
   // Each wave stages kSlices of the 16 1-KB slices of a K or V stage.
   static_assert(kWaves == 4 || (kWaves == 2 && !kGather), "2-wave groups: plain stream only");
   constexpr int kSlices = 16 / kWaves;
-  // Per-lane source offsets (elements) relative to the half-tile's first key.
-  int koff[kSlices], voff[kSlices];
+  // Per-lane source byte offsets relative to the half-tile's first key (a
+  // chunk of dims at or past head_dim loads zeros, dsa::dead_bits).
+  uint32_t koff[kSlices], voff[kSlices];
 #pragma unroll
   for (int j = 0; j < kSlices; ++j) {
     const int idx = (wave * kSlices + j) * 64 + lane;
     const int row = idx >> 4;
-    koff[j] = row * (int)p.k_st + k2_swz(row, idx & 15) * 8;
-    voff[j] = row * (int)p.v_st + v_swz(row, idx & 15) * 8;
+    const int kc = k2_swz(row, idx & 15), vc = v_swz(row, idx & 15);
+    koff[j] = (uint32_t)((row * (int)p.k_st + kc * 8) * 2) | dsa::dead_bits(kc, p.head_dim);
+    voff[j] = (uint32_t)((row * (int)p.v_st + vc * 8) * 2) | dsa::dead_bits(vc, p.head_dim);
   }
 
   // V^T fragment reads: lane (g, i = lane % 32) of the PV product needs dims
@@ -235,10 +242,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     const __amdgpu_buffer_rsrc_t v_rsrc = k_tile_rsrc(vbase, p.v_st, key0, p.kv_tokens);
 #pragma unroll
     for (int j = 0; j < kSlices; ++j)
-      lds_load16(k_rsrc, kdst + (wave * kSlices + j) * 1024, koff[j] * 2, 0);
+      lds_load16(k_rsrc, kdst + (wave * kSlices + j) * 1024, koff[j], 0);
 #pragma unroll
     for (int j = 0; j < kSlices; ++j)
-      lds_load16(v_rsrc, vdst + (wave * kSlices + j) * 1024, voff[j] * 2, 0);
+      lds_load16(v_rsrc, vdst + (wave * kSlices + j) * 1024, voff[j], 0);
   };
   // Stages the 64-key chunk that starts `o0` slots into stream block kb0 and
   // runs on into kb1 (the blocks are in range; pad and tail slots load
@@ -256,10 +263,13 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       const bool first = o < p.block_pad;
       const uint32_t token =
           (uint32_t)((first ? kb0 : kb1) * p.block + (first ? o : o - p.block_pad));
+      const int kc = k2_swz(row, lane & 15), vc = v_swz(row, lane & 15);
       lds_load16(k_all_rsrc, kdst + (wave * 4 + j) * 1024,
-                 token * (uint32_t)(p.k_st * 2) + (uint32_t)(k2_swz(row, lane & 15) * 16), 0);
+                 (token * (uint32_t)(p.k_st * 2) + (uint32_t)(kc * 16)) |
+                     dsa::dead_bits(kc, p.head_dim), 0);
       lds_load16(v_all_rsrc, vdst + (wave * 4 + j) * 1024,
-                 token * (uint32_t)(p.v_st * 2) + (uint32_t)(v_swz(row, lane & 15) * 16), 0);
+                 (token * (uint32_t)(p.v_st * 2) + (uint32_t)(vc * 16)) |
+                     dsa::dead_bits(vc, p.head_dim), 0);
     }
   };
   // Valid keys of half-tile `half` of block kb (0 for an invalid block).
@@ -284,8 +294,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // Gathered stream: `invalid` has bit p set when stream position p of the
   // chunk is a pad slot, past the row's last key or in an out-of-range block;
   // accumulator r of lane half g holds position 32 kt + 8 (r >> 2) + 4 g + (r & 3).
+  // lim: causal bound of this lane's row, keys at or past `lim` in the
+  // half-tile are masked (at least 64 when nothing is).
   auto compute = [&](const unsigned char* kt_lds, const unsigned char* v_lds, int valid,
-                     uint64_t invalid, auto nkt_c) __attribute__((always_inline)) {
+                     int lim, uint64_t invalid, auto nkt_c) __attribute__((always_inline)) {
     constexpr int NKT = decltype(nkt_c)::value;
     dsa_f32x16 sacc[NKT];
 #pragma unroll
@@ -313,12 +325,13 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
             if (bits & (1u << (8 * (r >> 2) + (r & 3)))) sacc[kt][r] = -INFINITY;
         }
       }
-    } else if (valid < NKT * 32) {
+    } else if (valid < NKT * 32 || lim < NKT * 32) {
+      const int bound = min(valid, lim);
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= valid) sacc[kt][r] = -INFINITY;
+          if (kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= bound) sacc[kt][r] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -383,10 +396,12 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     if (next_kb != -2) issue(next_kb, next_half, kn, vn);
     if (wave_active) {
       const int valid = valid_of(kb, half);
+      // Causal (dense): keys past this lane's query row are masked.
+      const int lim = !kRouted && p.causal ? tq - (kb * p.block + half * kHalfKeys) + 1 : kHalfKeys;
       if (decltype(skip_c)::value && valid <= 32)
-        compute(kc, vc, valid, 0ull, std::integral_constant<int, 1>{});
+        compute(kc, vc, valid, lim, 0ull, std::integral_constant<int, 1>{});
       else
-        compute(kc, vc, valid, 0ull, std::integral_constant<int, 2>{});
+        compute(kc, vc, valid, lim, 0ull, std::integral_constant<int, 2>{});
     }
   };
   // Gathered stream step: chunk at slot o0 of stream block j0 (whose block
@@ -413,9 +428,9 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       if (kb0 < 0) invalid |= second >= 64 ? ~0ull : (1ull << second) - 1;
       if (kb1 < 0 && second < 64) invalid |= ~0ull << second;
       if (left <= 32)
-        compute(kc, vc, 0, invalid, std::integral_constant<int, 1>{});
+        compute(kc, vc, 0, kHalfKeys, invalid, std::integral_constant<int, 1>{});
       else
-        compute(kc, vc, 0, invalid, std::integral_constant<int, 2>{});
+        compute(kc, vc, 0, kHalfKeys, invalid, std::integral_constant<int, 2>{});
     }
   };
   const std::bool_constant<false> no_skip;
@@ -506,7 +521,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         const typename E::x2 blo = __builtin_convertvector(lo, typename E::x2);
         const typename E::x2 bhi = __builtin_convertvector(hi, typename E::x2);
         const typename E::x4 v4 = {blo[0], blo[1], bhi[0], bhi[1]};
-        *reinterpret_cast<typename E::x4*>(orow + dt * 32 + rr * 8 + g * 4) = v4;
+        if (dt * 32 + rr * 8 + g * 4 < p.head_dim)
+          *reinterpret_cast<typename E::x4*>(orow + dt * 32 + rr * 8 + g * 4) = v4;
       }
     if (p.lse && g == 0) {
       p.lse[((int64_t)b * p.heads + h) * p.q_tokens + tq] =
@@ -599,6 +615,7 @@ __global__ void __launch_bounds__(256) bsa_merge_kernel(BsaParams p) {
   const float inv = l > 0.f ? 1.f / l : 0.f;
   T* orow = static_cast<T*>(p.o) + b * p.o_sb + h * p.o_sh + (int64_t)tq * p.o_st;
   for (int c = half * 8; c < half * 8 + 8; ++c) {  // 8-dim chunks of this thread's 64
+    if (c * 8 >= p.head_dim) break;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {

@@ -46,15 +46,41 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t k_tile_rsrc(const void* kbase,
   return make_rsrc(static_cast<const unsigned char*>(kbase) + (int64_t)key0 * k_st * 2, bytes);
 }
 
+// A chunk of 8 dims at or past head_dim stages from this offset: past every
+// buffer's range (the hosts keep K and V within 2^31 bytes), so it reads as
+// zeros and a head_dim below 128 runs as 128 with zero dims.
+constexpr uint32_t kDeadChunk = 0x80000000u;
+
+__device__ __forceinline__ uint32_t dead_bits(int chunk, int head_dim) {
+  return chunk * 8 < head_dim ? 0u : kDeadChunk;
+}
+
 // Per-lane byte offsets of one 256-thread workgroup's share of a K half-tile:
 // thread (wave, lane) loads 16-byte chunks j = 0..3 of the [64][128] tile in
 // the k2_swz layout.  `k_st` is the token stride in elements.
-__device__ __forceinline__ void k_tile_offsets(int wave, int lane, int64_t k_st, int koff[4]) {
+__device__ __forceinline__ void k_tile_offsets(int wave, int lane, int64_t k_st, int head_dim,
+                                               uint32_t koff[4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = (wave * 4 + j) * 64 + lane;
     const int row = idx >> 4;
-    koff[j] = (row * (int)k_st + k2_swz(row, idx & 15) * 8) * 2;
+    const int c = k2_swz(row, idx & 15);
+    koff[j] = (uint32_t)((row * (int)k_st + c * 8) * 2) | dead_bits(c, head_dim);
+  }
+}
+
+// Q fragments of one query row for the S^T = K Q^T products: qf[dc] holds
+// dims 16 dc + 8 g .. + 7, zeros at or past head_dim.
+template <typename X8, typename T>
+__device__ __forceinline__ void load_q_fragments(const T* qrow, int g, int head_dim, X8 qf[8]) {
+#pragma unroll
+  for (int dc = 0; dc < 8; ++dc) {
+    if (dc * 16 + g * 8 < head_dim) {
+      qf[dc] = *reinterpret_cast<const X8*>(qrow + dc * 16 + g * 8);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[dc][e] = (T)0.0f;
+    }
   }
 }
 

@@ -33,6 +33,7 @@ struct MassParams {
   float* mass;  // [heads, blocks, blocks]
   int64_t q_st, q_sh, k_st, k_sh;
   int32_t tokens, heads, blocks, block_size, samples;  // samples: S (real)
+  int32_t head_dim;  // 8..128, a multiple of 8
   float scale;      // score scale (d^-1/2 unless given)
   float logw_full;  // log(block_size / S)
   float logw_last;  // log(size of the last block / S)
@@ -106,9 +107,7 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
   const T* qrow = static_cast<const T*>(p.q) + h * p.q_sh +
                   (int64_t)sampled_token<SP>(qs, p.tokens, p.block_size, S) * p.q_st;
   typename E::x8 qf[8];
-#pragma unroll
-  for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const typename E::x8*>(qrow + dc * 16 + g * 8);
+  dsa::load_q_fragments(qrow, g, p.head_dim, qf);
 
   // The head's K rows as one raw buffer (the host keeps them within 2^31 bytes).
   const T* kbase = static_cast<const T*>(p.k) + h * p.k_sh;
@@ -126,7 +125,8 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
       int key = kt0 + row;
       key = key < ns ? key : ns - 1;
       const uint32_t off = (uint32_t)(
-          ((int64_t)sampled_token<SP>(key, p.tokens, p.block_size, S) * p.k_st + c * 8) * 2);
+          ((int64_t)sampled_token<SP>(key, p.tokens, p.block_size, S) * p.k_st + c * 8) * 2) |
+                           dsa::dead_bits(c, p.head_dim);
       dsa::lds_load16(k_rsrc, dst + (wave * 4 + j) * 1024, off, 0);
     }
   };
@@ -337,8 +337,9 @@ extern "C" int dsa_sampled_mass(const void* q, const void* k, int32_t dtype,
                           dtype);
   if (tokens <= 0 || heads <= 0 || block_size <= 0)
     return dsa::set_error(DSA_EINVAL, "dsa_sampled_mass: tokens/heads/block must be positive");
-  if (head_dim != kHeadDim)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_sampled_mass: head_dim %d unsupported (128)",
+  if (head_dim <= 0 || head_dim > kHeadDim || head_dim % 8 != 0)
+    return dsa::set_error(DSA_EUNSUPPORTED,
+                          "dsa_sampled_mass: head_dim %d unsupported (a multiple of 8 up to 128)",
                           head_dim);
   if (block_size > 128)
     return dsa::set_error(DSA_EUNSUPPORTED, "dsa_sampled_mass: block_size %d unsupported (<= 128)",
@@ -366,6 +367,7 @@ extern "C" int dsa_sampled_mass(const void* q, const void* k, int32_t dtype,
   p.heads = heads;
   p.block_size = block_size;
   p.samples = samples;
+  p.head_dim = head_dim;
   p.blocks = (tokens + block_size - 1) / block_size;
   if ((int64_t)p.blocks * sp > 0x3fffffff)
     return dsa::set_error(DSA_EUNSUPPORTED, "dsa_sampled_mass: too many sampled tokens");

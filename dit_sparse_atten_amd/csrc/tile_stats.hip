@@ -62,6 +62,7 @@ struct TileStatsParams {
   int64_t q_st, q_sh, k_st, k_sh, lse_sh;
   int32_t tokens, heads, tiles, tile, tile_h, tile_w;
   int32_t tile_pad;  // gathered stream: key slots per tile (tile rounded up to 8)
+  int32_t head_dim;  // 8..128, a multiple of 8
   float scale_log2;
 };
 
@@ -109,9 +110,7 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
   const int tq_c = tq < p.tokens ? tq : p.tokens - 1;
   const T* qrow = static_cast<const T*>(p.q) + h * p.q_sh + (int64_t)tq_c * p.q_st;
   typename E::x8 qf[8];
-#pragma unroll
-  for (int dc = 0; dc < 8; ++dc)
-    qf[dc] = *reinterpret_cast<const typename E::x8*>(qrow + dc * 16 + g * 8);
+  dsa::load_q_fragments(qrow, g, p.head_dim, qf);
   const float lse2 = row_ok ? p.lse[h * p.lse_sh + tq] * kLog2e : INFINITY;
 
   int start = 0, end = p.tiles;
@@ -128,8 +127,8 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
   const int ntile = end - start;
 
   const T* kbase = static_cast<const T*>(p.k) + h * p.k_sh;
-  int koff[4];
-  dsa::k_tile_offsets(wave, lane, p.k_st, koff);
+  uint32_t koff[4];
+  dsa::k_tile_offsets(wave, lane, p.k_st, p.head_dim, koff);
   auto issue = [&](int kt, int half, unsigned char* dst) __attribute__((always_inline)) {
     const int key0 = (kt < 0 ? 0 : kt) * p.tile + half * kHalfKeys;
     const __amdgpu_buffer_rsrc_t rsrc = dsa::k_tile_rsrc(kbase, p.k_st, key0, p.tokens);
@@ -140,8 +139,10 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
       // The stage's 16 1-KB slices, dealt round-robin over the waves.
       for (int i = wave; i < kKStage / 1024; i += kWaves) {
         const int row = i * 4 + (lane >> 4);
+        const int c = dsa::k2_swz(row, lane & 15);
         dsa::lds_load16(rsrc, dst + i * 1024,
-                        (uint32_t)((row * (int)p.k_st + dsa::k2_swz(row, lane & 15) * 8) * 2), 0);
+                        (uint32_t)((row * (int)p.k_st + c * 8) * 2) | dsa::dead_bits(c, p.head_dim),
+                        0);
       }
     }
   };
@@ -249,8 +250,9 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
         const int o = o0 + row;
         const bool first = o < bp;
         const int token = (first ? kta : ktb) * p.tile + (first ? o : o - bp);
+        const int c = dsa::k2_swz(row, lane & 15);
         dsa::lds_load16(k_all, dst + i * 1024,
-                        (uint32_t)token * kst2 + (uint32_t)(dsa::k2_swz(row, lane & 15) * 16),
+                        ((uint32_t)token * kst2 + (uint32_t)(c * 16)) | dsa::dead_bits(c, p.head_dim),
                         0);
       }
     };
@@ -454,8 +456,9 @@ extern "C" int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const
     return dsa::set_error(DSA_EINVAL, "dsa_tile_stats: row_ptr and col_idx must both be set");
   if (tokens <= 0 || heads <= 0)
     return dsa::set_error(DSA_EINVAL, "dsa_tile_stats: tokens and heads must be positive");
-  if (head_dim != dsa::kHeadDim)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_tile_stats: head_dim %d unsupported (128)",
+  if (head_dim <= 0 || head_dim > dsa::kHeadDim || head_dim % 8 != 0)
+    return dsa::set_error(DSA_EUNSUPPORTED,
+                          "dsa_tile_stats: head_dim %d unsupported (a multiple of 8 up to 128)",
                           head_dim);
   if (tile_h <= 0 || tile_w <= 0 || tile_h * tile_w > 128)
     return dsa::set_error(DSA_EUNSUPPORTED, "dsa_tile_stats: tile %dx%d unsupported (<= 128)",
@@ -506,6 +509,7 @@ extern "C" int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const
   p.tile_h = tile_h;
   p.tile_w = tile_w;
   p.tile_pad = (tile + 7) & ~7;
+  p.head_dim = head_dim;
   p.scale_log2 = scale * kLog2e;
   const bool routed = row_ptr != nullptr;
   const int32_t plain_slots = tile - kHalfKeys <= 32 ? kHalfKeys + 32 : 2 * kHalfKeys;

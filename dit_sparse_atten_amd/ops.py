@@ -110,17 +110,20 @@ def csr_from_route(route, block_size=128):
     return route_to_csr(route, block_size=block_size)
 
 
-def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_size=128):
+def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_size=128,
+            causal=False):
     """Block-sparse (or, with ``csr=None``, dense) attention forward on the GPU.
 
     ``block_size`` (1..128) is the number of consecutive tokens per query
     block and per key block that the route addresses: 128 for ``flex_reuse``,
     the spatial tile size for the matrix-sparse backend.
 
-    q: [B,Tq,H,128], k/v: [B,Tk,H,128], all bf16 or all fp16 (the compute
-    type), on a HIP device, any strides with a contiguous head dim.  Returns O
-    [B,Tq,H,128] in that type (contiguous unless ``out`` is given) and, with
-    ``return_lse``, the natural-log LSE [B,H,Tq] fp32.
+    q: [B,Tq,H,D], k/v: [B,Tk,H,D], D a multiple of 8 up to 128, all bf16 or
+    all fp16 (the compute type), on a HIP device, any strides with a
+    contiguous head dim.  ``causal`` (dense calls only): query t attends keys
+    k <= t, as SDPA's is_causal.  Returns O [B,Tq,H,D] in that type
+    (contiguous unless ``out`` is given) and, with ``return_lse``, the
+    natural-log LSE [B,H,Tq] fp32.
     """
     lib = _lib.load()
     q = _kernel_view("q", q)
@@ -179,7 +182,7 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
             batch, q_tokens, kv_tokens, heads, head_dim, block_size,
             row_ptr.data_ptr() if row_ptr is not None else None,
             col_idx.data_ptr() if col_idx is not None else None,
-            route_batches, float(scale),
+            route_batches, float(scale), int(bool(causal)),
             lse.data_ptr() if lse is not None else None,
             workspace.data_ptr() if workspace is not None else None, workspace_bytes,
             _stream_handle(q.device))

@@ -44,7 +44,9 @@ const char* dsa_last_error(void);
  * SDPA (attention_backends/dense.py:14-48).
  *   strides[12]: q (b,t,h), k (b,t,h), v (b,t,h), o (b,t,h), in elements,
  *                each a multiple of 8; pointers 16-byte aligned.
- *   head_dim: 128.  block_size: 1..128 tokens per query block and per key
+ *   head_dim: a multiple of 8 up to 128 (dims past it are zero-filled in the
+ *                kernel; the matrix products run at 128).  block_size: 1..128
+ *                tokens per query block and per key
  *                block (128 for the flex_reuse route; the spatial tile size of
  *                the matrix-sparse backend, sparse.py:51-103, 670-751).
  *   row_ptr/col_idx: CSR over rows ((rb * heads + h) * q_blocks + qb), rb <
@@ -53,6 +55,10 @@ const char* dsa_last_error(void);
  *                Requires q_tokens == kv_tokens.  Out-of-range key blocks are
  *                skipped; a row with no key blocks yields zeros.
  *   scale: softmax scale (d^-1/2 for softmax_scale=None).
+ *   causal: 1 for SDPA's is_causal (query t attends keys k <= t, top-left
+ *                aligned when q_tokens != kv_tokens); dense calls only (the
+ *                reference sends causal calls to its dense backend,
+ *                flex.py:655-668, dense.py:40-47).
  *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
  *   workspace: optional device scratch (NULL with workspace_bytes == 0, or
  *                16-byte aligned) for the fp32 partials of the query blocks in
@@ -69,8 +75,8 @@ const char* dsa_last_error(void);
 int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                 const int64_t* strides, int32_t batch, int32_t q_tokens, int32_t kv_tokens,
                 int32_t heads, int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
-                const int32_t* col_idx, int32_t route_batches, float scale, float* lse,
-                void* workspace, size_t workspace_bytes, hipStream_t stream);
+                const int32_t* col_idx, int32_t route_batches, float scale, int32_t causal,
+                float* lse, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Workspace bytes that let dsa_bsa_fwd with 128-token blocks split its last
  * round as far as it ever does: 68,157,440 (1,024 partials of 128 x 130
@@ -103,7 +109,7 @@ int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o, in
                         const int64_t* strides, int32_t batch, int32_t q_tokens,
                         int32_t kv_tokens, int32_t heads, int32_t head_dim, int32_t block_size,
                         const int32_t* row_ptr, const int32_t* col_idx, int32_t route_batches,
-                        float scale, float* lse, hipStream_t stream);
+                        float scale, int32_t causal, float* lse, hipStream_t stream);
 
 /*
  * Sampled block-mass estimate for one batch-1 self-attention call, bf16 or

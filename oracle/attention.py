@@ -27,7 +27,7 @@ def _as_route(route, batch):
     return route
 
 
-def block_sparse_attention(q, k, v, route, block_size, scale=None, rows=None):
+def block_sparse_attention(q, k, v, route, block_size, scale=None, rows=None, causal=False):
     """Masked-softmax attention in float64.
 
     q: [B,Tq,H,D]; k, v: [B,Tk,H,D] (any float dtype); route: boolean
@@ -35,7 +35,9 @@ def block_sparse_attention(q, k, v, route, block_size, scale=None, rows=None):
     the evaluation to a list of (b, h, query_block) triples; the result then
     holds only those query blocks (others are NaN).  Query rows whose route row
     is empty produce zeros (the convention of an attention kernel without the
-    ROWS_GUARANTEED_SAFE guarantee, flex.py:360-364).
+    ROWS_GUARANTEED_SAFE guarantee, flex.py:360-364).  ``causal`` (dense only)
+    additionally masks keys k > t for query t, as SDPA's is_causal does
+    (dense.py:40-47 passes it through).
     Returns (O [B,Tq,H,D] float64, LSE [B,H,Tq] float64 natural log).
     """
     q = np.asarray(q, dtype=np.float64)
@@ -60,6 +62,9 @@ def block_sparse_attention(q, k, v, route, block_size, scale=None, rows=None):
         if route is not None:
             allowed = route[0 if route.shape[0] == 1 else b, h, qb][key_block]
             scores = np.where(allowed[None, :], scores, -np.inf)
+        if causal:
+            later = np.arange(kv_tokens)[None, :] > np.arange(t0, t1)[:, None]
+            scores = np.where(later, -np.inf, scores)
         row_max = scores.max(-1, keepdims=True)
         empty = ~np.isfinite(row_max[:, 0])
         row_max = np.where(np.isfinite(row_max), row_max, 0.0)

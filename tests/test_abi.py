@@ -62,21 +62,21 @@ def test_version_and_workspace_size(lib):
 def test_invalid_arguments_are_reported_before_any_launch(lib):
     strides = _lib.int64_array([8] * 12)
     status = lib.dsa_bsa_fwd(None, None, None, None, 0, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, None, None, 0, None)
+                             None, None, 1, 0.1, 0, None, None, 0, None)
     assert status == _lib.DSA_EINVAL
     assert "null" in _lib.last_error()
     with pytest.raises(ValueError, match="null"):
         _lib.check(status, "dsa_bsa_fwd")
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 64, 128,
-                             None, None, 1, 0.1, None, fake, 1 << 20, None)
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 136, 128,
+                             None, None, 1, 0.1, 0, None, fake, 1 << 20, None)
     assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
     misaligned = ctypes.c_void_p(24)
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, None, misaligned, 1 << 20, None)
+                             None, None, 1, 0.1, 0, None, misaligned, 1 << 20, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, None, None, 1 << 20, None)
+                             None, None, 1, 0.1, 0, None, None, 1 << 20, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
     status = lib.dsa_route_select(fake, None, 4, 2100, 0.5, 0.95, 1, 0, fake, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "2048" in _lib.last_error()
@@ -87,8 +87,14 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
                                   16, 0.1, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "dtype" in _lib.last_error()
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 7, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, None, None, 0, None)
+                             None, None, 1, 0.1, 0, None, None, 0, None)
     assert status == _lib.DSA_EUNSUPPORTED and "dtype" in _lib.last_error()
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
+                             fake, fake, 1, 0.1, 1, None, None, 0, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "causal" in _lib.last_error()
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
+                             None, None, 1, 0.1, 2, None, None, 0, None)
+    assert status == _lib.DSA_EINVAL and "causal" in _lib.last_error()
     status = lib.dsa_permute_rows(4, None, None, None, None, None, 1, 1, 1, 16, None)
     assert status == _lib.DSA_EINVAL
 
@@ -96,7 +102,7 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
 def test_exact_and_routing_entry_points_validate_first(lib):
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     strides = _lib.int64_array([8] * 4)
-    status = lib.dsa_block_mass(fake, fake, 0, strides, 256, 2, 64, 128, fake, 256, 0.1, fake, None)
+    status = lib.dsa_block_mass(fake, fake, 0, strides, 256, 2, 60, 128, fake, 256, 0.1, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
     status = lib.dsa_block_mass(fake, fake, 0, strides, 256, 2, 128, 128, fake, 100, 0.1, fake,
                                 None)

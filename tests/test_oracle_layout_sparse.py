@@ -159,3 +159,25 @@ def test_attention_oracle_full_route_equals_sdpa():
                                        np.ones((2, 2, 2), bool), 128)
     np.testing.assert_allclose(out, expected.numpy(), atol=2e-6)
     np.testing.assert_allclose(ones, out, atol=0)
+
+
+@pytest.mark.parametrize("q_tokens,kv_tokens", [(200, 200), (150, 230), (230, 150)])
+def test_attention_oracle_causal_equals_sdpa_is_causal(q_tokens, kv_tokens):
+    """causal=True == SDPA(is_causal=True), including SDPA's top-left alignment
+    when the query and key lengths differ (torch CPU fp64)."""
+    generator = torch.Generator().manual_seed(q_tokens + kv_tokens)
+    q = torch.randn(1, q_tokens, 2, 16, generator=generator, dtype=torch.float64)
+    k, v = (torch.randn(1, kv_tokens, 2, 16, generator=generator, dtype=torch.float64)
+            for _ in range(2))
+    expected = torch.nn.functional.scaled_dot_product_attention(
+        q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True).transpose(1, 2)
+    out, _ = A.block_sparse_attention(q.numpy(), k.numpy(), v.numpy(), None, 64, causal=True)
+    np.testing.assert_allclose(out, expected.numpy(), atol=1e-12)
+    # A planted mistake (keys k < t instead of k <= t: the diagonal dropped)
+    # must not pass the same check.
+    scores = np.einsum("bqhd,bkhd->bhqk", q.numpy(), k.numpy()) / 4.0
+    strict = np.arange(kv_tokens)[None, :] >= np.arange(q_tokens)[:, None]
+    scores = np.where(strict, -np.inf, scores)[:, :, 1:]
+    weights = np.exp(scores - scores.max(-1, keepdims=True))
+    wrong = np.einsum("bhqk,bkhd->bqhd", weights / weights.sum(-1, keepdims=True), v.numpy())
+    assert not np.allclose(wrong, expected.numpy()[:, 1:], atol=1e-3)

@@ -48,7 +48,7 @@ def test_noalloc_matches_workspace_entry_point(cuda_device):
         assert bytes_ > 0
         workspace = torch.empty(bytes_, dtype=torch.uint8, device=cuda_device)
         args = (strides, 1, tokens, tokens, heads, 128, 128, csr.row_ptr.data_ptr(),
-                csr.col_idx.data_ptr(), 1, 128 ** -0.5)
+                csr.col_idx.data_ptr(), 1, 128 ** -0.5, 0)
         _lib.check(lib.dsa_bsa_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), want.data_ptr(),
                                    0, *args, want_lse.data_ptr(), workspace.data_ptr(), bytes_,
                                    stream), "dsa_bsa_fwd")
@@ -71,5 +71,5 @@ def test_noalloc_validates_before_launch(cuda_device):
     from dit_sparse_atten_amd import _lib
     lib = _lib.load()
     status = lib.dsa_bsa_fwd_noalloc(None, None, None, None, 0, _lib.int64_array([8] * 12), 1, 128,
-                                     128, 1, 128, 128, None, None, 1, 0.1, None, None)
+                                     128, 1, 128, 128, None, None, 1, 0.1, 0, None, None)
     assert status == _lib.DSA_EINVAL and "null" in _lib.last_error()
