@@ -61,12 +61,19 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
     float x = e < K ? mrow[e] : 0.f;
     v[j] = x > 0.f ? x : 0.f;  // rows are probabilities: clamp -0.0 and noise
   }
+  auto row_max = [&]() {
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) mx = fmaxf(mx, v[j]);
+    return dsa::wave_max_f32(mx);
+  };
   if (p.previous) {
+    const int s0 = dsa::row_shift(row_max(), K);
     int64_t s = 0;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) s += to_fixed(v[j]);
+    for (int j = 0; j < kPer; ++j) s += to_fixed(v[j], s0);
     s = wave_sum_i64(s);
-    const float mean = fixed_to_f32(s) / (float)K;
+    const float mean = fixed_to_f32(s, s0) / (float)K;
     const float prior = p.rho * mean;
     const uint8_t* prow = p.previous + (int64_t)row * K;
 #pragma unroll
@@ -75,11 +82,12 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
       if (e < K && prow[e]) v[j] = v[j] + prior;
     }
   }
+  const int shift = dsa::row_shift(row_max(), K);
   int64_t total = 0;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) total += to_fixed(v[j]);
+  for (int j = 0; j < kPer; ++j) total += to_fixed(v[j], shift);
   total = wave_sum_i64(total);
-  const float threshold = fixed_to_f32(total) * p.target;
+  const float threshold = fixed_to_f32(total, shift) * p.target;
 
   // Descending sort of key = value bits << 32 | (kN - 1 - index).
   uint64_t key[kPer];
@@ -95,7 +103,7 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
   int64_t run = 0;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
-    run += to_fixed(__uint_as_float((uint32_t)(key[j] >> 32)));
+    run += to_fixed(__uint_as_float((uint32_t)(key[j] >> 32)), shift);
     pre[j] = run;
   }
   int64_t scan = run;
@@ -109,7 +117,7 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int e = lane * kPer + j;
-    if (e < K && fixed_to_f32(pre[j] + offset) < threshold) ++below;
+    if (e < K && fixed_to_f32(pre[j] + offset, shift) < threshold) ++below;
   }
   int count = wave_sum_i32(below) + 1;
   count = count < p.cap ? count : p.cap;
@@ -139,6 +147,143 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
   }
   selected = wave_sum_i32(selected);
   if (lane == 0) p.counts[row] = selected;
+}
+
+// Rows of 2049..16384 keys: one 256-thread workgroup per row, the same
+// arithmetic as route_select_kernel, values in registers (kPer per thread,
+// element e = tid + 256 j) and a bitonic sort of the 64-bit keys in LDS.
+constexpr int kWideKeys = 16384;
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = dsa::wave_max_f32(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  dsa::lds_barrier();
+  const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  dsa::lds_barrier();
+  return r;
+}
+
+__device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* red) {
+  v = wave_sum_i64(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  dsa::lds_barrier();
+  const int64_t r = (red[0] + red[1]) + (red[2] + red[3]);
+  dsa::lds_barrier();
+  return r;
+}
+
+template <int kPer>
+__global__ void __launch_bounds__(256) route_select_wide_kernel(SelectParams p) {
+  constexpr int kN = 256 * kPer;
+  __shared__ uint64_t keys[kN];  // 128 KB at 16384 keys (LDS: 160 KB per CU)
+  __shared__ uint8_t flags[kN];
+  __shared__ int64_t scan[256];
+  __shared__ int64_t red64[4];
+  __shared__ float red32[4];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const int K = p.keys;
+  const float* mrow = p.mass + (int64_t)row * K;
+
+  float v[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid + 256 * j;
+    const float x = e < K ? mrow[e] : 0.f;
+    v[j] = x > 0.f ? x : 0.f;
+  }
+  auto row_max = [&]() {
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) mx = fmaxf(mx, v[j]);
+    return block_max(mx, red32);
+  };
+  if (p.previous) {
+    const int s0 = dsa::row_shift(row_max(), K);
+    int64_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) sum += to_fixed(v[j], s0);
+    sum = block_sum_i64(sum, red64);
+    const float mean = fixed_to_f32(sum, s0) / (float)K;
+    const float prior = p.rho * mean;
+    const uint8_t* prow = p.previous + (int64_t)row * K;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid + 256 * j;
+      if (e < K && prow[e]) v[j] = v[j] + prior;
+    }
+  }
+  const int shift = dsa::row_shift(row_max(), K);
+  int64_t total = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) total += to_fixed(v[j], shift);
+  total = block_sum_i64(total, red64);
+  const float threshold = fixed_to_f32(total, shift) * p.target;
+
+  // Descending bitonic sort of value bits << 32 | (kN - 1 - index).
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid + 256 * j;
+    keys[e] = e < K ? ((uint64_t)__float_as_uint(v[j]) << 32) | (uint32_t)(kN - 1 - e) : 0ull;
+  }
+  for (int size = 2; size <= kN; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      dsa::lds_barrier();
+      for (int i = tid; i < kN / 2; i += 256) {
+        const int lo = 2 * stride * (i / stride) + (i % stride);
+        const int hi = lo + stride;
+        const bool descending = (lo & size) == 0;
+        const uint64_t a = keys[lo], b = keys[hi];
+        if ((a < b) == descending) {
+          keys[lo] = b;
+          keys[hi] = a;
+        }
+      }
+    }
+  }
+  dsa::lds_barrier();
+
+  // Exact prefix sums in sorted order: each thread a contiguous segment.
+  const int seg0 = tid * kPer;
+  int64_t local = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) local += to_fixed(__uint_as_float((uint32_t)(keys[seg0 + j] >> 32)), shift);
+  scan[tid] = local;
+  dsa::lds_barrier();
+  for (int offset = 1; offset < 256; offset <<= 1) {
+    const int64_t add = tid >= offset ? scan[tid - offset] : 0;
+    dsa::lds_barrier();
+    scan[tid] += add;
+    dsa::lds_barrier();
+  }
+  int64_t run = scan[tid] - local;
+  int below = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    run += to_fixed(__uint_as_float((uint32_t)(keys[seg0 + j] >> 32)), shift);
+    if (seg0 + j < K && fixed_to_f32(run, shift) < threshold) ++below;
+  }
+  below = (int)block_sum_i64(below, red64);
+  int count = below + 1;
+  count = count < p.cap ? count : p.cap;
+
+  // Selected flags: the first `count` sorted positions.
+  for (int e = tid; e < kN; e += 256) flags[e] = 0;
+  dsa::lds_barrier();
+  for (int pos = tid; pos < count; pos += 256)
+    flags[kN - 1 - (int)(keys[pos] & 0xffffffffu)] = 1;
+  dsa::lds_barrier();
+  int selected = 0;
+  uint8_t* rout = p.route + (int64_t)row * K;
+  for (int e = tid; e < K; e += 256) {
+    const uint8_t on = (flags[e] || e < p.sink) ? 1 : 0;
+    rout[e] = on;
+    selected += on;
+  }
+  selected = (int)block_sum_i64(selected, red64);
+  if (tid == 0) p.counts[row] = selected;
 }
 
 // ---------------------------------------------------------------------------
@@ -243,9 +388,9 @@ extern "C" int dsa_route_select(const float* mass, const uint8_t* previous, int3
   dsa::clear_error();
   if (!mass || !route || !counts) return dsa::set_error(DSA_EINVAL, "dsa_route_select: null pointer");
   if (rows <= 0 || keys <= 0) return dsa::set_error(DSA_EINVAL, "dsa_route_select: empty route");
-  if (keys > 2048)
-    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_route_select: at most 2048 key blocks (got %d)",
-                          keys);
+  if (keys > kWideKeys)
+    return dsa::set_error(DSA_EUNSUPPORTED, "dsa_route_select: at most %d key blocks (got %d)",
+                          kWideKeys, keys);
   if (!(target > 0.f && target <= 1.f))
     return dsa::set_error(DSA_EINVAL, "mass_target must be in (0, 1]");
   if (cap < 1) return dsa::set_error(DSA_EINVAL, "dsa_route_select: cap must be >= 1");
@@ -266,8 +411,14 @@ extern "C" int dsa_route_select(const float* mass, const uint8_t* previous, int3
     hipLaunchKernelGGL(route_select_kernel<8>, groups, threads, 0, stream, p);
   else if (keys <= 1024)
     hipLaunchKernelGGL(route_select_kernel<16>, groups, threads, 0, stream, p);
-  else
+  else if (keys <= 2048)
     hipLaunchKernelGGL(route_select_kernel<32>, groups, threads, 0, stream, p);
+  else if (keys <= 4096)
+    hipLaunchKernelGGL(route_select_wide_kernel<16>, dim3((unsigned)rows), threads, 0, stream, p);
+  else if (keys <= 8192)
+    hipLaunchKernelGGL(route_select_wide_kernel<32>, dim3((unsigned)rows), threads, 0, stream, p);
+  else
+    hipLaunchKernelGGL(route_select_wide_kernel<64>, dim3((unsigned)rows), threads, 0, stream, p);
   return dsa::check_launch("dsa_route_select");
 }
 

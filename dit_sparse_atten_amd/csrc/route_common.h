@@ -1,10 +1,13 @@
 // Row arithmetic shared by the route kernels (gfx950): exact fixed-point row
 // sums and a one-wave bitonic sort of up to 2048 keys.
 //
-// A row value m >= 0 is represented as the integer floor(m * 2^52), so row and
-// prefix sums are exact and independent of summation order; a sum is rounded
-// once to fp32.  The CPU oracle uses the same arithmetic, which makes routes
-// bit-exact given the same fp32 inputs.
+// A row value m >= 0 is represented as the integer floor(m * 2^(52 + s)), so
+// row and prefix sums are exact and independent of summation order; a sum is
+// rounded once to fp32 and scaled back by 2^-(52 + s).  The row exponent s
+// (row_shift) is the largest integer with keys * max * 2^s < 2^10, so no sum
+// of a row's images reaches 2^62 whatever the mass's magnitude; a power-of-two
+// scale leaves the fp32 arithmetic on the sums unchanged.  The CPU oracle uses
+// the same arithmetic, which makes routes bit-exact given the same fp32 inputs.
 #pragma once
 
 #include "dsa_common.h"
@@ -20,6 +23,27 @@ __device__ __forceinline__ int64_t to_fixed(float v) {
 
 __device__ __forceinline__ float fixed_to_f32(int64_t x) {
   return (float)x * kInvFixed;  // i64 -> f32 rounds to nearest even
+}
+
+// Row exponent s of a row of `keys` values whose largest is max_value (0 for
+// an all-zero row).
+__device__ __forceinline__ int row_shift(float max_value, int keys) {
+  if (!(max_value > 0.f)) return 0;
+  return 9 - ilogb((double)keys * (double)max_value);
+}
+
+__device__ __forceinline__ int64_t to_fixed(float v, int shift) {
+  return (int64_t)__builtin_floor(ldexp((double)v, 52 + shift));
+}
+
+__device__ __forceinline__ float fixed_to_f32(int64_t x, int shift) {
+  return ldexpf((float)x, -(52 + shift));  // i64 -> f32 rounds to nearest even
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m));
+  return v;
 }
 
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {

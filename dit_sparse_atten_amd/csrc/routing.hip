@@ -228,7 +228,16 @@ __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
     cand[j] = in && !prev[j] && p.candidates[base + e] != 0;
     pool[j] = prev[j] || cand[j];
     prev_count += prev[j];
-    fixed_sum += in ? to_fixed(m[j] > 0.f ? m[j] : 0.f) : 0;
+  }
+  // Exact row sum (scaled fixed point, route_common.h) for the row mean.
+  float row_max = 0.f;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) row_max = fmaxf(row_max, m[j] > 0.f ? m[j] : 0.f);
+  const int shift = dsa::row_shift(dsa::wave_max_f32(row_max), K);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = lane * kPer + j;
+    fixed_sum += e < K ? to_fixed(m[j] > 0.f ? m[j] : 0.f, shift) : 0;
   }
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
@@ -268,7 +277,7 @@ __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
   pool_count = wave_sum_i32(pool_count);
   prev_count = wave_sum_i32(prev_count);
   fixed_sum = wave_sum_i64(fixed_sum);
-  const float mean = fixed_to_f32(fixed_sum) / (float)K;
+  const float mean = fixed_to_f32(fixed_sum, shift) / (float)K;
   const float prior = p.persistence * mean;
   const float bonus = p.bonus * mean;
   int budget = (int)ceilf((float)prev_count * p.budget_scale);

@@ -10,10 +10,13 @@ Follows attention_backends/flex.py:
 
 Route-selection arithmetic (the one documented arithmetic shared with the HIP
 kernel, so that routes are bit-exact given the same fp32 mass):
-  * a row value m >= 0 is represented exactly as the integer floor(m * 2^52)
-    (values below 2^-29 lose their low bits; below 2^-52 they count as 0);
+  * a row value m >= 0 is represented exactly as the integer
+    floor(m * 2^(52 + s)), with the row exponent s the largest integer for
+    which K * max(row) * 2^s < 2^10 (s = 0 for an all-zero row), so no sum of
+    the row reaches 2^62 whatever the mass's magnitude;
   * every row sum and prefix sum is the exact integer sum, rounded once to
-    fp32 (round-to-nearest-even) and scaled by 2^-52;
+    fp32 (round-to-nearest-even) and scaled by 2^-(52 + s) (a power of two:
+    the fp32 arithmetic below does not depend on s);
   * threshold = fp32(fp32(row sum) * fp32(target)); mean = fp32(row sum / K);
   * prior: m' = fp32(m + fp32(fp32(rho) * mean) * prev);
   * the row is ordered by value descending, ties by key index ascending;
@@ -106,20 +109,41 @@ def sampled_block_mass(q, k, block_size, samples, scale=None, bf16_scores=True,
     return probabilities.reshape(heads, rows, samples, blocks, samples).sum(-1).mean(2)
 
 
-def _fixed(row):
-    """Exact integer image floor(m * 2^52) of non-negative fp32 values."""
-    return np.floor(np.asarray(row, dtype=np.float32).astype(np.float64) * _FIXED_SCALE).astype(
-        np.int64)
+def row_shift(mass):
+    """Row exponent s of every row of a non-negative fp32 [..., K] tensor: the
+    largest integer with K * max(row) * 2^s < 2^10, 0 for an all-zero row."""
+    mass = np.asarray(mass, dtype=np.float32)
+    top = mass.max(-1).astype(np.float64)
+    _, exponent = np.frexp(mass.shape[-1] * top)  # K * max = f * 2^e, f in [0.5, 1)
+    return np.where(top > 0, 10 - exponent, 0).astype(np.int64)
 
 
-def _fixed_to_f32(total):
-    """Round exact fixed-point sums to fp32 (RNE) and rescale."""
-    return np.asarray(total, dtype=np.int64).astype(np.float32) * _INV_SCALE
+def _fixed(row, shift=None):
+    """Exact integer image floor(m * 2^(52 + s)) of non-negative fp32 values
+    (s per row, [..., 1]; None: s = 0)."""
+    row = np.asarray(row, dtype=np.float32).astype(np.float64)
+    if shift is None:
+        return np.floor(row * _FIXED_SCALE).astype(np.int64)
+    return np.floor(np.ldexp(row, (FIXED_SHIFT + shift).astype(np.int32))).astype(np.int64)
 
 
-def row_sums_f32(mass):
-    """Exact row sums of a non-negative fp32 [..., K] tensor, rounded to fp32."""
-    return _fixed_to_f32(_fixed(mass).sum(-1))
+def _fixed_to_f32(total, shift=None):
+    """Round exact fixed-point sums to fp32 (RNE) and rescale by 2^-(52 + s)."""
+    total = np.asarray(total, dtype=np.int64).astype(np.float32)
+    if shift is None:
+        return total * _INV_SCALE
+    return np.ldexp(total, (-(FIXED_SHIFT + shift)).astype(np.int32)).astype(np.float32)
+
+
+def row_sums_f32(mass, scaled=True):
+    """Exact row sums of a non-negative fp32 [..., K] tensor, rounded to fp32:
+    in the scaled fixed point of the route arithmetic, or (scaled=False) at
+    the fixed scale 2^52, as the matrix-sparse head sums accumulate across
+    workgroups."""
+    if not scaled:
+        return _fixed_to_f32(_fixed(mass).sum(-1))
+    shift = row_shift(mass)
+    return _fixed_to_f32(_fixed(mass, shift[..., None]).sum(-1), shift)
 
 
 def persistence_prior(mass, previous, rho):
@@ -152,10 +176,12 @@ def top_mass_route(mass, target, keep, return_margins=False):
     cap = route_cap(keys, keep)
     target32 = np.float32(target)
     order = np.argsort(-rows, axis=-1, kind="stable")
-    fixed = _fixed(rows)
-    totals = _fixed_to_f32(fixed.sum(-1))
+    shift = row_shift(rows)
+    fixed = _fixed(rows, shift[:, None])
+    totals = _fixed_to_f32(fixed.sum(-1), shift)
     thresholds = (totals * target32).astype(np.float32)
-    prefix = _fixed_to_f32(np.cumsum(np.take_along_axis(fixed, order, -1), axis=-1))
+    prefix = _fixed_to_f32(np.cumsum(np.take_along_axis(fixed, order, -1), axis=-1),
+                           shift[:, None])
     below = prefix < thresholds[:, None]
     counts = np.minimum(below.sum(-1) + 1, cap)
     ranks = np.empty_like(order)

@@ -227,7 +227,7 @@ def head_sums(mask, mass):
     fp32, and the selected counts."""
     m32 = np.where(mask, np.maximum(np.asarray(mass, dtype=np.float32), 0), 0).astype(np.float32)
     flat = m32.reshape(m32.shape[0], -1)
-    return route_oracle.row_sums_f32(flat), mask.reshape(mask.shape[0], -1).sum(-1)
+    return route_oracle.row_sums_f32(flat, scaled=False), mask.reshape(mask.shape[0], -1).sum(-1)
 
 
 def preserve_one_per_row(kept, original, mass):

@@ -78,8 +78,8 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
                              None, None, 1, 0.1, 0, None, None, 1 << 20, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
-    status = lib.dsa_route_select(fake, None, 4, 2100, 0.5, 0.95, 1, 0, fake, fake, None)
-    assert status == _lib.DSA_EUNSUPPORTED and "2048" in _lib.last_error()
+    status = lib.dsa_route_select(fake, None, 4, 16385, 0.5, 0.95, 1, 0, fake, fake, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "16384" in _lib.last_error()
     status = lib.dsa_sampled_mass(fake, fake, 0, _lib.int64_array([8] * 4), 1024, 2, 128, 128,
                                   129, 0.1, fake, None)
     assert status == _lib.DSA_EINVAL and "route_samples" in _lib.last_error()

@@ -239,9 +239,48 @@ def test_route_select_beyond_1024_keys(ops, cuda_device, keys):
     assert (counts.cpu().numpy() == expected.sum(-1)).all()
 
 
-def test_route_select_rejects_more_than_2048_keys(ops, cuda_device):
-    with pytest.raises(ValueError, match="2048"):
-        ops.route_select(torch.zeros(1, 1, 2049, device=cuda_device), 0.95, 0.625)
+@pytest.mark.parametrize("keys", [2049, 3000, 4096, 6000, 16384])
+def test_route_select_beyond_2048_keys(ops, cuda_device, keys):
+    """Rows of more than 2,048 key blocks (a workgroup per row, LDS sort):
+    bit-exact with the oracle, prior and sink included."""
+    rows = 8 if keys <= 6000 else 3
+    mass = _random_mass((1, rows, keys), seed=keys)
+    rng = np.random.default_rng(keys + 1)
+    previous = rng.random((1, rows, keys)) < 0.625
+    route, counts = ops.route_select(
+        torch.from_numpy(mass).to(cuda_device), 0.95, 0.625,
+        previous=torch.from_numpy(previous).to(cuda_device), persistence=0.5, sink_blocks=29)
+    plain, _ = ops.route_select(torch.from_numpy(mass).to(cuda_device), 0.9, 0.5)
+    torch.cuda.synchronize()
+    expected = R.top_mass_route(R.persistence_prior(mass, previous, 0.5), 0.95, 0.625)
+    expected[..., :29] = True
+    got = route.cpu().numpy()
+    assert (got == expected).all(), np.argwhere((got != expected).any(-1))[:5]
+    assert (counts.cpu().numpy() == expected.sum(-1)).all()
+    assert (plain.cpu().numpy() == R.top_mass_route(mass, 0.9, 0.5)).all()
+
+
+@pytest.mark.parametrize("keys", [450, 3000])
+def test_route_select_any_magnitude(ops, cuda_device, keys):
+    """Power-of-two scales of the mass (row sums from about 2^-90 to 2^40,
+    far past the 2^11 a fixed 2^52 fixed point holds) give the unscaled
+    route, and the oracle's, bit for bit."""
+    mass = _random_mass((2, 16, keys), seed=keys + 7)
+    rng = np.random.default_rng(keys + 8)
+    previous = rng.random(mass.shape) < 0.6
+    base = R.top_mass_route(R.persistence_prior(mass, previous, 0.5), 0.95, 0.625)
+    for exponent in (-90, 0, 40):
+        scaled = np.ldexp(mass, exponent).astype(np.float32)
+        route, _ = ops.route_select(
+            torch.from_numpy(scaled).to(cuda_device), 0.95, 0.625,
+            previous=torch.from_numpy(previous).to(cuda_device), persistence=0.5)
+        torch.cuda.synchronize()
+        assert (route.cpu().numpy() == base).all(), exponent
+
+
+def test_route_select_rejects_more_than_16384_keys(ops, cuda_device):
+    with pytest.raises(ValueError, match="16384"):
+        ops.route_select(torch.zeros(1, 1, 16385, device=cuda_device), 0.95, 0.625)
 
 
 @pytest.mark.parametrize("name", ["bootstrap", "prior"])

@@ -299,3 +299,35 @@ def test_oracle_matches_reference_route_at_config3_scale(name):
     near, tie_order, differing = compare_config3(route, primed, margins, expected, value_sum)
     assert near <= 40, near
     print(f"{name}: near-tie rows {near}, tie-order rows {tie_order}, differing rows {differing}")
+
+
+@pytest.mark.parametrize("prior", [False, True])
+def test_route_is_invariant_to_power_of_two_scaling(prior):
+    """Top-mass selection depends only on the ratios of a row's values, so a
+    power-of-two scale of the mass (exact in fp32) must not change the route,
+    including scales whose row sums are far above the 2^11 a fixed 2^52 fixed
+    point holds and far below fp32's normal range of sums."""
+    rng = np.random.default_rng(7)
+    mass = rng.dirichlet(np.full(450, 0.4), size=(4, 32)).astype(np.float32)
+    previous = rng.random(mass.shape) < 0.6 if prior else None
+    base = R.sampled_route(None, None, 128, 16, 0.95, 0.625, previous=previous, rho=0.5,
+                           mass=mass)
+    for exponent in (-90, -20, 12, 40):
+        scaled = np.ldexp(mass, exponent).astype(np.float32)
+        got = R.sampled_route(None, None, 128, 16, 0.95, 0.625, previous=previous, rho=0.5,
+                              mass=scaled)
+        assert (got == base).all(), exponent
+
+
+def test_row_shift_bounds_every_sum():
+    """K * max * 2^s < 2^10 <= 2 K * max * 2^s: sums of a row's fixed-point
+    images stay below 2^62, and s is the largest such exponent."""
+    rng = np.random.default_rng(8)
+    for keys in (1, 450, 2048, 16384):
+        mass = (rng.random((6, keys)) * np.float32(10.0) ** rng.integers(-30, 30, (6, 1))
+                ).astype(np.float32)
+        shift = R.row_shift(mass)
+        bound = keys * mass.max(-1).astype(np.float64) * np.ldexp(1.0, shift)
+        assert (bound < 2 ** 10).all() and (2 * bound >= 2 ** 10).all()
+        fixed = R._fixed(mass, shift[:, None])
+        assert (fixed.sum(-1) < 2 ** 62).all()
