@@ -161,7 +161,7 @@ class MatrixSparseBackend:
         key = (tuple(grid) if grid is not None else None, self.config.tile, tokens)
         if key not in self._layouts:
             layout = _spatial_layout(grid, self.config.tile, tokens)
-            if layout is not None and (layout.tile_tokens > 128 or layout.tile_count > 2048):
+            if layout is not None and (layout.tile_tokens > 128 or layout.tile_count > 16384):
                 layout = None  # beyond the kernels' tile limits: dense
             self._layouts[key] = layout
         return self._layouts[key]

@@ -154,26 +154,6 @@ __global__ void __launch_bounds__(256) route_select_kernel(SelectParams p) {
 // element e = tid + 256 j) and a bitonic sort of the 64-bit keys in LDS.
 constexpr int kWideKeys = 16384;
 
-__device__ __forceinline__ float block_max(float v, float* red) {
-  v = dsa::wave_max_f32(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) red[wave] = v;
-  dsa::lds_barrier();
-  const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  dsa::lds_barrier();
-  return r;
-}
-
-__device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* red) {
-  v = wave_sum_i64(v);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) red[wave] = v;
-  dsa::lds_barrier();
-  const int64_t r = (red[0] + red[1]) + (red[2] + red[3]);
-  dsa::lds_barrier();
-  return r;
-}
-
 template <int kPer>
 __global__ void __launch_bounds__(256) route_select_wide_kernel(SelectParams p) {
   constexpr int kN = 256 * kPer;
@@ -198,14 +178,14 @@ __global__ void __launch_bounds__(256) route_select_wide_kernel(SelectParams p) 
     float mx = 0.f;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) mx = fmaxf(mx, v[j]);
-    return block_max(mx, red32);
+    return dsa::block_max(mx, red32);
   };
   if (p.previous) {
     const int s0 = dsa::row_shift(row_max(), K);
     int64_t sum = 0;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) sum += to_fixed(v[j], s0);
-    sum = block_sum_i64(sum, red64);
+    sum = dsa::block_sum_i64(sum, red64);
     const float mean = fixed_to_f32(sum, s0) / (float)K;
     const float prior = p.rho * mean;
     const uint8_t* prow = p.previous + (int64_t)row * K;
@@ -219,7 +199,7 @@ __global__ void __launch_bounds__(256) route_select_wide_kernel(SelectParams p) 
   int64_t total = 0;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) total += to_fixed(v[j], shift);
-  total = block_sum_i64(total, red64);
+  total = dsa::block_sum_i64(total, red64);
   const float threshold = fixed_to_f32(total, shift) * p.target;
 
   // Descending bitonic sort of value bits << 32 | (kN - 1 - index).
@@ -228,22 +208,7 @@ __global__ void __launch_bounds__(256) route_select_wide_kernel(SelectParams p) 
     const int e = tid + 256 * j;
     keys[e] = e < K ? ((uint64_t)__float_as_uint(v[j]) << 32) | (uint32_t)(kN - 1 - e) : 0ull;
   }
-  for (int size = 2; size <= kN; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      dsa::lds_barrier();
-      for (int i = tid; i < kN / 2; i += 256) {
-        const int lo = 2 * stride * (i / stride) + (i % stride);
-        const int hi = lo + stride;
-        const bool descending = (lo & size) == 0;
-        const uint64_t a = keys[lo], b = keys[hi];
-        if ((a < b) == descending) {
-          keys[lo] = b;
-          keys[hi] = a;
-        }
-      }
-    }
-  }
-  dsa::lds_barrier();
+  dsa::sort_desc_lds<kN>(keys);
 
   // Exact prefix sums in sorted order: each thread a contiguous segment.
   const int seg0 = tid * kPer;
@@ -265,7 +230,7 @@ __global__ void __launch_bounds__(256) route_select_wide_kernel(SelectParams p) 
     run += to_fixed(__uint_as_float((uint32_t)(keys[seg0 + j] >> 32)), shift);
     if (seg0 + j < K && fixed_to_f32(run, shift) < threshold) ++below;
   }
-  below = (int)block_sum_i64(below, red64);
+  below = (int)dsa::block_sum_i64(below, red64);
   int count = below + 1;
   count = count < p.cap ? count : p.cap;
 
@@ -282,7 +247,7 @@ __global__ void __launch_bounds__(256) route_select_wide_kernel(SelectParams p) 
     rout[e] = on;
     selected += on;
   }
-  selected = (int)block_sum_i64(selected, red64);
+  selected = (int)dsa::block_sum_i64(selected, red64);
   if (tid == 0) p.counts[row] = selected;
 }
 

@@ -1,5 +1,6 @@
 // Row arithmetic shared by the route kernels (gfx950): exact fixed-point row
-// sums and a one-wave bitonic sort of up to 2048 keys.
+// sums, a one-wave bitonic sort of up to 2048 keys and a workgroup-wide one
+// in LDS for longer rows.
 //
 // A row value m >= 0 is represented as the integer floor(m * 2^(52 + s)), so
 // row and prefix sums are exact and independent of summation order; a sum is
@@ -97,6 +98,53 @@ __device__ __forceinline__ void sort_desc(uint64_t key[kPer], int lane) {
       }
     }
   }
+}
+
+// Reductions over a 256-thread workgroup (four waves); red holds four
+// entries.  Every thread returns the result.
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max_f32(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  lds_barrier();
+  const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  lds_barrier();
+  return r;
+}
+
+__device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* red) {
+  v = wave_sum_i64(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  lds_barrier();
+  const int64_t r = (red[0] + red[1]) + (red[2] + red[3]);
+  lds_barrier();
+  return r;
+}
+
+// Sorts kN (a power of two) keys in LDS into descending order with a bitonic
+// network run by a 256-thread workgroup.  Keys written before the call are
+// covered by its first barrier; the sorted keys are visible to every thread
+// when it returns.
+template <int kN>
+__device__ __forceinline__ void sort_desc_lds(uint64_t* keys) {
+  const int tid = threadIdx.x;
+  for (int size = 2; size <= kN; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      lds_barrier();
+      for (int i = tid; i < kN / 2; i += 256) {
+        const int lo = 2 * stride * (i / stride) + (i % stride);
+        const int hi = lo + stride;
+        const bool descending = (lo & size) == 0;
+        const uint64_t a = keys[lo], b = keys[hi];
+        if ((a < b) == descending) {
+          keys[lo] = b;
+          keys[hi] = a;
+        }
+      }
+    }
+  }
+  lds_barrier();
 }
 
 }  // namespace dsa

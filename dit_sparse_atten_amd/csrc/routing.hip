@@ -313,18 +313,140 @@ __global__ void __launch_bounds__(256) dir_select_kernel(DirParams p) {
   if (lane == 0) p.counts[row] = selected;
 }
 
-unsigned row_groups(int64_t rows) { return (unsigned)((rows + 3) / 4); }
+// Rows of 2049..16384 blocks: one 256-thread workgroup per (head, query
+// block), the arithmetic of dir_select_kernel with element e = tid + 256 j in
+// registers and both sorts over LDS keys.  Keys order by flag, value, then
+// ascending index whatever kN is, so the selection equals the one-wave
+// kernel's.
+constexpr int kWideBlocks = 16384;
 
-constexpr int kMaxBlocks = 2048;  // 64 lanes x 32 keys per selection wave
+template <int kPer>
+__global__ void __launch_bounds__(256) dir_select_wide_kernel(DirParams p) {
+  constexpr int kN = 256 * kPer;
+  __shared__ uint64_t keys[kN];  // 128 KB at 16384 blocks (LDS: 160 KB per CU)
+  __shared__ uint8_t flags[kN];
+  __shared__ int64_t red64[4];
+  __shared__ float red32[4];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;
+  const int K = p.blocks;
+  const int64_t base = (int64_t)row * K;
+
+  float m[kPer];
+  bool prev[kPer], cand[kPer], pool[kPer];
+  int prev_count = 0;
+  float row_max = 0.f;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid + 256 * j;
+    const bool in = e < K;
+    m[j] = in ? p.mass[base + e] : 0.f;
+    prev[j] = in && p.previous[base + e] != 0;
+    cand[j] = in && !prev[j] && p.candidates[base + e] != 0;
+    pool[j] = prev[j] || cand[j];
+    prev_count += prev[j];
+    row_max = fmaxf(row_max, m[j] > 0.f ? m[j] : 0.f);
+    if (in) p.candidates[base + e] = cand[j];
+  }
+  const int shift = dsa::row_shift(dsa::block_max(row_max, red32), K);
+  int64_t fixed_sum = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid + 256 * j;
+    fixed_sum += e < K ? to_fixed(m[j] > 0.f ? m[j] : 0.f, shift) : 0;
+  }
+
+  // The first `count` sorted keys (with the flag bit, if need_flag) as flags
+  // of their elements; out[j] for this thread's elements.
+  auto prefix_flags = [&](int count, bool need_flag, bool out[kPer]) {
+    for (int e = tid; e < kN; e += 256) flags[e] = 0;
+    dsa::lds_barrier();
+    for (int pos = tid; pos < count; pos += 256)
+      if (!need_flag || (keys[pos] >> 63)) flags[key_index<kN>(keys[pos])] = 1;
+    dsa::lds_barrier();
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) out[j] = flags[tid + 256 * j] != 0;
+    dsa::lds_barrier();  // keys and flags are free again
+  };
+
+  if (p.explore > 0) {
+    // Highest-mass blocks outside the pool (pool blocks rank last, by index).
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid + 256 * j;
+      keys[e] = e < K ? order_key<kN>(!pool[j], pool[j] ? 0.f : m[j], e) : 0ull;
+    }
+    dsa::sort_desc_lds<kN>(keys);
+    bool ex[kPer];
+    prefix_flags(p.explore < K ? p.explore : K, false, ex);
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid + 256 * j;
+      if (e < K) {
+        if (p.exploration) p.exploration[base + e] = ex[j];
+        pool[j] = pool[j] || ex[j];
+      }
+    }
+  } else if (p.exploration) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int e = tid + 256 * j;
+      if (e < K) p.exploration[base + e] = 0;
+    }
+  }
+
+  int pool_count = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) pool_count += pool[j];
+  pool_count = (int)dsa::block_sum_i64(pool_count, red64);
+  prev_count = (int)dsa::block_sum_i64(prev_count, red64);
+  fixed_sum = dsa::block_sum_i64(fixed_sum, red64);
+  const float mean = fixed_to_f32(fixed_sum, shift) / (float)K;
+  const float prior = p.persistence * mean;
+  const float bonus = p.bonus * mean;
+  int budget = (int)ceilf((float)prev_count * p.budget_scale);
+  budget = budget < 1 ? 1 : (budget > p.cap ? p.cap : budget);
+  int count = budget < pool_count ? budget : pool_count;
+  count = count < 1 ? 1 : count;
+
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid + 256 * j;
+    float score = m[j];
+    if (prev[j]) score = score + prior;
+    if (p.bonus != 0.f && cand[j]) score = score + bonus;
+    keys[e] = e < K ? order_key<kN>(pool[j], pool[j] ? score : 0.f, e) : 0ull;
+  }
+  dsa::sort_desc_lds<kN>(keys);
+  bool sel[kPer];
+  prefix_flags(count, true, sel);
+
+  int selected = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int e = tid + 256 * j;
+    if (e < K) {
+      const uint8_t on = (sel[j] || e < p.sink) ? 1 : 0;
+      p.route[base + e] = on;
+      selected += on;
+      if (p.dropped) p.dropped[base + e] = prev[j] && !sel[j];
+      if (p.added) p.added[base + e] = sel[j] && !prev[j];
+    }
+  }
+  selected = (int)dsa::block_sum_i64(selected, red64);
+  if (tid == 0) p.counts[row] = selected;
+}
+
+unsigned row_groups(int64_t rows) { return (unsigned)((rows + 3) / 4); }
 
 int check_route_shape(const char* what, int32_t heads, int32_t blocks, const int32_t* nb) {
   if (heads <= 0 || blocks <= 0)
     return dsa::set_error(DSA_EINVAL, "%s: heads and blocks must be positive", what);
-  if (blocks > kMaxBlocks)
+  if (blocks > kWideBlocks)
     return dsa::set_error(DSA_EUNSUPPORTED, "%s: %d blocks (at most %d)", what, blocks,
-                          kMaxBlocks);
+                          kWideBlocks);
   if (!nb) return dsa::set_error(DSA_EINVAL, "%s: neighbors must be given", what);
-  if ((int64_t)heads * blocks * blocks > 0x7fffffffLL)
+  if ((int64_t)heads * blocks > 0x7fffffffLL)
     return dsa::set_error(DSA_EINVAL, "%s: route too large", what);
   return DSA_OK;
 }
@@ -393,13 +515,20 @@ extern "C" int dsa_directional_update(
   const int64_t cells = (int64_t)heads * blocks * blocks;
   hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((cells + 4095) / 4096)), dim3(256), 0,
                      stream, candidates, cells);
-  const unsigned groups = row_groups((int64_t)heads * blocks);
+  const unsigned rows = (unsigned)((int64_t)heads * blocks);
+  const unsigned groups = row_groups(rows);
   hipLaunchKernelGGL(dir_expand_kernel, dim3(groups), dim3(256), 0, stream, p);
   if (blocks <= 512)
     hipLaunchKernelGGL(dir_select_kernel<8>, dim3(groups), dim3(256), 0, stream, p);
   else if (blocks <= 1024)
     hipLaunchKernelGGL(dir_select_kernel<16>, dim3(groups), dim3(256), 0, stream, p);
-  else
+  else if (blocks <= 2048)
     hipLaunchKernelGGL(dir_select_kernel<32>, dim3(groups), dim3(256), 0, stream, p);
+  else if (blocks <= 4096)
+    hipLaunchKernelGGL(dir_select_wide_kernel<16>, dim3(rows), dim3(256), 0, stream, p);
+  else if (blocks <= 8192)
+    hipLaunchKernelGGL(dir_select_wide_kernel<32>, dim3(rows), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(dir_select_wide_kernel<64>, dim3(rows), dim3(256), 0, stream, p);
   return dsa::check_launch("dsa_directional_update");
 }

@@ -44,7 +44,7 @@ using dsa::kKStage;
 using dsa::kRowBytes;
 
 constexpr int kStats = 5;  // mass, q_y, q_x, k_y, k_x
-constexpr int kMaxTiles = 2048;
+constexpr int kMaxTiles = 16384;  // key tiles a row's `listed` bitmap covers (2 KB)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct TileStatsParams {
@@ -101,7 +101,8 @@ __global__ void __launch_bounds__(kWaves * 64, 2) tile_stats_kernel(TileStatsPar
     off_y[i] = i < p.tile ? axis_offset(r, p.tile_h) : 0.f;
     off_x[i] = i < p.tile ? axis_offset(c, p.tile_w) : 0.f;
   }
-  if (tid < kMaxTiles / 32) listed[tid] = 0u;
+  if (kRouted)
+    for (int i = tid; i < kMaxTiles / 32; i += kThreads) listed[i] = 0u;
 
   const int local_row = wave * 32 + qi;
   const int tq = qt * p.tile + local_row;

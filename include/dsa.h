@@ -61,15 +61,19 @@ const char* dsa_last_error(void);
  *                flex.py:655-668, dense.py:40-47).
  *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
  *   workspace: optional device scratch (NULL with workspace_bytes == 0, or
- *                16-byte aligned) for the fp32 partials of the query blocks in
- *                the last, partial round of workgroups (two per CU of the
- *                stream's device), which then run as 2..8 key ranges merged by
- *                a second launch.  The split takes at most workspace_bytes /
- *                66,560 partials (128 x 130 fp32 each) and at most 1,024; with
- *                less room (none: unsplit) the result can differ in the last
- *                bits, since the fp32 accumulation order differs.  Contents
- *                need no initialisation and are dead after the call.  V is read
- *                in place; no transposed copy is made.
+ *                16-byte aligned).  A routed call first takes the launch
+ *                order of its query blocks from it (batch * heads * q_blocks
+ *                int32, rounded up to 256 bytes; only with q_blocks <= 8,192
+ *                and at most 262,144 blocks in all): each (batch, head)'s
+ *                blocks, longest row first.  The rest holds the fp32 partials
+ *                of the query blocks in the last, partial round of workgroups
+ *                (two per CU of the stream's device), which then run as 2..8
+ *                key ranges merged by a second launch: at most rest / 66,560
+ *                partials (128 x 130 fp32 each) and at most 1,024.  With less
+ *                room (none: natural order, unsplit) the result can differ in
+ *                the last bits, since a split row's fp32 accumulation order
+ *                differs.  Contents need no initialisation and are dead after
+ *                the call.  V is read in place; no transposed copy is made.
  * Keys past kv_tokens in a partial last block are masked.
  */
 int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, int32_t dtype,
@@ -78,12 +82,14 @@ int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, int32_t dt
                 const int32_t* col_idx, int32_t route_batches, float scale, int32_t causal,
                 float* lse, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* Workspace bytes that let dsa_bsa_fwd with 128-token blocks split its last
- * round as far as it ever does: 68,157,440 (1,024 partials of 128 x 130
- * fp32) when the key range holds at least 16 blocks (two parts of at least 8
- * key blocks each), else 0 (the call never splits, e.g. over 512 text
- * tokens); 0 for invalid sizes.  No counterpart in the reference, whose
- * FlexAttention allocates internally. */
+/* Workspace bytes that let a self-attention dsa_bsa_fwd with 128-token
+ * blocks order its launch and split its last round as far as it ever does:
+ * the launch order (batch * heads * kv_blocks int32 rounded up to 256, or 0
+ * where the call is not ordered) plus 68,157,440 (1,024 partials of 128 x
+ * 130 fp32) when the key range holds at least 16 blocks (two parts of at
+ * least 8 key blocks each; none otherwise, e.g. over 512 text tokens); 0 for
+ * invalid sizes.  No counterpart in the reference, whose FlexAttention
+ * allocates internally. */
 size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
                                int32_t head_dim);
 
@@ -97,13 +103,14 @@ size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_to
  * that forbid hipMalloc).  No counterpart in the reference.  Same arguments,
  * semantics and results as dsa_bsa_fwd given a workspace of
  * dsa_bsa_workspace_bytes_block() bytes; it calls no hipMalloc / hipFree.  The
- * split partials live in a library-owned device array of 68,157,440 bytes
- * (1,024 partials of 128 x 130 fp32), one per device the library runs on,
- * held until the process ends; the split never needs more, so no call size
- * is refused for want of scratch.  Every call on a device shares that
- * device's array: calls that overlap on one device (on different streams)
- * race; calls ordered on one stream do not.  Nothing in the array needs
- * clearing: a call writes every partial it reads.
+ * launch order and split partials live in a library-owned device array of
+ * 69,206,016 bytes (1 MiB of order, then 1,024 partials of 128 x 130 fp32),
+ * one per device the library runs on, held until the process ends; neither
+ * ever needs more, so no call size is refused for want of scratch.  Every
+ * call on a device shares that device's array: calls that overlap on one
+ * device (on different streams) race; calls ordered on one stream do not.
+ * Nothing in the array needs clearing: a call writes every order entry and
+ * partial it reads.
  */
 int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                         const int64_t* strides, int32_t batch, int32_t q_tokens,
@@ -145,7 +152,7 @@ int dsa_block_mass(const void* q, const void* k, int32_t dtype, const int64_t* s
 /*
  * Spatial-tile attention statistics of one batch-1 self-attention call over
  * tile-major tokens, bf16 or fp16 Q/K (dtype) (tile_h * tile_w <= 128 tokens per tile, tokens a whole
- * number of tiles, at most 2048 tiles).  Replaces the statistics of the
+ * number of tiles, at most 16384 tiles).  Replaces the statistics of the
  * matrix-sparse backend: `_dense_route` (attention_backends/sparse.py:184-233)
  * with row_ptr == col_idx == NULL, `sparse_chunk` (sparse.py:718-750) with the
  * CSR of the tiles each (head, query tile) row attended, and the
@@ -170,7 +177,7 @@ int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const int64_t* s
  * (flex.py:83-94, == sparse.py:171-181 `_row_mask`) and `_add_first_frame_sink`
  * (flex.py:550-566).  mass: [rows, keys] fp32, non-negative; previous: [rows,
  * keys] bytes or NULL (no prior); cap = max(1, ceil(keys * keep)); the first
- * sink_blocks columns are set after the cap.  keys <= 2048.  Outputs route
+ * sink_blocks columns are set after the cap.  keys <= 16384.  Outputs route
  * [rows, keys] bytes and counts [rows] (selected blocks per row, sink included).
  */
 int dsa_route_select(const float* mass, const uint8_t* previous, int32_t rows, int32_t keys,
@@ -182,7 +189,7 @@ int dsa_route_select(const float* mass, const uint8_t* previous, int32_t rows, i
  * neighbour along the query axis (route[h, nb[q][d], k]) or the key axis
  * (route[h, q, nb[k][d]]).  Replaces `frontier_mask`
  * (attention_backends/routing.py:10-41).  route, frontier: [heads, blocks,
- * blocks] bytes; neighbors: [blocks, 4] int32 (-1 = none), blocks <= 2048.
+ * blocks] bytes; neighbors: [blocks, 4] int32 (-1 = none), blocks <= 16384.
  * count (optional, device) receives the number of frontier cells.
  */
 int dsa_frontier_mask(const uint8_t* route, int32_t heads, int32_t blocks,
@@ -196,7 +203,7 @@ int dsa_frontier_mask(const uint8_t* route, int32_t heads, int32_t blocks,
  * first-frame sink that flex.py:544-546 applies to its result.
  *   mass: [heads, blocks, blocks] fp32, non-negative; previous: route bytes;
  *   previous_frontier: bytes or NULL (then the frontier of previous);
- *   neighbors: [blocks, 4] int32, blocks <= 2048; cap = max(1, ceil(blocks *
+ *   neighbors: [blocks, 4] int32, blocks <= 16384; cap = max(1, ceil(blocks *
  *   keep)); explore_count = 0 or max(1, ceil(blocks * exploration_fraction));
  *   expand_flags: 1 query axis, 2 key axis, 4 joint.
  * Outputs (bytes, [heads, blocks, blocks]): route (selection, then the first

@@ -6,6 +6,7 @@ Follows attention_backends/routing.py:
   best_targets               routing.py:53-80  (_sparse_best_targets)
   select_fixed_budget        routing.py:83-89  (_select_fixed_budget)
   directional_budget_update  routing.py:92-168
+  budget_select              its row-local half, routing.py:139-160
 
 Arithmetic shared bit-for-bit with the HIP kernels (the reference's torch
 reductions and unstable argsorts leave these open):
@@ -144,10 +145,35 @@ def directional_budget_update(mass, previous, neighbors, *, keep, persistence=0.
         joint = q_eligible & k_eligible
         candidates[cells[joint, 0], q_targets[joint], k_targets[joint]] = True
     candidates &= ~previous
+    route, exploration = budget_select(
+        mass, previous, candidates, keep=keep, persistence=persistence,
+        candidate_bonus=candidate_bonus, budget_scale=budget_scale,
+        exploration_fraction=exploration_fraction)
+    return {
+        "route": route,
+        "frontier": frontier_mask(route, neighbors),
+        "candidates": candidates,
+        "exploration": exploration,
+        "dropped": previous & ~route,
+        "added": route & ~previous,
+    }
+
+
+def budget_select(mass, previous, candidates, *, keep, persistence=0.5, candidate_bonus=0.0,
+                  budget_scale=1.0, exploration_fraction=0.0):
+    """The row-local half of directional_budget_update (routing.py:139-160):
+    exploration, scores and the fixed-budget selection of every row of
+    [..., K] inputs, given the row's candidates (disjoint from previous).
+    Each row's result depends only on that row and K.  Returns (route,
+    exploration)."""
+    mass = np.asarray(mass, dtype=np.float32)
+    previous = np.asarray(previous, dtype=bool)
+    candidates = np.asarray(candidates, dtype=bool)
+    blocks = mass.shape[-1]
     pool = previous | candidates
     exploration = np.zeros_like(pool)
     if exploration_fraction:
-        explore = max(1, math.ceil(mass.shape[-1] * exploration_fraction))
+        explore = max(1, math.ceil(blocks * exploration_fraction))
         ranks = _rank(np.where(pool, -np.inf, mass.astype(np.float64)))
         exploration = ranks < explore
         pool = pool | exploration
@@ -158,16 +184,8 @@ def directional_budget_update(mass, previous, neighbors, *, keep, persistence=0.
         bonus = (np.float32(candidate_bonus) * mean).astype(np.float32)
         score = (score + (bonus * candidates.astype(np.float32)).astype(np.float32)).astype(
             np.float32)
-    cap = max(1, math.ceil(mass.shape[-1] * keep))
+    cap = max(1, math.ceil(blocks * keep))
     budget = np.ceil((previous.sum(-1).astype(np.float32) * np.float32(budget_scale)).astype(
         np.float32)).astype(np.int64)
     budget = np.clip(budget, 1, cap)
-    route = select_fixed_budget(score, pool, budget)
-    return {
-        "route": route,
-        "frontier": frontier_mask(route, neighbors),
-        "candidates": candidates,
-        "exploration": exploration,
-        "dropped": previous & ~route,
-        "added": route & ~previous,
-    }
+    return select_fixed_budget(score, pool, budget), exploration

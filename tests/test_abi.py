@@ -110,8 +110,15 @@ def test_exact_and_routing_entry_points_validate_first(lib):
     status = lib.dsa_block_mass(fake, fake, 0, strides, 256, 2, 128, 128, fake, 256, -1.0, fake,
                                 None)
     assert status == _lib.DSA_EINVAL and "scale" in _lib.last_error()
-    status = lib.dsa_frontier_mask(fake, 2, 2100, fake, fake, None, None)
-    assert status == _lib.DSA_EUNSUPPORTED and "2048" in _lib.last_error()
+    aligned = ctypes.c_void_p(4096)
+    status = lib.dsa_frontier_mask(fake, 2, 16385, fake, fake, None, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "16384" in _lib.last_error()
+    status = lib.dsa_directional_update(fake, fake, None, fake, 1, 16385, 8, 0.5, 0.0, 0.0, 1.0,
+                                        0, 7, 0, fake, fake, aligned, None, None, None, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "16384" in _lib.last_error()
+    status = lib.dsa_tile_stats(fake, fake, 0, strides, 16385, 1, 128, 1, 1, fake, 16385, None,
+                                None, 0.1, fake, None, None, None, None, None, None)
+    assert status == _lib.DSA_EUNSUPPORTED and "16384" in _lib.last_error()
     status = lib.dsa_frontier_mask(fake, 2, 16, None, fake, None, None)
     assert status == _lib.DSA_EINVAL and "neighbors" in _lib.last_error()
     aligned = ctypes.c_void_p(4096)

@@ -182,6 +182,62 @@ def test_route_select_up_to_2048_tiles(ops, cuda_device):
         np.testing.assert_array_equal(counts.cpu().numpy(), expected.sum(-1))
 
 
+def test_tile_path_beyond_2048_tiles(ops, cuda_device):
+    """2,400 tiles of 2x2 tokens (one head), every step the sparse backend
+    runs past 2,048 tiles: dense and routed statistics (the 2 KB `listed`
+    bitmap), the tile route (a workgroup per row), drop and both expansions,
+    against the oracle."""
+    case, q, k, v = _tile_major_inputs((1, 60, 160), 1, seed=21, tile=4)
+    tiles = q.shape[1] // case.tile
+    assert tiles == 2400
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    _, lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
+    dense = ops.tile_stats(qd, kd, lse, case.tile_shape)
+    torch.cuda.synchronize()
+    expected, _ = _oracle_stats(case, q, k, v)
+    _compare_stats(dense, expected)
+    mask, counts = ops.route_select(dense["mass"], 0.9, 0.625, sink_blocks=80)
+    torch.cuda.synchronize()
+    expected_mask = R.top_mass_route(dense["mass"].cpu().numpy(), 0.9, 0.625)
+    expected_mask[..., :80] = True
+    np.testing.assert_array_equal(mask.cpu().numpy(), expected_mask)
+    np.testing.assert_array_equal(counts.cpu().numpy(), expected_mask.sum(-1))
+
+    route = random_route(1, tiles, seed=3, keep=0.05).numpy()
+    route[..., 0] = True
+    csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=case.tile)
+    out, lse = ops.bsa_fwd(qd, kd, vd, csr, return_lse=True, block_size=case.tile)
+    routed = ops.tile_stats(qd, kd, lse, case.tile_shape, csr=csr)
+    torch.cuda.synchronize()
+    expected, expected_out = _oracle_stats(case, q, k, v, route)
+    _compare_stats(routed, expected)
+    metrics = A.summarize(out.float().cpu().numpy(), expected_out)
+    assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
+    assert (routed["mass"].cpu().numpy()[~route] == 0).all()
+
+    mass16 = routed["mass_f16"].cpu().numpy()
+    dropped, counts = ops.drop_low_mass(torch.from_numpy(route).to(cuda_device),
+                                        routed["mass_f16"], 0.1, sink_tiles=80)
+    torch.cuda.synchronize()
+    expected_drop = S.drop_low_mass(route, mass16, 0.1)
+    expected_drop[..., :80] = True
+    np.testing.assert_array_equal(dropped.cpu().numpy(), expected_drop)
+    np.testing.assert_array_equal(counts.cpu().numpy(), expected_drop.sum(-1))
+
+    state = {"mask": route, "mass": mass16}
+    names = ("q_y", "q_x", "k_y", "k_x")
+    for name in names:
+        state[f"centroid_{name}"] = routed[f"centroid_{name}"].cpu().numpy()
+    grid_tiles = (1, 30, 80)
+    for policy in ("all", "directional"):
+        expanded = ops.expand_route(torch.from_numpy(route).to(cuda_device), grid_tiles, policy,
+                                    mass=routed["mass_f16"],
+                                    centroids=[routed[f"centroid_{n}"] for n in names])
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(expanded.cpu().numpy(),
+                                      S.expand(state, policy, grid_tiles), err_msg=policy)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("heads,tiles,drop", [(4, 16, 0.1), (8, 800, 0.1), (4, 100, 1.5)])
 def test_drop_low_mass_bit_exact(ops, cuda_device, dtype, heads, tiles, drop):

@@ -151,16 +151,18 @@ def test_backend_directional_update_uses_frontier(cuda_device):
         context.reset_runtime_state()
 
 
-@pytest.mark.parametrize("grid", [(21, 45, 80), (62, 45, 80)])
-def test_frontier_and_directional_beyond_512_blocks(ops, cuda_device, grid):
-    """81 frames at 720p (591 blocks) and 244 frames (1,744 blocks): the
-    spatial layout's neighbour table, bit-exact against the oracle."""
+@pytest.mark.parametrize("grid,heads", [((21, 45, 80), 2), ((62, 45, 80), 2),
+                                        ((84, 45, 80), 1)])
+def test_frontier_and_directional_beyond_512_blocks(ops, cuda_device, grid, heads):
+    """81 frames at 720p (591 blocks), 244 frames (1,744 blocks) and 333
+    frames (2,363 blocks: a workgroup per row): the spatial layout's neighbour
+    table, bit-exact against the oracle."""
     from dit_sparse_atten_amd.attention_backends.spatial import build_spatial_layout
     layout = build_spatial_layout(grid, 128, 32)
     nb = layout.neighbors_cpu.numpy()
     blocks = nb.shape[0]
-    mass = route_mass(2, blocks, seed=blocks).numpy()
-    previous = random_route(2, blocks, seed=blocks + 1, keep=0.5).numpy()
+    mass = route_mass(heads, blocks, seed=blocks).numpy()
+    previous = random_route(heads, blocks, seed=blocks + 1, keep=0.5).numpy()
     frontier = ops.frontier_mask(_dev(previous, cuda_device), _dev(nb, cuda_device))
     kwargs = dict(keep=0.625, persistence=0.5, min_ratio=0.25, candidate_bonus=0.5,
                   budget_scale=1.1, exploration_fraction=0.01)
@@ -173,3 +175,38 @@ def test_frontier_and_directional_beyond_512_blocks(ops, cuda_device, grid):
     route[..., :29] = True
     np.testing.assert_array_equal(result["route"].cpu().numpy(), route)
     np.testing.assert_array_equal(result["counts"].cpu().numpy(), route.sum(-1))
+
+
+@pytest.mark.parametrize("blocks", [4219, 16384])
+def test_directional_rows_up_to_16384_blocks(ops, cuda_device, blocks):
+    """Rows of 4,219 and 16,384 (the maximum) blocks.  Without neighbours
+    there are no candidates and every row is independent, so sampled rows are
+    checked bit-exact against the oracle's row-local selection, which the
+    oracle tests show equal to the full update's rows."""
+    generator = torch.Generator(device=cuda_device).manual_seed(blocks)
+    mass = torch.rand(1, blocks, blocks, device=cuda_device, generator=generator) ** 4
+    previous = torch.rand(1, blocks, blocks, device=cuda_device, generator=generator) < 0.3
+    nb = torch.full((blocks, 4), -1, dtype=torch.int32, device=cuda_device)
+    # A budget below the pool, and a prior small enough that explored blocks
+    # compete with previous ones.
+    kwargs = dict(keep=0.4, persistence=0.05, candidate_bonus=0.5, budget_scale=0.9,
+                  exploration_fraction=0.01)
+    result = ops.directional_update(mass, previous, nb, sink_blocks=29, **kwargs)
+    torch.cuda.synchronize()
+    rows = torch.tensor(sorted({0, 1, blocks // 2, blocks - 1,
+                                *torch.randint(0, blocks, (28,), generator=torch.Generator()
+                                               .manual_seed(1)).tolist()}))
+    m = mass[0, rows.to(cuda_device)].cpu().numpy()
+    prev = previous[0, rows.to(cuda_device)].cpu().numpy()
+    route, exploration = G.budget_select(m, prev, np.zeros_like(prev), **kwargs)
+    sunk = route.copy()
+    sunk[:, :29] = True
+    got = {name: result[name][0, rows.to(cuda_device)].cpu().numpy()
+           for name in ("route", "exploration", "candidates", "dropped", "added")}
+    np.testing.assert_array_equal(got["route"], sunk)
+    np.testing.assert_array_equal(got["exploration"], exploration)
+    assert not got["candidates"].any()
+    np.testing.assert_array_equal(got["dropped"], prev & ~route)
+    np.testing.assert_array_equal(got["added"], route & ~prev)
+    np.testing.assert_array_equal(result["counts"][0, rows.to(cuda_device)].cpu().numpy(),
+                                  sunk.sum(-1))

@@ -149,3 +149,22 @@ def test_planted_mistakes_fail():
                                           previous_frontier=frontier, **kwargs)
     golden_route = _unpack(data["default__route"], mass.shape)
     assert not np.array_equal(flipped["route"], golden_route)
+
+
+def test_budget_select_is_row_local():
+    """Without neighbours there are no candidates, so the full update's rows
+    equal budget_select applied to any subset of rows on its own."""
+    rng = np.random.default_rng(5)
+    heads, blocks = 2, 40
+    mass = (rng.random((heads, blocks, blocks)) ** 4).astype(np.float32)
+    previous = rng.random((heads, blocks, blocks)) < 0.3
+    neighbors = np.full((blocks, 4), -1)
+    kwargs = dict(keep=0.4, persistence=0.5, candidate_bonus=0.5, budget_scale=1.1,
+                  exploration_fraction=0.05)
+    full = G.directional_budget_update(mass, previous, neighbors, **kwargs)
+    assert not full["candidates"].any()
+    rows = [0, 7, 39]
+    route, exploration = G.budget_select(mass[1, rows], previous[1, rows],
+                                         np.zeros((3, blocks), bool), **kwargs)
+    np.testing.assert_array_equal(route, full["route"][1, rows])
+    np.testing.assert_array_equal(exploration, full["exploration"][1, rows])
