@@ -21,6 +21,7 @@ Prints one JSON line (rank 0).  Effective TFLOP/s counts kept blocks only:
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -40,6 +41,10 @@ TOKENS, HEADS, HEAD_DIM, BLOCK = 57600, 40, 128, 128
 GRID = (16, 45, 80)
 KEEP = 0.625
 TRAFFIC_FILE = ROOT / "profiles" / "bsa_fwd_config2_traffic.json"
+# The sources of the config-2 kernel: a counter file taken on other sources
+# does not describe this build.
+KERNEL_SOURCES = ("dit_sparse_atten_amd/csrc/bsa_kernel.h", "dit_sparse_atten_amd/csrc/bsa_fwd.hip",
+                  "dit_sparse_atten_amd/csrc/bsa_tiles.h", "dit_sparse_atten_amd/csrc/dsa_common.h")
 
 
 def parse_args():
@@ -61,6 +66,27 @@ def parse_args():
                         help="run only a plain device copy of this many MiB (scales the "
                              "FETCH_SIZE / WRITE_SIZE counters) and exit")
     return parser.parse_args()
+
+
+def kernel_sources_sha16():
+    digest = hashlib.sha256()
+    for relative in KERNEL_SOURCES:
+        digest.update((ROOT / relative).read_bytes())
+    return digest.hexdigest()[:16]
+
+
+def measured_traffic():
+    """(bytes per config-2 launch, note): L2 fills from the memory fabric
+    (FETCH_SIZE) plus L2 write-backs (WRITE_SIZE), each copy-calibrated, from
+    the committed rocprofv3 counter runs, or None when those runs predate the
+    kernel's current sources.  FETCH_SIZE includes fills served by the MALL,
+    so this bounds the HBM bytes from above."""
+    if not TRAFFIC_FILE.exists():
+        return None, "no counter file"
+    data = json.loads(TRAFFIC_FILE.read_text())
+    if data.get("sources_sha16") != kernel_sources_sha16():
+        return None, "counter runs predate these kernel sources"
+    return data.get("fabric_bytes_per_launch"), str(TRAFFIC_FILE.relative_to(ROOT))
 
 
 def copy_calibration(mib):
@@ -516,23 +542,23 @@ def main():
         "wall_seconds_timed_region": round(wall, 4),
     }
     achieved = flops / (kernel_ms * 1e-3) / 1e12
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    traffic, traffic_source = measured_traffic()
     result["roofline"] = {
         "bound": "mfma",
-        "kernel": ("bsa_fwd_kernel<true, 2, false, false, 4> (event window also holds "
-                   "vt_transpose_kernel and the split-tail bsa_merge_kernel)"),
+        "kernel": ("bsa_fwd_kernel<__bf16, true, 2, false, false, 4> (the event window also "
+                   "holds launch_order_kernel and the split-tail bsa_merge_kernel)"),
         "achieved": round(achieved, 2),
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
         "traffic": traffic,
+        "traffic_source": traffic_source,
         "launch_ms_mean": round(kernel_ms, 4),
         "launch_ms_median": round(sorted(per_call)[len(per_call) // 2], 4),
     }
     if traffic:
-        result["roofline"]["hbm_gbs_at_traffic"] = round(traffic / (kernel_ms * 1e-3) / 1e9, 1)
+        # L2 <-> memory-fabric rate (MALL hits included), not an HBM rate.
+        result["roofline"]["l2_fabric_gbs"] = round(traffic / (kernel_ms * 1e-3) / 1e9, 1)
     if not args.only_sparse:
         # What the matrix cores sustain on this box for random bf16 data under
         # its power limit: the vendor GEMM (hipBLASLt through torch.mm), 16384^3.
