@@ -99,12 +99,28 @@ def _gpu_metrics(actual, expected):
             "cosine_similarity": float(torch.dot(a, e) / (a.norm() * e.norm()))}
 
 
+def _chunked_fp32_attention(qh, kh, vh, rows=2048):
+    """softmax(q k^T / sqrt(d)) v in float32 over [B, H, T, D] inputs, in
+    query-row chunks (contiguous operands throughout)."""
+    out = torch.empty(qh.shape, dtype=torch.float32, device=qh.device)
+    scale = qh.shape[-1] ** -0.5
+    for b in range(qh.shape[0]):
+        for h in range(qh.shape[1]):
+            kt = kh[b, h].float().t().contiguous()
+            vf = vh[b, h].float().contiguous()
+            for start in range(0, qh.shape[2], rows):
+                qs = qh[b, h, start:start + rows].float().contiguous()
+                out[b, h, start:start + rows] = torch.softmax(qs @ kt * scale, dim=-1) @ vf
+    return out
+
+
 def test_config1_dense_rope_against_sdpa_and_fp32(cuda_device):
     """the dense path at the Wan2.1-1.3B shape, B=2 (CFG
     pair), 12 heads, grid 21x30x52 = 32,760 tokens, Q/K with 3D RoPE, handed
     over as [B,T,H,D] views of BHSD storage.  Every row is compared with
-    PyTorch SDPA (flash or memory-efficient kernel, never the math path), and
-    sampled rows with a float32 matmul reference."""
+    PyTorch SDPA (flash or memory-efficient kernel, never the math path) or,
+    where neither runs, a chunked float32 reference (the one used is
+    printed), and sampled rows with a float32 matmul reference."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
 
     from dit_sparse_atten_amd.attention_backends.dense import DenseBackend
@@ -117,19 +133,24 @@ def test_config1_dense_rope_against_sdpa_and_fp32(cuda_device):
     torch.cuda.synchronize()
     assert out.shape == (2, 32760, 12, 128) and out.dtype == torch.bfloat16
 
-    sdpa = None
+    reference, ran = None, None
     for backend in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
         try:
             with sdpa_kernel([backend]):
-                sdpa = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh)
+                reference = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh)
+            ran = backend.name
             break
         except RuntimeError:
             continue
-    if sdpa is not None:
-        torch.cuda.synchronize()
-        metrics = _gpu_metrics(out, sdpa.transpose(1, 2))
-        assert metrics["max_absolute_error"] <= MAX_ABS, metrics
-        assert metrics["cosine_similarity"] >= MIN_COSINE, metrics
+    if reference is None:
+        # Neither fused SDPA kernel runs on this build: every row against a
+        # float32 reference in row chunks instead, never skipped.
+        reference, ran = _chunked_fp32_attention(qh, kh, vh), "float32 chunked"
+    print(f"config-1 every-row reference: {ran}", flush=True)
+    torch.cuda.synchronize()
+    metrics = _gpu_metrics(out, reference.transpose(1, 2))
+    assert metrics["max_absolute_error"] <= MAX_ABS, (ran, metrics)
+    assert metrics["cosine_similarity"] >= MIN_COSINE, (ran, metrics)
 
     generator = torch.Generator().manual_seed(2)
     rows = torch.randint(0, 32760, (256,), generator=generator).to(cuda_device)
