@@ -314,6 +314,17 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         sacc[kt] = E::mfma32(a, qf[dc], sacc[kt]);
       }
     }
+    if constexpr (NKT == 2) {
+      // Keep four K reads in flight ahead of the MFMA chain (the default
+      // schedule issues two, and each MFMA then waits on LDS latency).
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
     if constexpr (kGather) {
       if (invalid != 0) {
         const uint64_t mine = invalid >> (4 * g);
@@ -382,6 +393,16 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         const x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         oacc[dt] = E::mfma32(a, pf[j], oacc[dt]);
       }
+    }
+    if constexpr (kGather && NKT == 2) {
+      // Gathered stream: V^T reads two per MFMA, four ahead.
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+      for (int i = 0; i < 14; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     }
   };
 
