@@ -40,7 +40,7 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int,    # batch, q_tokens, kv_tokens, heads, head_dim
         _c_int,                                    # block_size
         _c_ptr, _c_ptr, _c_int,                    # row_ptr, col_idx, route_batches
-        _c_float, _c_int, _c_ptr,                  # scale, causal, lse
+        _c_float, _c_int, _c_int, _c_ptr,          # scale, causal, deterministic, lse
         _c_ptr, _c_size, _c_ptr,                   # workspace, workspace_bytes, stream
     )),
     "dsa_bsa_fwd_noalloc": (_c_int, (
@@ -49,7 +49,7 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int, _c_int,    # batch, q_tokens, kv_tokens, heads, head_dim
         _c_int,                                    # block_size
         _c_ptr, _c_ptr, _c_int,                    # row_ptr, col_idx, route_batches
-        _c_float, _c_int, _c_ptr, _c_ptr,          # scale, causal, lse, stream
+        _c_float, _c_int, _c_int, _c_ptr, _c_ptr,  # scale, causal, deterministic, lse, stream
     )),
     "dsa_bsa_workspace_bytes": (_c_size, (_c_int, _c_int, _c_int, _c_int)),
     "dsa_bsa_workspace_bytes_block": (_c_size, (_c_int, _c_int, _c_int, _c_int, _c_int)),

@@ -128,14 +128,17 @@ def _build_block_mask(route, tokens, block_size, counts=None):
     return ops.route_to_csr(route, counts, block_size=block_size)
 
 
-def _flex_output(q, k, v, block_mask, block_size, compile_kernel=True, scale=None):
+def _flex_output(q, k, v, block_mask, block_size, compile_kernel=True, scale=None,
+                 deterministic=False):
     """Block-sparse attention of [B, T, H, D] tensors over a CSR route.
 
     Partial last blocks are masked inside the kernel, so no padding copies are
-    made; the output is contiguous [B, T, H, D].
+    made; the output is contiguous [B, T, H, D].  ``deterministic`` (the
+    backend call's own flag) asks for results reproducible bit for bit.
     """
     del compile_kernel
-    return ops.bsa_fwd(q, k, v, block_mask, scale=scale, block_size=block_size)
+    return ops.bsa_fwd(q, k, v, block_mask, scale=scale, block_size=block_size,
+                       deterministic=deterministic)
 
 
 def _route_keep(block_mask):
@@ -517,7 +520,7 @@ class FlexReuseBackend:
                 return finish(dense_output())
 
         output = _flex_output(q, k, v, state["block_mask"], self.config.block_size,
-                              scale=softmax_scale)
+                              scale=softmax_scale, deterministic=deterministic)
         self.phase_counts["sparse_reuse"] += 1
         if self.config.prefetch_sampled_update and sampled_update_due:
             state["block_mask"] = None

@@ -181,7 +181,7 @@ class MatrixSparseBackend:
             centroid_threshold=self.config.centroid_threshold,
             huge_factor=self.config.huge_factor)
 
-    def _sparse_attention(self, q, k, v, scale, layout):
+    def _sparse_attention(self, q, k, v, scale, layout, deterministic=False):
         c = self.config
         # The reference computes in the input dtype; so do the kernels, for
         # bfloat16 and float16 (float32 raises ValueError, as in every
@@ -228,14 +228,15 @@ class MatrixSparseBackend:
         collect = c.policy != "reuse"
         if collect:
             output, lse = ops.bsa_fwd(q, k, v, csr, scale=scale, return_lse=True,
-                                      block_size=layout.tile_tokens)
+                                      block_size=layout.tile_tokens, deterministic=deterministic)
             stats = ops.tile_stats(q, k, lse, tile_shape, csr=csr, scale=scale)
             next_mask, _ = ops.drop_low_mass(route, stats["mass"], c.drop_factor, sink)
             next_state = {"mass": stats["mass_f16"]}
             for name in ("q_y", "q_x", "k_y", "k_x"):
                 next_state[f"centroid_{name}"] = stats[f"centroid_{name}"]
         else:
-            output = ops.bsa_fwd(q, k, v, csr, scale=scale, block_size=layout.tile_tokens)
+            output = ops.bsa_fwd(q, k, v, csr, scale=scale, block_size=layout.tile_tokens,
+                                 deterministic=deterministic)
             # Reuse drops against the stored (fp16) route mass and keeps it.
             next_mask, _ = ops.drop_low_mass(route, previous["mass"], c.drop_factor, sink)
             next_state = {name: previous[name] for name in (
@@ -283,7 +284,8 @@ class MatrixSparseBackend:
                 return self.dense(q, k, v, softmax_scale=softmax_scale, **kwargs)
             layout = self._layout(grid, q.shape[1])
             if layout is not None:
-                return self._sparse_attention(q, k, v, softmax_scale, layout)
+                return self._sparse_attention(q, k, v, softmax_scale, layout,
+                                              bool(kwargs.get("deterministic", False)))
         return self.dense(q, k, v, softmax_scale=softmax_scale, **kwargs)
 
 

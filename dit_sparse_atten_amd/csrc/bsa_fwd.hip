@@ -19,7 +19,7 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
             int32_t batch, int32_t q_tokens, int32_t kv_tokens, int32_t heads,
             int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
             const int32_t* col_idx, int32_t route_batches, float scale, int32_t causal,
-            float* lse, const char* who, BsaParams* p) {
+            int32_t deterministic, float* lse, const char* who, BsaParams* p) {
   if (!q || !k || !v || !o || !strides)
     return dsa::set_error(DSA_EINVAL, "%s: null tensor or stride pointer", who);
   if (dtype != DSA_BF16 && dtype != DSA_F16)
@@ -31,6 +31,8 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                           "%s: head_dim %d unsupported (a multiple of 8 up to 128)", who, head_dim);
   if (causal != 0 && causal != 1)
     return dsa::set_error(DSA_EINVAL, "%s: causal must be 0 or 1", who);
+  if (deterministic != 0 && deterministic != 1)
+    return dsa::set_error(DSA_EINVAL, "%s: deterministic must be 0 or 1", who);
   if (causal && row_ptr)
     return dsa::set_error(DSA_EUNSUPPORTED, "%s: causal attention takes no block route", who);
   if (block_size <= 0 || block_size > 128)
@@ -77,6 +79,7 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
   p->block_pad = (block_size + 7) & ~7;
   p->head_dim = head_dim;
   p->causal = causal;
+  p->deterministic = deterministic;
   p->scale = scale;
   p->scale_log2 = scale * 1.4426950408889634f;
   return DSA_OK;
@@ -93,11 +96,12 @@ int launch(int32_t dtype, BsaParams p, void* scratch, size_t scratch_bytes, hipS
 }  // namespace
 
 // Scratch of dsa_bsa_fwd_noalloc: the launch order of up to kMaxOrderItems
-// work items (1 MiB), then kMaxPartGroups split partials (68,157,440 bytes).
+// work items (1 MiB) and the aligned-walk table (4 KiB), then kMaxPartGroups
+// split partials (68,157,440 bytes).
 // Every device the library runs on holds its own copy until the process
 // ends; host code reaches it only through the address hipGetSymbolAddress
 // returns on that device (scratch_on).
-constexpr size_t kScratchBytes = (size_t)kMaxOrderItems * sizeof(int32_t) +
+constexpr size_t kScratchBytes = (size_t)kMaxOrderItems * sizeof(int32_t) + kWalkBytes +
                                  (size_t)kMaxPartGroups * kPartBytes;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
@@ -152,13 +156,13 @@ extern "C" int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o,
                            int32_t kv_tokens, int32_t heads, int32_t head_dim,
                            int32_t block_size, const int32_t* row_ptr,
                            const int32_t* col_idx, int32_t route_batches, float scale,
-                           int32_t causal, float* lse, void* workspace, size_t workspace_bytes,
-                           hipStream_t stream) {
+                           int32_t causal, int32_t deterministic, float* lse, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
   dsa::clear_error();
   BsaParams p;
   const int status = prepare(q, k, v, o, dtype, strides, batch, q_tokens, kv_tokens, heads, head_dim,
-                             block_size, row_ptr, col_idx, route_batches, scale, causal, lse,
-                             "dsa_bsa_fwd", &p);
+                             block_size, row_ptr, col_idx, route_batches, scale, causal,
+                             deterministic, lse, "dsa_bsa_fwd", &p);
   if (status != DSA_OK) return status;
   if (workspace_bytes > 0 && (!workspace || !aligned16(workspace)))
     return dsa::set_error(DSA_EINVAL, "dsa_bsa_fwd: workspace must be 16-byte aligned");
@@ -170,12 +174,13 @@ extern "C" int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, 
                                    int32_t kv_tokens, int32_t heads, int32_t head_dim,
                                    int32_t block_size, const int32_t* row_ptr,
                                    const int32_t* col_idx, int32_t route_batches, float scale,
-                                   int32_t causal, float* lse, hipStream_t stream) {
+                                   int32_t causal, int32_t deterministic, float* lse,
+                                   hipStream_t stream) {
   dsa::clear_error();
   BsaParams p;
   const int status = prepare(q, k, v, o, dtype, strides, batch, q_tokens, kv_tokens, heads, head_dim,
-                             block_size, row_ptr, col_idx, route_batches, scale, causal, lse,
-                             "dsa_bsa_fwd_noalloc", &p);
+                             block_size, row_ptr, col_idx, route_batches, scale, causal,
+                             deterministic, lse, "dsa_bsa_fwd_noalloc", &p);
   if (status != DSA_OK) return status;
   const int device = stream_device(stream);
   if (device < 0)

@@ -37,7 +37,10 @@
 //    as one gathered key sequence (kGather), and routed blocks of at most 64
 //    tokens run 2-wave workgroups (kWaves);
 //  * the last, partial round of query blocks may run as 2..8 key ranges each
-//    (choose_split), whose fp32 partials bsa_merge_kernel combines.
+//    (choose_split), whose fp32 partials bsa_merge_kernel combines;
+//  * routed calls may walk each row's key blocks from a rotated start (the
+//    aligned walk, walk_start): the workgroups resident on one XCD then read
+//    the same key blocks at about the same time, from its L2.
 #pragma once
 
 #include <algorithm>
@@ -60,10 +63,12 @@ struct BsaParams {
   const int32_t* row_ptr;  // null: every key block (dense)
   const int32_t* col_idx;
   const int32_t* order;    // routed: work item of each launch slot (null: identity)
+  uint64_t* walk;          // routed: aligned-walk position table (null: plain walk)
   int32_t batch, heads, q_tokens, kv_tokens, q_blocks, kv_blocks, route_batches;
   int32_t block;     // tokens per query block and per key block (1..128)
   int32_t head_dim;  // 8..128, a multiple of 8; dims past it are zero in the stages
   int32_t causal;    // dense only: query t attends keys k <= t
+  int32_t deterministic;  // host side: 1 = plain walk (results reproducible bit for bit)
   int32_t block_pad; // gathered stream: key slots per block (block rounded up to 8)
   float scale;       // softmax scale applied to <q, k>
   float scale_log2;  // scale * log2(e)
@@ -106,6 +111,68 @@ __device__ __forceinline__ typename dsa::Elem<T>::x4 lds_read_tr(const unsigned 
   const dsa_i16x4 raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) dsa_i16x4*)(lds));
   return __builtin_bit_cast(typename dsa::Elem<T>::x4, raw);
+}
+
+// Aligned key walk.  The accumulation order of a row's key blocks does not
+// change its result beyond fp32 rounding, so a routed workgroup may start its
+// walk anywhere in its row and wrap around.  Workgroups that each walk their
+// own route from the first key block drift apart within a few rows (their
+// rows differ in length and their clocks in speed), and an XCD's resident
+// workgroups then read key blocks spread over most of a head, far more than
+// its 4 MB L2 holds.  With a walk table, every workgroup publishes (time,
+// batch-head, key block) in its XCD's row of the table once per key block,
+// and a starting workgroup starts at the first of its key blocks at or past
+// the circular mean of the fresh positions of the same batch-head, so the
+// XCD's workgroups of one head move as a pack.  The start then depends on
+// timing: results can differ in the last bits from run to run, which is why
+// a deterministic call passes no table.
+constexpr int kWalkSlots = 64;                             // entries per XCD
+constexpr size_t kWalkBytes = (size_t)dsa::kNumXcd * kWalkSlots * sizeof(uint64_t);
+constexpr uint32_t kWalkFreshTicks = 100;                  // 16 us in 0.16 us ticks
+constexpr int kWalkMaxBlocks = 65535;                      // key blocks a position encodes
+
+// XCD of the calling wave (HW_REG_XCC_ID, bits 3:0).
+__device__ __forceinline__ int xcc_id() {
+  return (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & (dsa::kNumXcd - 1));
+}
+
+// The 100 MHz real-time counter in 0.16 us ticks, truncated to 32 bits.
+__device__ __forceinline__ uint32_t walk_now() {
+  return (uint32_t)(__builtin_amdgcn_s_memrealtime() >> 4);
+}
+
+__device__ __forceinline__ uint64_t walk_entry(int bh, int kb) {
+  return ((uint64_t)walk_now() << 32) | ((uint64_t)(bh & 0xffff) << 16) | (uint64_t)kb;
+}
+
+// Index into the row's key list at which a workgroup of batch-head bh starts
+// (one full wave calls it; every lane gets the result): 0 without fresh
+// entries, else the first entry at or past the entries' circular mean key
+// block (the list is ascending; for any other order the start is still a
+// valid rotation).
+__device__ __forceinline__ int walk_start(const uint64_t* tab, int lane, int bh, int kv_blocks,
+                                          dsa::const_i32 cidx, int start, int nblk) {
+  const uint64_t e = __hip_atomic_load(tab + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool fresh = e != 0 && (int)((e >> 16) & 0xffff) == (bh & 0xffff) &&
+                     walk_now() - (uint32_t)(e >> 32) < kWalkFreshTicks;
+  const float turn = 6.2831853f / (float)kv_blocks;
+  const float angle = fresh ? (float)(int)(e & 0xffff) * turn : 0.f;
+  const float c = dsa::wave_total(fresh ? __cosf(angle) : 0.f);
+  const float sn = dsa::wave_total(fresh ? __sinf(angle) : 0.f);
+  if (c * c + sn * sn < 1e-6f) return 0;
+  float mean = atan2f(sn, c);
+  if (mean < 0.f) mean += 6.2831853f;
+  const int pos = min(kv_blocks - 1, max(0, (int)(mean / turn)));
+  // 64 evenly spaced probes bracket the answer; a second probe of the
+  // bracketing segment (at most 64 entries up to 4,096 blocks) finds it.
+  const int below = (int)__popcll(__ballot(cidx[start + (int)(((int64_t)lane * nblk) >> 6)] < pos));
+  const int lo = below == 0 ? 0 : (int)(((int64_t)(below - 1) * nblk) >> 6);
+  const int hi = below == 64 ? nblk : (int)(((int64_t)below * nblk) >> 6);
+  if (hi - lo > 64) return lo < nblk ? lo : 0;
+  const int i = lo + lane;
+  const int in_seg = (int)__popcll(__ballot(i < hi && cidx[start + i] < pos));
+  const int r = lo + in_seg;
+  return r < nblk ? r : 0;
 }
 
 // kRouted: key blocks from the CSR row (false: every key block, dense).
@@ -182,6 +249,26 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   const dsa_const_i32 cidx = (dsa_const_i32)p.col_idx;
   const int nblk = end - start;
 
+  // Aligned walk (split workgroups keep their plain key range): wave 0 picks
+  // the start, the others read it from LDS; thread 0 publishes positions.
+  int rot = 0;
+  uint64_t* walk_at = nullptr;
+  if (kRouted && !split && p.walk != nullptr) {
+    uint64_t* const tab = p.walk + xcc_id() * kWalkSlots;
+    if (nblk > 1) {
+      __shared__ int rot_lds;
+      if (wave == 0) {
+        const int r = walk_start(tab, lane, bh, p.kv_blocks, cidx, start, nblk);
+        if (lane == 0) rot_lds = r;
+      }
+      __syncthreads();
+      rot = __builtin_amdgcn_readfirstlane(rot_lds);
+    }
+    if (tid == 0) walk_at = tab + (wg / dsa::kNumXcd) % kWalkSlots;
+  }
+  // List index of the j-th key block walked.
+  auto walked = [&](int j) -> int { return start + (j + rot < nblk ? j + rot : j + rot - nblk); };
+
   // Rows past the block (blocks shorter than 128) or the sequence are
   // computed on a clamped row and never stored; waves wholly past the block
   // only stage their share of K/V.
@@ -228,8 +315,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   }
 
   auto block_of = [&](int j) -> int {
-    const int it = start + j;
-    const int kb = kRouted ? cidx[it] : it;
+    const int kb = kRouted ? cidx[walked(j)] : start + j;
     return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
   };
 
@@ -415,6 +501,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     if (next_kb != -2) issue(next_kb, next_half, kn, vn);
+    if (walk_at != nullptr && half == 0 && kb >= 0)
+      __hip_atomic_store(walk_at, walk_entry(bh, kb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (wave_active) {
       const int valid = valid_of(kb, half);
       // Causal (dense): keys past this lane's query row are masked.
@@ -436,6 +524,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     __syncthreads();
     if (next_kb0 != -2)
       issue_gather(next_kb0 < 0 ? 0 : next_kb0, next_kb1 < 0 ? 0 : next_kb1, next_o0, kn, vn);
+    if (walk_at != nullptr && kb0 >= 0)
+      __hip_atomic_store(walk_at, walk_entry(bh, kb0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (wave_active) {
       const int second = p.block_pad - o0;  // first slot of block kb1
       uint64_t invalid = 0;
@@ -461,7 +551,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     // Stream block j: CSR entry j clamped to the row (slots past the row's
     // last key are masked), -1 when out of range.
     auto gblock = [&](int j) -> int {
-      const int kb = cidx[start + (j < nblk ? j : nblk - 1)];
+      const int kb = cidx[walked(j < nblk ? j : nblk - 1)];
       return (unsigned)kb < (unsigned)p.kv_blocks ? kb : -1;
     };
     const int bp = p.block_pad;
@@ -598,11 +688,12 @@ static __global__ void __launch_bounds__(256) launch_order_kernel(const int32_t*
     order[base + i] = base + (int32_t)~(uint32_t)keys[i];
 }
 
-// Bytes of the launch order of a routed call of `items` work items (0 when
-// the call is not ordered), rounded up to 256.
+// Bytes of the launch order of a routed call of `items` work items, rounded
+// up to 256, plus the aligned-walk table after it (0 when the call is not
+// ordered).
 inline size_t order_bytes(int64_t items, int32_t q_blocks) {
   if (items > kMaxOrderItems || q_blocks > kMaxOrderBlocks) return 0;
-  return ((size_t)items * sizeof(int32_t) + 255) & ~(size_t)255;
+  return (((size_t)items * sizeof(int32_t) + 255) & ~(size_t)255) + kWalkBytes;
 }
 
 // Combines the `parts` partials of each split query block: with M the largest
@@ -749,12 +840,18 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
   const int64_t grid = (int64_t)p.batch * p.heads * p.q_blocks;
   size_t used = 0;
   p.order = nullptr;
+  p.walk = nullptr;
   if (p.row_ptr) {
     const size_t need = order_bytes(grid, p.q_blocks);
     if (need > 0 && scratch_bytes >= need) {
       int32_t* order = static_cast<int32_t*>(scratch);
       p.order = order;
       used = need;
+      // The walk table needs no clearing: stale entries are too old to count
+      // and any entry only moves where a row's walk starts.
+      if (!p.deterministic && p.kv_blocks <= kWalkMaxBlocks)
+        p.walk = reinterpret_cast<uint64_t*>(static_cast<unsigned char*>(scratch) + need -
+                                             kWalkBytes);
       int n = 2;
       while (n < p.q_blocks) n <<= 1;
       hipLaunchKernelGGL(launch_order_kernel, dim3((unsigned)(p.batch * p.heads)), dim3(256), 0,

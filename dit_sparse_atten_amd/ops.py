@@ -111,7 +111,7 @@ def csr_from_route(route, block_size=128):
 
 
 def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_size=128,
-            causal=False):
+            causal=False, deterministic=False):
     """Block-sparse (or, with ``csr=None``, dense) attention forward on the GPU.
 
     ``block_size`` (1..128) is the number of consecutive tokens per query
@@ -121,7 +121,11 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     q: [B,Tq,H,D], k/v: [B,Tk,H,D], D a multiple of 8 up to 128, all bf16 or
     all fp16 (the compute type), on a HIP device, any strides with a
     contiguous head dim.  ``causal`` (dense calls only): query t attends keys
-    k <= t, as SDPA's is_causal.  Returns O [B,Tq,H,D] in that type
+    k <= t, as SDPA's is_causal.  ``deterministic``: results reproducible bit
+    for bit; otherwise a routed call may start each row's key walk where the
+    other rows of its head are reading (better L2 reuse), which changes the
+    fp32 accumulation order and so the last bits from run to run.  Returns
+    O [B,Tq,H,D] in that type
     (contiguous unless ``out`` is given) and, with ``return_lse``, the
     natural-log LSE [B,H,Tq] fp32.
     """
@@ -182,7 +186,7 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
             batch, q_tokens, kv_tokens, heads, head_dim, block_size,
             row_ptr.data_ptr() if row_ptr is not None else None,
             col_idx.data_ptr() if col_idx is not None else None,
-            route_batches, float(scale), int(bool(causal)),
+            route_batches, float(scale), int(bool(causal)), int(bool(deterministic)),
             lse.data_ptr() if lse is not None else None,
             workspace.data_ptr() if workspace is not None else None, workspace_bytes,
             _stream_handle(q.device))

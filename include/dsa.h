@@ -59,12 +59,20 @@ const char* dsa_last_error(void);
  *                aligned when q_tokens != kv_tokens); dense calls only (the
  *                reference sends causal calls to its dense backend,
  *                flex.py:655-668, dense.py:40-47).
+ *   deterministic: 1 for results reproducible bit for bit from run to run;
+ *                0 lets a routed call that has the launch order (below) and
+ *                at most 65,535 key blocks start each row's key walk where
+ *                the workgroups resident on its XCD are reading (an aligned
+ *                walk, for L2 reuse), so its fp32 accumulation order, and the
+ *                last bits of O and LSE, depend on timing.  Dense calls are
+ *                always reproducible.
  *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
  *   workspace: optional device scratch (NULL with workspace_bytes == 0, or
  *                16-byte aligned).  A routed call first takes the launch
  *                order of its query blocks from it (batch * heads * q_blocks
- *                int32, rounded up to 256 bytes; only with q_blocks <= 8,192
- *                and at most 262,144 blocks in all): each (batch, head)'s
+ *                int32, rounded up to 256 bytes, then 4,096 bytes of
+ *                aligned-walk positions; only with q_blocks <= 8,192 and at
+ *                most 262,144 blocks in all): each (batch, head)'s
  *                blocks, longest row first.  The rest holds the fp32 partials
  *                of the query blocks in the last, partial round of workgroups
  *                (two per CU of the stream's device), which then run as 2..8
@@ -80,15 +88,16 @@ int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, int32_t dt
                 const int64_t* strides, int32_t batch, int32_t q_tokens, int32_t kv_tokens,
                 int32_t heads, int32_t head_dim, int32_t block_size, const int32_t* row_ptr,
                 const int32_t* col_idx, int32_t route_batches, float scale, int32_t causal,
-                float* lse, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                int32_t deterministic, float* lse, void* workspace, size_t workspace_bytes,
+                hipStream_t stream);
 
 /* Workspace bytes that let a self-attention dsa_bsa_fwd with 128-token
  * blocks order its launch and split its last round as far as it ever does:
- * the launch order (batch * heads * kv_blocks int32 rounded up to 256, or 0
- * where the call is not ordered) plus 68,157,440 (1,024 partials of 128 x
- * 130 fp32) when the key range holds at least 16 blocks (two parts of at
- * least 8 key blocks each; none otherwise, e.g. over 512 text tokens); 0 for
- * invalid sizes.  No counterpart in the reference, whose FlexAttention
+ * the launch order (batch * heads * kv_blocks int32 rounded up to 256, plus
+ * 4,096 bytes of aligned-walk positions, or 0 where the call is not ordered)
+ * plus 68,157,440 (1,024 partials of 128 x 130 fp32) when the key range holds
+ * at least 16 blocks (two parts of at least 8 key blocks each; none
+ * otherwise, e.g. over 512 text tokens); 0 for invalid sizes.  No counterpart in the reference, whose FlexAttention
  * allocates internally. */
 size_t dsa_bsa_workspace_bytes(int32_t batch, int32_t heads, int32_t kv_tokens,
                                int32_t head_dim);
@@ -103,20 +112,22 @@ size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_to
  * that forbid hipMalloc).  No counterpart in the reference.  Same arguments,
  * semantics and results as dsa_bsa_fwd given a workspace of
  * dsa_bsa_workspace_bytes_block() bytes; it calls no hipMalloc / hipFree.  The
- * launch order and split partials live in a library-owned device array of
- * 69,206,016 bytes (1 MiB of order, then 1,024 partials of 128 x 130 fp32),
- * one per device the library runs on, held until the process ends; neither
- * ever needs more, so no call size is refused for want of scratch.  Every
- * call on a device shares that device's array: calls that overlap on one
- * device (on different streams) race; calls ordered on one stream do not.
- * Nothing in the array needs clearing: a call writes every order entry and
- * partial it reads.
+ * launch order, the aligned-walk positions and the split partials live in a
+ * library-owned device array of 69,210,112 bytes (1 MiB of order, 4 KiB of
+ * positions, then 1,024 partials of 128 x 130 fp32), one per device the
+ * library runs on, held until the process ends; no call ever needs more, so
+ * no call size is refused for want of scratch.  Every call on a device
+ * shares that device's array: calls that overlap on one device (on
+ * different streams) race; calls ordered on one stream do not.  Nothing in
+ * the array needs clearing: a call writes every order entry and partial it
+ * reads, and a stale walk position only moves where a row's walk starts.
  */
 int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                         const int64_t* strides, int32_t batch, int32_t q_tokens,
                         int32_t kv_tokens, int32_t heads, int32_t head_dim, int32_t block_size,
                         const int32_t* row_ptr, const int32_t* col_idx, int32_t route_batches,
-                        float scale, int32_t causal, float* lse, hipStream_t stream);
+                        float scale, int32_t causal, int32_t deterministic, float* lse,
+                        hipStream_t stream);
 
 /*
  * Sampled block-mass estimate for one batch-1 self-attention call, bf16 or

@@ -38,12 +38,13 @@ def test_header_symbols_are_exported_and_bound(lib):
 def test_version_and_workspace_size(lib):
     assert lib.dsa_version() == 1
     # The workspace holds the launch order of a routed call (4 bytes per
-    # (batch, head, query block) work item, rounded up to 256), then the split
+    # (batch, head, query block) work item, rounded up to 256) and the
+    # aligned-walk table (8 XCDs x 64 entries of 8 bytes), then the split
     # partials of the last round, 1,024 workgroups of 128 x (128 + 2) fp32,
     # when the key range can be split (at least 16 key blocks, 2 parts of 8).
     # V is read in place.
     def order(items):
-        return (items * 4 + 255) // 256 * 256
+        return (items * 4 + 255) // 256 * 256 + 8 * 64 * 8
 
     split = 1024 * (128 * 128 + 256) * 4
     assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == order(2 * 12 * 256) + split
@@ -62,21 +63,21 @@ def test_version_and_workspace_size(lib):
 def test_invalid_arguments_are_reported_before_any_launch(lib):
     strides = _lib.int64_array([8] * 12)
     status = lib.dsa_bsa_fwd(None, None, None, None, 0, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, 0, None, None, 0, None)
+                             None, None, 1, 0.1, 0, 0, None, None, 0, None)
     assert status == _lib.DSA_EINVAL
     assert "null" in _lib.last_error()
     with pytest.raises(ValueError, match="null"):
         _lib.check(status, "dsa_bsa_fwd")
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 136, 128,
-                             None, None, 1, 0.1, 0, None, fake, 1 << 20, None)
+                             None, None, 1, 0.1, 0, 0, None, fake, 1 << 20, None)
     assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
     misaligned = ctypes.c_void_p(24)
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, 0, None, misaligned, 1 << 20, None)
+                             None, None, 1, 0.1, 0, 0, None, misaligned, 1 << 20, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, 0, None, None, 1 << 20, None)
+                             None, None, 1, 0.1, 0, 0, None, None, 1 << 20, None)
     assert status == _lib.DSA_EINVAL and "workspace" in _lib.last_error()
     status = lib.dsa_route_select(fake, None, 4, 16385, 0.5, 0.95, 1, 0, fake, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "16384" in _lib.last_error()
@@ -87,14 +88,17 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
                                   16, 0.1, fake, None)
     assert status == _lib.DSA_EUNSUPPORTED and "dtype" in _lib.last_error()
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 7, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, 0, None, None, 0, None)
+                             None, None, 1, 0.1, 0, 0, None, None, 0, None)
     assert status == _lib.DSA_EUNSUPPORTED and "dtype" in _lib.last_error()
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
-                             fake, fake, 1, 0.1, 1, None, None, 0, None)
+                             fake, fake, 1, 0.1, 1, 0, None, None, 0, None)
     assert status == _lib.DSA_EUNSUPPORTED and "causal" in _lib.last_error()
     status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
-                             None, None, 1, 0.1, 2, None, None, 0, None)
+                             None, None, 1, 0.1, 2, 0, None, None, 0, None)
     assert status == _lib.DSA_EINVAL and "causal" in _lib.last_error()
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 128, 128,
+                             fake, fake, 1, 0.1, 0, 2, None, None, 0, None)
+    assert status == _lib.DSA_EINVAL and "deterministic" in _lib.last_error()
     status = lib.dsa_permute_rows(4, None, None, None, None, None, 1, 1, 1, 16, None)
     assert status == _lib.DSA_EINVAL
 

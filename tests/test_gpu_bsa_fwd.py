@@ -321,3 +321,30 @@ def test_dense_result_independent_of_block(cuda_device, block):
     out = bsa_fwd(qd, kd, vd, block_size=block)
     torch.cuda.synchronize()
     _check(out, q, k, v, None)
+
+
+@pytest.mark.parametrize("block, tokens, heads", [(128, 32768, 8), (72, 72 * 400, 6),
+                                                  (64, 64 * 512, 4)])
+def test_aligned_walk_and_deterministic_calls(cuda_device, block, tokens, heads):
+    """Routed calls over several rounds of workgroups (so later rows start
+    from the walk table's positions): deterministic calls repeat bit for bit;
+    default calls (aligned walk) match them to fp32 accumulation-order noise
+    and the closed form on sampled rows.  Covers the plain 128-token stream,
+    the gathered 72-token stream and 2-wave 64-token workgroups."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    q, k, v = _inputs(1, tokens, heads, seed=block)
+    blocks = tokens // block
+    generator = torch.Generator().manual_seed(block)
+    route = torch.rand(heads, blocks, blocks, generator=generator) < 0.6
+    route[..., 0] = True
+    csr = csr_from_route(route.to(cuda_device), block_size=block)
+    qd, kd, vd = (t.to(cuda_device) for t in (q, k, v))
+    first = bsa_fwd(qd, kd, vd, csr, block_size=block, deterministic=True, return_lse=True)
+    again = bsa_fwd(qd, kd, vd, csr, block_size=block, deterministic=True, return_lse=True)
+    aligned = bsa_fwd(qd, kd, vd, csr, block_size=block, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
+    assert (aligned[0].float() - first[0].float()).abs().max().item() <= 8e-3
+    np.testing.assert_allclose(aligned[1].cpu().numpy(), first[1].cpu().numpy(), atol=1e-4)
+    rows = [(0, h, qb) for h in range(heads) for qb in (0, 1, blocks // 2, blocks - 1)]
+    _check(aligned[0], q, k, v, route, block=block, rows=rows)

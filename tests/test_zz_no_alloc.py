@@ -1,6 +1,7 @@
 """dsa_bsa_fwd_noalloc (no workspace argument, library-owned split scratch)
 against dsa_bsa_fwd with its workspace, through the C-ABI: two calls in a row
-on one stream, the second smaller, both with a split last round."""
+on one stream, the second smaller, both with a split last round, each both
+deterministic (bit for bit) and with the aligned walk (oracle tolerance)."""
 
 import math
 
@@ -47,29 +48,33 @@ def test_noalloc_matches_workspace_entry_point(cuda_device):
         bytes_ = lib.dsa_bsa_workspace_bytes(1, heads, tokens, 128)
         assert bytes_ > 0
         workspace = torch.empty(bytes_, dtype=torch.uint8, device=cuda_device)
-        args = (strides, 1, tokens, tokens, heads, 128, 128, csr.row_ptr.data_ptr(),
-                csr.col_idx.data_ptr(), 1, 128 ** -0.5, 0)
-        _lib.check(lib.dsa_bsa_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), want.data_ptr(),
-                                   0, *args, want_lse.data_ptr(), workspace.data_ptr(), bytes_,
-                                   stream), "dsa_bsa_fwd")
-        _lib.check(lib.dsa_bsa_fwd_noalloc(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
-                                           got.data_ptr(), 0, *args, got_lse.data_ptr(), stream),
-                   "dsa_bsa_fwd_noalloc")
-        torch.cuda.synchronize()
-        # Same kernels, same split plan: identical bits.
-        assert torch.equal(got, want), (tokens, heads)
-        assert torch.equal(got_lse, want_lse), (tokens, heads)
         expected, expected_lse = block_sparse_attention(
             q.float().numpy(), k.float().numpy(), v.float().numpy(), route.numpy(), 128)
-        metrics = summarize(got.float().cpu().numpy(), expected)
-        assert metrics["max_absolute_error"] <= 2e-2, metrics
-        assert metrics["cosine_similarity"] >= 0.9995, metrics
-        np.testing.assert_allclose(got_lse.cpu().numpy(), expected_lse, atol=1e-3, rtol=1e-4)
+        # deterministic = 1: same kernels, same split plan, identical bits;
+        # deterministic = 0 (aligned walk): the oracle's tolerance.
+        for deterministic in (1, 0):
+            args = (strides, 1, tokens, tokens, heads, 128, 128, csr.row_ptr.data_ptr(),
+                    csr.col_idx.data_ptr(), 1, 128 ** -0.5, 0, deterministic)
+            _lib.check(lib.dsa_bsa_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                       want.data_ptr(), 0, *args, want_lse.data_ptr(),
+                                       workspace.data_ptr(), bytes_, stream), "dsa_bsa_fwd")
+            _lib.check(lib.dsa_bsa_fwd_noalloc(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                               got.data_ptr(), 0, *args, got_lse.data_ptr(),
+                                               stream), "dsa_bsa_fwd_noalloc")
+            torch.cuda.synchronize()
+            if deterministic:
+                assert torch.equal(got, want), (tokens, heads)
+                assert torch.equal(got_lse, want_lse), (tokens, heads)
+            for out, lse in ((got, got_lse), (want, want_lse)):
+                metrics = summarize(out.float().cpu().numpy(), expected)
+                assert metrics["max_absolute_error"] <= 2e-2, (deterministic, metrics)
+                assert metrics["cosine_similarity"] >= 0.9995, (deterministic, metrics)
+                np.testing.assert_allclose(lse.cpu().numpy(), expected_lse, atol=1e-3, rtol=1e-4)
 
 
 def test_noalloc_validates_before_launch(cuda_device):
     from dit_sparse_atten_amd import _lib
     lib = _lib.load()
     status = lib.dsa_bsa_fwd_noalloc(None, None, None, None, 0, _lib.int64_array([8] * 12), 1, 128,
-                                     128, 1, 128, 128, None, None, 1, 0.1, 0, None, None)
+                                     128, 1, 128, 128, None, None, 1, 0.1, 0, 0, None, None)
     assert status == _lib.DSA_EINVAL and "null" in _lib.last_error()
