@@ -707,11 +707,25 @@ def main():
         def tile_attention():
             ops.bsa_fwd(qt, kt, vt, tile_csr, out=tile_out, block_size=tile)
 
+        tile_shape = (tile_layout.tile_h, tile_layout.tile_w)
+
+        def tile_fused():
+            return ops.bsa_fwd_tile_stats(qt, kt, vt, tile_csr, tile_shape)
+
         def tile_step_directional():
+            # sparse_chunk: attention and its statistics in one call, then the drop.
+            _, _, tstats = tile_fused()
+            ops.drop_low_mass(tile_route, tstats["mass"], 0.1, tile_sink)
+
+        tile_lse = {}
+
+        def tile_stats_pass():
+            ops.tile_stats(qt, kt, tile_lse["lse"], tile_shape, csr=tile_csr)
+
+        def tile_step_two_pass():
             _, tlse = ops.bsa_fwd(qt, kt, vt, tile_csr, out=tile_out, return_lse=True,
                                   block_size=tile)
-            tstats = ops.tile_stats(qt, kt, tlse, (tile_layout.tile_h, tile_layout.tile_w),
-                                    csr=tile_csr)
+            tstats = ops.tile_stats(qt, kt, tlse, tile_shape, csr=tile_csr)
             ops.drop_low_mass(tile_route, tstats["mass"], 0.1, tile_sink)
 
         def tile_bootstrap():
@@ -721,9 +735,14 @@ def main():
 
         tile_attention()
         tile_step_directional()
+        _, tile_lse["lse"] = ops.bsa_fwd(qt, kt, vt, tile_csr, return_lse=True, block_size=tile)
+        tile_step_two_pass()
         torch.cuda.synchronize()
         tile_ms, _ = timer.time(tile_attention, 5)
+        tile_fused_ms, _ = timer.time(tile_fused, 3)
         tile_step_ms, _ = timer.time(tile_step_directional, 3)
+        tile_stats_ms, _ = timer.time(tile_stats_pass, 3)
+        tile_two_pass_ms, _ = timer.time(tile_step_two_pass, 3)
         tile_boot_ms, _ = timer.time(tile_bootstrap, 2)
         tile_flops = 4.0 * HEAD_DIM * tile * tile * tile_nnz
         result["matrix_sparse"] = {
@@ -732,7 +751,11 @@ def main():
             "realized_keep": round(tile_nnz / (HEADS * tiles * tiles), 6),
             "attention_ms": round(tile_ms, 4),
             "attention_eff_tflops": round(tile_flops / (tile_ms * 1e-3) / 1e12, 2),
+            "fused_attention_and_stats_ms": round(tile_fused_ms, 4),
+            "fused_stats_extra_ms": round(tile_fused_ms - tile_ms, 4),
             "directional_step_ms": round(tile_step_ms, 4),
+            "two_pass_stats_pass_ms": round(tile_stats_ms, 4),
+            "directional_step_two_pass_ms": round(tile_two_pass_ms, 4),
             "bootstrap_ms": round(tile_boot_ms, 4),
             "reference_pytorch_sparse_ms": 8396.6, "reference_triton_sparse_ms": 4038.5,
             "reference_source": ("results/sparse_attention_profile.json (57,600 tokens, "

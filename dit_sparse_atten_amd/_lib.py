@@ -73,6 +73,18 @@ SIGNATURES = {
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # mass, mass_f16, centroids q_y q_x k_y k_x
         _c_ptr,                                    # stream
     )),
+    "dsa_bsa_fwd_tile_stats": (_c_int, (
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,  # q, k, v, o, dtype
+        ctypes.POINTER(_c_i64),                    # strides[12]
+        _c_int, _c_int, _c_int, _c_int, _c_int,    # tokens, heads, head_dim, tile_h, tile_w
+        _c_ptr, _c_ptr, _c_i64,                    # row_ptr, col_idx, entries
+        _c_float, _c_int, _c_ptr,                  # scale, deterministic, lse
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,  # mass, mass_f16, centroids q_y q_x k_y k_x
+        _c_ptr, _c_size, _c_ptr,                   # workspace, workspace_bytes, stream
+    )),
+    "dsa_bsa_fwd_tile_stats_workspace_bytes": (_c_size, (
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,  # heads, tokens, head_dim, tile_h, tile_w, entries
+    )),
     "dsa_route_select": (_c_int, (
         _c_ptr, _c_ptr, _c_int, _c_int,            # mass, previous, rows, keys
         _c_float, _c_float, _c_int, _c_int,        # rho, target, cap, sink_blocks

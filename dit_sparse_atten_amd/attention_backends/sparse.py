@@ -227,9 +227,10 @@ class MatrixSparseBackend:
         csr = ops.route_to_csr(route, block_size=layout.tile_tokens)
         collect = c.policy != "reuse"
         if collect:
-            output, lse = ops.bsa_fwd(q, k, v, csr, scale=scale, return_lse=True,
-                                      block_size=layout.tile_tokens, deterministic=deterministic)
-            stats = ops.tile_stats(q, k, lse, tile_shape, csr=csr, scale=scale)
+            # Attention and the statistics of the same softmax in one call
+            # (sparse_chunk, sparse.py:670-751).
+            output, _, stats = ops.bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=scale,
+                                                      deterministic=deterministic)
             next_mask, _ = ops.drop_low_mass(route, stats["mass"], c.drop_factor, sink)
             next_state = {"mass": stats["mass_f16"]}
             for name in ("q_y", "q_x", "k_y", "k_x"):

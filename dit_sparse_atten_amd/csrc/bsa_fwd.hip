@@ -6,6 +6,7 @@
 // (attention_backends/flex.py:379-399 `_flex_output`, kernel options
 // flex.py:360-364) and its dense SDPA fallback (attention_backends/dense.py:14-48).
 #include <cmath>
+#include <hip/hip_fp16.h>
 #include <mutex>
 
 #include "bsa_kernel.h"
@@ -80,6 +81,10 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
   p->head_dim = head_dim;
   p->causal = causal;
   p->deterministic = deterministic;
+  p->rs_logm = nullptr;
+  p->rs_mean = nullptr;
+  p->rs_entries = 0;
+  p->tile_h = p->tile_w = 0;
   p->scale = scale;
   p->scale_log2 = scale * 1.4426950408889634f;
   return DSA_OK;
@@ -131,6 +136,100 @@ int scratch_on(int device, void** out, const char* who) {
   *out = g_scratch[device];
   return DSA_OK;
 }
+
+}  // namespace
+
+namespace {
+
+// Cells of the fused statistics: one workgroup per (head, query tile) row.
+// For each key tile the row lists, query row r of the tile contributes
+// w_r = 2^(rs_logm - lse_r log2 e), its probability mass on that key tile:
+//   mass = sum w_r, q_y = sum w_r y(r), q_x = sum w_r x(r),
+//   k_y = sum w_r mean_y, k_x = sum w_r mean_x,
+// each summed in a fixed order (one wave per listed tile, a fixed-shape wave
+// reduction).  Outputs as dsa_tile_stats writes them: mass / tokens (fp32,
+// fp16) and the centroids moment / max(mass, 1e-12) (fp16); cells the row
+// does not list are zero.
+struct ReduceParams {
+  const float* rs_logm;
+  const uint32_t* rs_mean;
+  int64_t entries;
+  const float* lse;  // [heads, tokens]
+  const int32_t* row_ptr;
+  const int32_t* col_idx;
+  float* mass32;
+  __half* mass16;
+  __half* cqy;
+  __half* cqx;
+  __half* cky;
+  __half* ckx;
+  int32_t tokens, tiles, tile, tile_h, tile_w;
+};
+
+__global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) {
+  __shared__ float lse2[128], uy[128], ux[128];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row = blockIdx.x;
+  const int h = row / p.tiles, qt = row % p.tiles;
+  for (int i = tid; i < p.tile; i += 256) {
+    lse2[i] = p.lse[(int64_t)h * p.tokens + (int64_t)qt * p.tile + i] * 1.4426950408889634f;
+    uy[i] = dsa::tile_axis(i / p.tile_w, p.tile_h);
+    ux[i] = dsa::tile_axis(i % p.tile_w, p.tile_w);
+  }
+  const int64_t cell0 = (int64_t)row * p.tiles;
+  const __half zero = __float2half(0.f);
+  for (int kt = tid; kt < p.tiles; kt += 256) {
+    p.mass32[cell0 + kt] = 0.f;
+    if (p.mass16) p.mass16[cell0 + kt] = zero;
+    if (p.cqy) p.cqy[cell0 + kt] = zero;
+    if (p.cqx) p.cqx[cell0 + kt] = zero;
+    if (p.cky) p.cky[cell0 + kt] = zero;
+    if (p.ckx) p.ckx[cell0 + kt] = zero;
+  }
+  // The zeros land before the listed cells are written (vmcnt(0) barrier).
+  dsa::lds_barrier<true>();
+  const int start = p.row_ptr[row];
+  const int end = (int)min((int64_t)p.row_ptr[row + 1], p.entries);
+  for (int e = start + wave; e < end; e += 4) {
+    const int kt = p.col_idx[e];
+    if ((unsigned)kt >= (unsigned)p.tiles) continue;
+    float m = 0.f, qy = 0.f, qx = 0.f, ky = 0.f, kx = 0.f;
+    for (int r = lane; r < p.tile; r += 64) {
+      const int64_t at = (int64_t)e * p.tile + r;
+      const float w = __builtin_amdgcn_exp2f(p.rs_logm[at] - lse2[r]);
+      const dsa_f16x2 mean = __builtin_bit_cast(dsa_f16x2, p.rs_mean[at]);
+      m += w;
+      qy = fmaf(w, uy[r], qy);
+      qx = fmaf(w, ux[r], qx);
+      ky = fmaf(w, (float)mean[0], ky);
+      kx = fmaf(w, (float)mean[1], kx);
+    }
+    m = dsa::wave_total(m);
+    qy = dsa::wave_total(qy);
+    qx = dsa::wave_total(qx);
+    ky = dsa::wave_total(ky);
+    kx = dsa::wave_total(kx);
+    if (lane == 0) {
+      const int64_t cell = cell0 + kt;
+      const float normalized = m / (float)p.tokens;
+      const float den = fmaxf(m, 1e-12f);
+      p.mass32[cell] = normalized;
+      if (p.mass16) p.mass16[cell] = __float2half(normalized);
+      if (p.cqy) p.cqy[cell] = __float2half(qy / den);
+      if (p.cqx) p.cqx[cell] = __float2half(qx / den);
+      if (p.cky) p.cky[cell] = __float2half(ky / den);
+      if (p.ckx) p.ckx[cell] = __float2half(kx / den);
+    }
+  }
+}
+
+// Bytes of the fused per-row statistics of `entries` CSR entries of `tile`
+// query rows (fp32 log-mass and two fp16 means each), rounded up to 256.
+size_t row_stats_bytes(int64_t entries, int32_t tile) {
+  return ((size_t)entries * tile * 2 * sizeof(float) + 255) & ~(size_t)255;
+}
+
 
 }  // namespace
 
@@ -192,4 +291,92 @@ extern "C" int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, 
   // order, as dsa_bsa_fwd does; the split never takes more partials than the
   // array holds.  So no call size needs more scratch than this.
   return launch(dtype, p, area, kScratchBytes, stream, "dsa_bsa_fwd_noalloc");
+}
+
+extern "C" size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t tokens,
+                                                         int32_t head_dim, int32_t tile_h,
+                                                         int32_t tile_w, int64_t entries) {
+  if (heads <= 0 || tokens <= 0 || head_dim <= 0 || tile_h <= 0 || tile_w <= 0 || entries < 0)
+    return 0;
+  if ((int64_t)tile_h * tile_w > 128) return 0;
+  const int32_t tile = tile_h * tile_w;
+  if (tokens % tile != 0) return 0;
+  const size_t attention = dsa_bsa_workspace_bytes_block(1, heads, tokens, head_dim, tile);
+  // Tiles that take the gathered key stream also hold the per-row statistics.
+  return attention + (gather_blocks(tile, tokens) ? row_stats_bytes(entries, tile) : 0);
+}
+
+extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* v, void* o,
+                                      int32_t dtype, const int64_t* strides, int32_t tokens,
+                                      int32_t heads, int32_t head_dim, int32_t tile_h,
+                                      int32_t tile_w, const int32_t* row_ptr,
+                                      const int32_t* col_idx, int64_t entries, float scale,
+                                      int32_t deterministic, float* lse, float* mass,
+                                      void* mass_f16, void* centroid_q_y, void* centroid_q_x,
+                                      void* centroid_k_y, void* centroid_k_x, void* workspace,
+                                      size_t workspace_bytes, hipStream_t stream) {
+  const char* who = "dsa_bsa_fwd_tile_stats";
+  dsa::clear_error();
+  if (!row_ptr || !col_idx || !lse || !mass || !strides)
+    return dsa::set_error(DSA_EINVAL, "%s: row_ptr, col_idx, lse, mass and strides are required",
+                          who);
+  if (tile_h <= 0 || tile_w <= 0 || (int64_t)tile_h * tile_w > 128)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: tile %dx%d unsupported (1..128 tokens)", who,
+                          tile_h, tile_w);
+  const int32_t tile = tile_h * tile_w;
+  if (tokens <= 0 || tokens % tile != 0)
+    return dsa::set_error(DSA_EINVAL, "%s: %d tokens are not whole %d-token tiles", who, tokens,
+                          tile);
+  if (entries < 0) return dsa::set_error(DSA_EINVAL, "%s: entries must be >= 0", who);
+  BsaParams p;
+  int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim, tile,
+                       row_ptr, col_idx, 1, scale, 0, deterministic, lse, who, &p);
+  if (status != DSA_OK) return status;
+  if (workspace_bytes > 0 && (!workspace || !aligned16(workspace)))
+    return dsa::set_error(DSA_EINVAL, "%s: workspace must be 16-byte aligned", who);
+  const size_t need = dsa_bsa_fwd_tile_stats_workspace_bytes(heads, tokens, head_dim, tile_h,
+                                                             tile_w, entries);
+  if (workspace_bytes < need)
+    return dsa::set_error(DSA_EINVAL, "%s: workspace of %zu bytes, %zu needed", who,
+                          workspace_bytes, need);
+  const size_t rs = gather_blocks(tile, tokens) ? row_stats_bytes(entries, tile) : 0;
+  if (!use_gather(tile, tokens, strides[4], strides[7])) {
+    // Tiles outside the gathered stream: the attention, then a second pass.
+    status = launch(dtype, p, static_cast<unsigned char*>(workspace) + rs, workspace_bytes - rs,
+                    stream, who);
+    if (status != DSA_OK) return status;
+    const int64_t stat_strides[4] = {strides[1], strides[2], strides[4], strides[5]};
+    return dsa_tile_stats(q, k, dtype, stat_strides, tokens, heads, head_dim, tile_h, tile_w, lse,
+                          tokens, row_ptr, col_idx, scale, mass, mass_f16, centroid_q_y,
+                          centroid_q_x, centroid_k_y, centroid_k_x, stream);
+  }
+  unsigned char* base = static_cast<unsigned char*>(workspace);
+  p.rs_logm = reinterpret_cast<float*>(base);
+  p.rs_mean = reinterpret_cast<uint32_t*>(base + (size_t)entries * tile * sizeof(float));
+  p.rs_entries = entries;
+  p.tile_h = tile_h;
+  p.tile_w = tile_w;
+  status = launch(dtype, p, base + rs, workspace_bytes - rs, stream, who);
+  if (status != DSA_OK) return status;
+  ReduceParams r;
+  r.rs_logm = p.rs_logm;
+  r.rs_mean = p.rs_mean;
+  r.entries = entries;
+  r.lse = lse;
+  r.row_ptr = row_ptr;
+  r.col_idx = col_idx;
+  r.mass32 = mass;
+  r.mass16 = static_cast<__half*>(mass_f16);
+  r.cqy = static_cast<__half*>(centroid_q_y);
+  r.cqx = static_cast<__half*>(centroid_q_x);
+  r.cky = static_cast<__half*>(centroid_k_y);
+  r.ckx = static_cast<__half*>(centroid_k_x);
+  r.tokens = tokens;
+  r.tiles = tokens / tile;
+  r.tile = tile;
+  r.tile_h = tile_h;
+  r.tile_w = tile_w;
+  hipLaunchKernelGGL(tile_stats_reduce_kernel, dim3((unsigned)(heads * r.tiles)), dim3(256), 0,
+                     stream, r);
+  return dsa::check_launch(who);
 }

@@ -78,6 +78,15 @@ struct BsaParams {
   int32_t split_from;
   int32_t parts;
   float* part;
+  // Fused tile statistics (the kStats instances): for CSR entry e (a kept key
+  // tile) and query row r of its row's query tile, at e * block + r,
+  // rs_logm = log2 of the row's unnormalised probability mass on that key
+  // tile, sum 2^(scale_log2 s), and rs_mean = its mass-weighted mean key
+  // offsets (y, x) as two fp16.  Entries at or past rs_entries are not written.
+  float* rs_logm;
+  uint32_t* rs_mean;
+  int64_t rs_entries;
+  int32_t tile_h, tile_w;  // the tile shape, tile_h * tile_w = block
 };
 
 // One split partial: O [128 rows][128 dims] relative to the row's reference
@@ -188,15 +197,34 @@ __device__ __forceinline__ int walk_start(const uint64_t* tab, int lane, int bh,
 // kWaves: waves per workgroup, 32 query rows each (4; 2 for routed blocks of
 // at most 64 tokens, whose rows two waves cover: smaller workgroups spread
 // over the four SIMDs instead of leaving two waves per workgroup idle).
-template <typename T, bool kRouted, int kNh, bool kSkip, bool kGather = false, int kWaves = 4>
+//
+// kStats (gathered stream only): the workgroup also writes the per-row tile
+// statistics (rs_logm, rs_mean) from the probabilities of its own softmax.
+// The key-side sums run on the matrix cores beside O^T = V^T P^T: with the
+// same P^T operand, C += W^T P^T where W^T (kStatRows x keys, an LDS table)
+// holds, for the key tiles of each parity (stream tile index mod 2), the
+// rows 1, y_hi, x_hi, y_lo, x_lo of each key's tile-local offsets split into
+// an input-type high part and the remainder.  The rows sit at C rows 0-3, 8
+// (even tiles) and 4-7, 12 (odd tiles), so each lane's accumulators 0..4
+// are its query row's five sums for the key tiles of its own half's parity.
+// Tiles span two chunks at most (65..127 keys against 64-key chunks) and two
+// tiles of one parity never share a chunk, so each lane carries the five sums
+// of one open tile across chunks and closes it in the chunk where it ends.
+constexpr int kStatRows = 11;    // 2 parities x 5 kinds, then a zero row
+constexpr int kStatCols = 392;   // >= 2 * 120 + 64 positions; = 8 mod 128 spreads the rows' banks
+
+template <typename T, bool kRouted, int kNh, bool kSkip, bool kGather = false, int kWaves = 4,
+          bool kStats = false>
 __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     bsa_fwd_kernel(BsaParams p) {
   typedef dsa::Elem<T> E;
   typedef typename E::x8 x8;
+  static_assert(!kStats || (kRouted && kGather), "fused statistics: gathered stream only");
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v1[kKStage];
+  __shared__ __attribute__((aligned(16))) T wtab[kStats ? kStatRows * kStatCols : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -366,6 +394,35 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     return min(valid, p.kv_tokens - key0);
   };
 
+  // Statistics weights: stream position pos (mod 2 block_pad) is tile-local
+  // offset off of a tile of parity par; pad slots weigh 0.  Within each
+  // 16-position group the positions are stored in the order 0-3, 8-11, 4-7,
+  // 12-15, so the eight keys a lane half supplies (P^T slot order) are one
+  // 16-byte read.
+  const T* wrow = wtab;
+  float carry[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  if constexpr (kStats) {
+    const int bp = p.block_pad;
+    for (int i = tid; i < kStatRows * kStatCols; i += kWaves * 64) {
+      const int r = i / kStatCols, si = i % kStatCols;
+      const int pos = (si & ~12) | ((si & 4) << 1) | ((si & 8) >> 1);
+      const int q2 = pos % (2 * bp);
+      const int par = q2 / bp, off = q2 % bp;
+      float w = 0.f;
+      if (r < 10 && r / 5 == par && off < p.block) {
+        const float y = dsa::tile_axis(off / p.tile_w, p.tile_h);
+        const float x = dsa::tile_axis(off % p.tile_w, p.tile_w);
+        const float yh = (float)(T)y, xh = (float)(T)x;
+        const int kind = r % 5;
+        w = kind == 0 ? 1.f : kind == 1 ? yh : kind == 2 ? xh : kind == 3 ? y - yh : x - xh;
+      }
+      wtab[i] = (T)w;
+    }
+    dsa::lds_barrier();
+    // C row of lane qi's A row: 0-3 and 8 even kinds, 4-7 and 12 odd, else zero.
+    wrow = wtab + (qi < 4 ? qi : qi < 8 ? qi + 1 : qi == 8 ? 4 : qi == 12 ? 9 : 10) * kStatCols;
+  }
+
   float m_run = -INFINITY;
   float l_run = 0.f;
   dsa_f32x16 oacc[4];
@@ -383,7 +440,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // lim: causal bound of this lane's row, keys at or past `lim` in the
   // half-tile are masked (at least 64 when nothing is).
   auto compute = [&](const unsigned char* kt_lds, const unsigned char* v_lds, int valid,
-                     int lim, uint64_t invalid, auto nkt_c) __attribute__((always_inline)) {
+                     int lim, uint64_t invalid, int wbase, auto nkt_c)
+      __attribute__((always_inline)) {
     constexpr int NKT = decltype(nkt_c)::value;
     dsa_f32x16 sacc[NKT];
 #pragma unroll
@@ -446,6 +504,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+      if constexpr (kStats) {
+#pragma unroll
+        for (int i = 0; i < 5; ++i) carry[i] *= alpha;
+      }
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     x8 pf[2 * NKT];
@@ -490,6 +552,19 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     }
+    if constexpr (kStats) {
+      // The key-side sums of this chunk (weights from stream position wbase).
+      dsa_f32x16 wacc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) wacc[r] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2 * NKT; ++j) {
+        const x8 a = *reinterpret_cast<const x8*>(wrow + wbase + 16 * j + 8 * g);
+        wacc = E::mfma32(a, pf[j], wacc);
+      }
+#pragma unroll
+      for (int i = 0; i < 5; ++i) carry[i] += wacc[i];
+    }
   };
 
   // One pipelined step: wait for the current stage, prefetch the next
@@ -508,18 +583,38 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       // Causal (dense): keys past this lane's query row are masked.
       const int lim = !kRouted && p.causal ? tq - (kb * p.block + half * kHalfKeys) + 1 : kHalfKeys;
       if (decltype(skip_c)::value && valid <= 32)
-        compute(kc, vc, valid, lim, 0ull, std::integral_constant<int, 1>{});
+        compute(kc, vc, valid, lim, 0ull, 0, std::integral_constant<int, 1>{});
       else
-        compute(kc, vc, valid, lim, 0ull, std::integral_constant<int, 2>{});
+        compute(kc, vc, valid, lim, 0ull, 0, std::integral_constant<int, 2>{});
     }
   };
   // Gathered stream step: chunk at slot o0 of stream block j0 (whose block
   // index is kb0; kb0 < 0 or kb1 < 0: out of range), `left` valid stream
   // slots from the chunk start to the row's last key; next_kb0 == -2: no
   // next chunk.
+  // Fused statistics: tile j (stream index) has ended; the lanes of its
+  // parity write their query row's entry and start the next tile of that
+  // parity from zero.
+  auto close_tile = [&](int j) __attribute__((always_inline)) {
+    if (g == (j & 1)) {
+      const int64_t e = walked(j);
+      if (row_ok && e < p.rs_entries) {
+        const float mass = carry[0];
+        const float inv = mass > 0.f ? 1.f / mass : 0.f;
+        const dsa_f32x2 mean = {(carry[1] + carry[3]) * inv, (carry[2] + carry[4]) * inv};
+        const dsa_f16x2 h = __builtin_convertvector(mean, dsa_f16x2);
+        const int64_t at = e * p.block + local_row;
+        p.rs_logm[at] = mass > 0.f ? __log2f(mass) + m_run : -INFINITY;
+        p.rs_mean[at] = __builtin_bit_cast(uint32_t, h);
+      }
+#pragma unroll
+      for (int i = 0; i < 5; ++i) carry[i] = 0.f;
+    }
+  };
   auto step_gather = [&](int kb0, int kb1, int o0, int left, int next_kb0, int next_kb1,
                          int next_o0, const unsigned char* kc, const unsigned char* vc,
-                         unsigned char* kn, unsigned char* vn) __attribute__((always_inline)) {
+                         unsigned char* kn, unsigned char* vn, int j0, int wbase)
+      __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     if (next_kb0 != -2)
@@ -539,9 +634,13 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       if (kb0 < 0) invalid |= second >= 64 ? ~0ull : (1ull << second) - 1;
       if (kb1 < 0 && second < 64) invalid |= ~0ull << second;
       if (left <= 32)
-        compute(kc, vc, 0, kHalfKeys, invalid, std::integral_constant<int, 1>{});
+        compute(kc, vc, 0, kHalfKeys, invalid, wbase, std::integral_constant<int, 1>{});
       else
-        compute(kc, vc, 0, kHalfKeys, invalid, std::integral_constant<int, 2>{});
+        compute(kc, vc, 0, kHalfKeys, invalid, wbase, std::integral_constant<int, 2>{});
+      // Block j0 ends in this chunk (the row's last block closes after the walk).
+      if constexpr (kStats) {
+        if (second <= 64 && j0 + 1 < nblk) close_tile(j0);
+      }
     }
   };
   const std::bool_constant<false> no_skip;
@@ -558,6 +657,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     const int total = (nblk - 1) * bp + p.block;  // slots up to the row's last key
     const int chunks = (total + 63) >> 6;
     int j0 = 0, o0 = 0;
+    int w0 = 0;  // the chunk's stream position mod 2 bp (statistics weights)
+    auto next_w = [&](int w) { return w + 64 >= 2 * bp ? w + 64 - 2 * bp : w + 64; };
     int kb0 = gblock(0), kb1 = gblock(1);
     issue_gather(kb0 < 0 ? 0 : kb0, kb1 < 0 ? 0 : kb1, 0, lds_k0, lds_v0);
     for (int c = 0; c < chunks; c += 2) {
@@ -565,16 +666,21 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       if (o1 >= bp) { o1 -= bp; ++j1; }
       const bool more1 = c + 1 < chunks;
       const int kb0n = more1 ? gblock(j1) : -2, kb1n = more1 ? gblock(j1 + 1) : -2;
+      const int w1 = next_w(w0);
       step_gather(kb0, kb1, o0, total - c * 64, kb0n, kb1n, o1, lds_k0, lds_v0, lds_k1,
-                  lds_v1);
+                  lds_v1, j0, w0);
       if (!more1) break;
       int j2 = j1, o2 = o1 + 64;
       if (o2 >= bp) { o2 -= bp; ++j2; }
       const bool more2 = c + 2 < chunks;
       const int kb0m = more2 ? gblock(j2) : -2, kb1m = more2 ? gblock(j2 + 1) : -2;
       step_gather(kb0n, kb1n, o1, total - (c + 1) * 64, kb0m, kb1m, o2, lds_k1, lds_v1,
-                  lds_k0, lds_v0);
+                  lds_k0, lds_v0, j1, w1);
       j0 = j2; o0 = o2; kb0 = kb0m; kb1 = kb1m;
+      w0 = next_w(w1);
+    }
+    if constexpr (kStats) {
+      if (wave_active) close_tile(nblk - 1);
     }
   } else if (!kGather && nblk > 0) {
     int kb = block_of(0);
@@ -821,12 +927,16 @@ constexpr size_t kPartBytes = sizeof(float) * kPartFloats;
 // holds 65..127 keys and its 8-rounded size is below the plain layout's slots
 // per block (64 + 32 up to 96 keys, else 128), and the whole K and V
 // sequences of one head each span < 2 GiB (one buffer resource addresses each).
-inline bool use_gather(int32_t block, int32_t kv_tokens, int64_t k_token_stride,
-                int64_t v_token_stride) {
+inline bool gather_blocks(int32_t block, int32_t kv_tokens) {
   if (block <= kHalfKeys || block >= 2 * kHalfKeys || kv_tokens % block != 0) return false;
   const int32_t pad = (block + 7) & ~7;
   const int32_t plain = block - kHalfKeys <= 32 ? kHalfKeys + 32 : 2 * kHalfKeys;
-  if (pad >= plain) return false;
+  return pad < plain;
+}
+
+inline bool use_gather(int32_t block, int32_t kv_tokens, int64_t k_token_stride,
+                int64_t v_token_stride) {
+  if (!gather_blocks(block, kv_tokens)) return false;
   const int64_t stride = std::max(k_token_stride, v_token_stride);
   return ((int64_t)kv_tokens + 8) * stride * 2 + kRowBytes <= 0x7fffffff;
 }
@@ -875,7 +985,8 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
   auto four = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p); };
   auto two = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, two_waves, 0, stream, p); };
   if (p.row_ptr && use_gather(p.block, p.kv_tokens, p.k_st, p.v_st)) {
-    four(bsa_fwd_kernel<T, true, 2, true, true>);
+    if (p.rs_logm) four(bsa_fwd_kernel<T, true, 2, true, true, 4, true>);
+    else four(bsa_fwd_kernel<T, true, 2, true, true>);
   } else if (p.row_ptr) {
     if (nh == 2) skip ? four(bsa_fwd_kernel<T, true, 2, true>) : four(bsa_fwd_kernel<T, true, 2, false>);
     else skip ? two(bsa_fwd_kernel<T, true, 1, true, false, 2>)

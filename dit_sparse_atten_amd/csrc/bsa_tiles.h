@@ -69,6 +69,15 @@ __device__ __forceinline__ void k_tile_offsets(int wave, int lane, int64_t k_st,
   }
 }
 
+// Tile-local coordinate of index i on a tile axis of `length` tokens, mapped
+// to [-1, 1] in fp32 as the reference's spatial offsets are
+// (attention_backends/sparse.py:141-146): (i - c) / max(c, 1/2), c = (length - 1) / 2.
+__device__ __forceinline__ float tile_axis(int i, int length) {
+  const float center = (float)(length - 1) / 2.0f;
+  const float scale = fmaxf((float)(length - 1) / 2.0f, 0.5f);
+  return ((float)i - center) / scale;
+}
+
 // Q fragments of one query row for the S^T = K Q^T products: qf[dc] holds
 // dims 16 dc + 8 g .. + 7, zeros at or past head_dim.
 template <typename X8, typename T>

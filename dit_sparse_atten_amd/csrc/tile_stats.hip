@@ -90,12 +90,7 @@ struct TileStatsParams {
   float scale_log2;
 };
 
-// (i - center) / scale for one tile axis, as sparse.py:141-146 computes it in fp32.
-__device__ __forceinline__ float axis_offset(int i, int length) {
-  const float center = (float)(length - 1) / 2.0f;
-  const float scale = fmaxf((float)(length - 1) / 2.0f, 0.5f);
-  return ((float)i - center) / scale;
-}
+using dsa::tile_axis;
 
 // Eight fp32 values as an fp16 MFMA operand (round to nearest even).
 __device__ __forceinline__ dsa_f16x8 pack_f16x8(const float* v) {
@@ -146,8 +141,8 @@ __global__ void __launch_bounds__(kWaves * 64, 3) tile_stats_kernel(TileStatsPar
     float w = 0.f;
     if (r / 5 == par && off < p.tile) {
       // Local token index -> (row, column) inside the tile, row-major.
-      const float y = axis_offset(off / p.tile_w, p.tile_h);
-      const float x = axis_offset(off % p.tile_w, p.tile_w);
+      const float y = tile_axis(off / p.tile_w, p.tile_h);
+      const float x = tile_axis(off % p.tile_w, p.tile_w);
       const int kind = r % 5;
       w = kind == 0 ? 1.f
         : kind == 1 ? (float)(_Float16)y
@@ -160,8 +155,8 @@ __global__ void __launch_bounds__(kWaves * 64, 3) tile_stats_kernel(TileStatsPar
   for (int i = tid; i < 128; i += kThreads) {
     const bool in = i < p.tile;
     uq[0][i] = 1.f;
-    uq[1][i] = in ? axis_offset(i / p.tile_w, p.tile_h) : 0.f;
-    uq[2][i] = in ? axis_offset(i % p.tile_w, p.tile_w) : 0.f;
+    uq[1][i] = in ? tile_axis(i / p.tile_w, p.tile_h) : 0.f;
+    uq[2][i] = in ? tile_axis(i % p.tile_w, p.tile_w) : 0.f;
   }
   const int64_t cell0 = ((int64_t)h * p.tiles + qt) * p.tiles;
   if (kRouted) {

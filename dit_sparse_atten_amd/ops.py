@@ -329,6 +329,70 @@ def tile_stats(q, k, lse, tile_shape, csr=None, scale=None, centroids=True):
     return out
 
 
+def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False,
+                       centroids=True):
+    """One routed matrix-sparse step: block-sparse attention of tile-major
+    q/k/v [1, T, H, D] over the CSR of kept tiles and the statistics of that
+    same softmax (the reference's ``sparse_chunk``, attention_backends/
+    sparse.py:670-751).  Returns ``(out, lse, stats)`` with ``out`` as
+    :func:`bsa_fwd` returns it, ``lse`` [1, H, T] and ``stats`` as
+    :func:`tile_stats` returns them.  Tiles that take the gathered key stream
+    (e.g. 9 x 8) get their statistics from the attention launch itself; other
+    tiles run the attention and then :func:`tile_stats`.
+    """
+    lib = _lib.load()
+    q = _kernel_view("q", q)
+    k = _kernel_view("k", k, q.dtype)
+    v = _kernel_view("v", v, q.dtype)
+    batch, tokens, heads, head_dim = q.shape
+    if batch != 1 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("tile statistics support batch-1 self-attention")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q, k and v must be on the same device")
+    tile_h, tile_w = (int(x) for x in tile_shape)
+    tile = tile_h * tile_w
+    if tile <= 0 or tile > 128 or tokens % tile:
+        raise ValueError("the tile shape must divide the token count (1..128 tokens per tile)")
+    tiles = tokens // tile
+    if csr is None:
+        raise ValueError("a route CSR is required")
+    if (csr.route_batches, csr.heads, csr.q_blocks, csr.k_blocks, csr.block_size) != (
+            1, heads, tiles, tiles, tile):
+        raise ValueError("route shape does not match the tile layout")
+    if csr.row_ptr.device != q.device or csr.col_idx.device != q.device:
+        raise ValueError("route must live on the attention device")
+    if scale is None:
+        scale = head_dim ** -0.5
+    entries = csr.nnz_value() if csr.nnz is not None else int(csr.row_ptr[-1].item())
+    out = torch.empty((1, tokens, heads, head_dim), dtype=q.dtype, device=q.device)
+    lse = torch.empty((1, heads, tokens), dtype=torch.float32, device=q.device)
+    shape = (heads, tiles, tiles)
+    stats = {"mass": torch.empty(shape, dtype=torch.float32, device=q.device),
+             "mass_f16": torch.empty(shape, dtype=torch.float16, device=q.device)}
+    names = ("centroid_q_y", "centroid_q_x", "centroid_k_y", "centroid_k_x")
+    if centroids:
+        for name in names:
+            stats[name] = torch.empty(shape, dtype=torch.float16, device=q.device)
+    strides = _lib.int64_array(
+        list(q.stride()[:3]) + list(k.stride()[:3]) + list(v.stride()[:3])
+        + list(out.stride()[:3]))
+    workspace_bytes = lib.dsa_bsa_fwd_tile_stats_workspace_bytes(
+        heads, tokens, head_dim, tile_h, tile_w, entries)
+    workspace = (torch.empty(workspace_bytes, dtype=torch.uint8, device=q.device)
+                 if workspace_bytes else None)
+    with torch.cuda.device(q.device):
+        status = lib.dsa_bsa_fwd_tile_stats(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dtype_code(q.dtype),
+            strides, tokens, heads, head_dim, tile_h, tile_w, csr.row_ptr.data_ptr(),
+            csr.col_idx.data_ptr(), entries, float(scale), int(bool(deterministic)),
+            lse.data_ptr(), stats["mass"].data_ptr(), stats["mass_f16"].data_ptr(),
+            *[stats[name].data_ptr() if name in stats else None for name in names],
+            workspace.data_ptr() if workspace is not None else None, workspace_bytes,
+            _stream_handle(q.device))
+    _lib.check(status, "dsa_bsa_fwd_tile_stats")
+    return out, lse, stats
+
+
 def route_select(mass, target, keep, previous=None, persistence=0.0, sink_blocks=0):
     """Prior + top-mass selection + sink on the GPU.
 

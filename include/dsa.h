@@ -183,6 +183,43 @@ int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const int64_t* s
                    void* centroid_k_x, hipStream_t stream);
 
 /*
+ * One routed step of the matrix-sparse backend: block-sparse attention over
+ * spatial tiles together with that attention's tile statistics.  Replaces
+ * `sparse_chunk` (attention_backends/sparse.py:670-751: output plus the
+ * statistics of the same softmax) and `_sparse_stats_kernel`
+ * (sparse.py:498-578, the Triton path's second pass over QK^T).  The
+ * arguments are those of dsa_bsa_fwd with batch 1, q_tokens = kv_tokens =
+ * tokens (tile-major, a whole number of tile_h x tile_w tiles of at most 128
+ * tokens) and the CSR of the kept tiles (route_batches 1; required), and
+ * those of dsa_tile_stats with lse required (written: [heads, tokens] fp32)
+ * and lse_head_stride = tokens.
+ *   entries: at least the CSR's entry count row_ptr[heads * tiles] (the
+ *            cells of entries past it read as zeros).
+ * Tiles that take the gathered key stream (65..127 tokens whose 8-rounded
+ * size is below the plain layout's key slots, e.g. 9 x 8) have their
+ * statistics taken from the attention's own probabilities in the same launch
+ * (the key-side sums on the matrix cores beside P V, per query row and key
+ * tile, into the workspace), then combined per cell by a short second
+ * launch; other tiles run dsa_bsa_fwd and then dsa_tile_stats.
+ *   workspace: dsa_bsa_fwd_tile_stats_workspace_bytes(...) bytes, 16-byte
+ *            aligned: entries * tile * 8 bytes of per-row statistics when
+ *            fused (rounded up to 256), then dsa_bsa_fwd's workspace.
+ */
+int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* v, void* o, int32_t dtype,
+                           const int64_t* strides, int32_t tokens, int32_t heads,
+                           int32_t head_dim, int32_t tile_h, int32_t tile_w,
+                           const int32_t* row_ptr, const int32_t* col_idx, int64_t entries,
+                           float scale, int32_t deterministic, float* lse, float* mass,
+                           void* mass_f16, void* centroid_q_y, void* centroid_q_x,
+                           void* centroid_k_y, void* centroid_k_x, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes dsa_bsa_fwd_tile_stats needs (0 for invalid sizes).  No
+ * counterpart in the reference. */
+size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t tokens, int32_t head_dim,
+                                              int32_t tile_h, int32_t tile_w, int64_t entries);
+
+/*
  * Persistence prior + top-mass selection + first-frame sink, per row.
  * Replaces the prior of `_sampled_route` (flex.py:535-541), `_top_mass_route`
  * (flex.py:83-94, == sparse.py:171-181 `_row_mask`) and `_add_first_frame_sink`

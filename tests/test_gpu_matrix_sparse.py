@@ -167,6 +167,81 @@ def test_routed_tile_stats_skip_out_of_range_tiles(ops, cuda_device):
     _compare_stats(got, expected)
 
 
+@pytest.mark.parametrize("grid,tile,deterministic", [
+    ((2, 18, 32), 64, True),    # 9 x 8 = 72 tokens: gathered stream, fused
+    ((2, 18, 32), 64, False),   # the same with the aligned walk
+    ((2, 15, 26), 64, True),    # 5 x 13 = 65 tokens padded to 72, fused
+    ((1, 20, 30), 100, False),  # 10 x 10 = 100 tokens padded to 104, fused
+    ((4, 16, 16), 64, True),    # 8 x 8 = 64 tokens: attention, then the statistics pass
+])
+def test_fused_step_matches_two_pass_and_oracle(ops, cuda_device, grid, tile, deterministic):
+    """dsa_bsa_fwd_tile_stats (attention and the statistics of the same
+    softmax in one call) against the separate attention + tile_stats passes
+    and the oracle's sparse_chunk: output, LSE, mass and centroids; cells the
+    route does not list are zero."""
+    case, q, k, v = _tile_major_inputs(grid, 2, seed=sum(grid), tile=tile)
+    tiles = q.shape[1] // case.tile
+    route = random_route(2, tiles, seed=9, keep=0.55).numpy()
+    route[..., 0] = True
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=case.tile)
+    out, lse, got = ops.bsa_fwd_tile_stats(qd, kd, vd, csr, case.tile_shape,
+                                           deterministic=deterministic)
+    ref_out, ref_lse = ops.bsa_fwd(qd, kd, vd, csr, return_lse=True, block_size=case.tile,
+                                   deterministic=True)
+    two_pass = ops.tile_stats(qd, kd, ref_lse, case.tile_shape, csr=csr)
+    torch.cuda.synchronize()
+    if deterministic:
+        assert torch.equal(out, ref_out) and torch.equal(lse, ref_lse)
+    expected, expected_out = _oracle_stats(case, q, k, v, route)
+    _compare_stats(got, expected)
+    metrics = A.summarize(out.float().cpu().numpy(), expected_out)
+    assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
+    np.testing.assert_allclose(got["mass"].cpu().numpy(), two_pass["mass"].cpu().numpy(),
+                               atol=STAT_ATOL, rtol=2e-3)
+    assert (got["mass"].cpu().numpy()[~route] == 0).all()
+    # Every query row's mass over its tiles sums to one.
+    np.testing.assert_allclose(got["mass"].sum(-1).cpu().numpy(), case.tile / q.shape[1],
+                               rtol=2e-3)
+
+
+def test_fused_step_at_720p_tile_shape(ops, cuda_device):
+    """The bench's 720p matrix-sparse step shape (9 x 8 tiles, 800 tiles
+    per head) at 4 heads: fused statistics against the two-pass statistics on
+    every cell, and the oracle on sampled query tiles."""
+    case, q, k, v = _tile_major_inputs((16, 45, 80), 4, seed=21, tile=64)
+    tiles = q.shape[1] // case.tile
+    route = random_route(4, tiles, seed=2, keep=0.625).numpy()
+    route[..., :4] = True
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=case.tile)
+    out, lse, got = ops.bsa_fwd_tile_stats(qd, kd, vd, csr, case.tile_shape)
+    _, ref_lse = ops.bsa_fwd(qd, kd, vd, csr, return_lse=True, block_size=case.tile)
+    two_pass = ops.tile_stats(qd, kd, ref_lse, case.tile_shape, csr=csr)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse.cpu().numpy(), atol=1e-4)
+    for name in ("mass", "mass_f16"):
+        np.testing.assert_allclose(got[name].float().cpu().numpy(),
+                                   two_pass[name].float().cpu().numpy(), atol=STAT_ATOL,
+                                   rtol=2e-3, err_msg=name)
+    for name in ("centroid_q_y", "centroid_q_x", "centroid_k_y", "centroid_k_x"):
+        np.testing.assert_allclose(got[name].float().cpu().numpy(),
+                                   two_pass[name].float().cpu().numpy(), atol=CENTROID_ATOL,
+                                   err_msg=name)
+    # Sampled query tiles of head 0 against the oracle's sparse_chunk.
+    qf, kf, vf = (x[:, :, :1].float().numpy() for x in (q, k, v))
+    stats = S.empty_stats(1, tiles)
+    offsets = S.spatial_offsets(case.tile_shape, tiles)
+    for qt in (0, 1, 399, 799):
+        start = qt * case.tile
+        S.sparse_chunk(qf, kf, vf, route[:1], case.tile, start, start + case.tile,
+                       128 ** -0.5, stats, offsets)
+        want = stats["mass"][0, qt] / np.float32(q.shape[1])
+        np.testing.assert_allclose(got["mass"][0, qt].cpu().numpy(), want, atol=STAT_ATOL,
+                                   rtol=2e-3, err_msg=f"query tile {qt}")
+
+
 def test_route_select_up_to_2048_tiles(ops, cuda_device):
     """The 720p tile route has 800 key tiles per row at 61 frames and 1,050 at
     81 frames (one-wave sorts of 1,024 and 2,048 keys)."""
