@@ -729,8 +729,13 @@ def main():
             ops.drop_low_mass(tile_route, tstats["mass"], 0.1, tile_sink)
 
         def tile_bootstrap():
+            # _dense_route: dense attention and its statistics in one call.
+            _, _, tstats = ops.bsa_fwd_tile_stats(qt, kt, vt, None, tile_shape)
+            ops.route_select(tstats["mass"], 0.9, KEEP, sink_blocks=tile_sink)
+
+        def tile_bootstrap_two_pass():
             _, tlse = ops.bsa_fwd(qt, kt, vt, out=tile_out, return_lse=True)
-            tstats = ops.tile_stats(qt, kt, tlse, (tile_layout.tile_h, tile_layout.tile_w))
+            tstats = ops.tile_stats(qt, kt, tlse, tile_shape)
             ops.route_select(tstats["mass"], 0.9, KEEP, sink_blocks=tile_sink)
 
         tile_attention()
@@ -743,7 +748,10 @@ def main():
         tile_step_ms, _ = timer.time(tile_step_directional, 3)
         tile_stats_ms, _ = timer.time(tile_stats_pass, 3)
         tile_two_pass_ms, _ = timer.time(tile_step_two_pass, 3)
+        tile_bootstrap()
         tile_boot_ms, _ = timer.time(tile_bootstrap, 2)
+        tile_bootstrap_two_pass()
+        tile_boot_two_pass_ms, _ = timer.time(tile_bootstrap_two_pass, 2)
         tile_flops = 4.0 * HEAD_DIM * tile * tile * tile_nnz
         result["matrix_sparse"] = {
             "tile_shape": [tile_layout.tile_h, tile_layout.tile_w],
@@ -757,6 +765,7 @@ def main():
             "two_pass_stats_pass_ms": round(tile_stats_ms, 4),
             "directional_step_two_pass_ms": round(tile_two_pass_ms, 4),
             "bootstrap_ms": round(tile_boot_ms, 4),
+            "bootstrap_two_pass_ms": round(tile_boot_two_pass_ms, 4),
             "reference_pytorch_sparse_ms": 8396.6, "reference_triton_sparse_ms": 4038.5,
             "reference_source": ("results/sparse_attention_profile.json (57,600 tokens, "
                                  "40 heads, 6x10 tiles, keep .625)"),

@@ -200,9 +200,9 @@ class MatrixSparseBackend:
         tile_shape = (layout.tile_h, layout.tile_w)
         sink = layout.block_h * layout.block_w if c.first_frame_sink else 0
         if step == 0 or key not in self.state:
-            # The first observation is dense; its LSE gives the exact route.
-            output, lse = ops.bsa_fwd(q, k, v, scale=scale, return_lse=True)
-            stats = ops.tile_stats(q, k, lse, tile_shape, scale=scale)
+            # The first observation is dense; its statistics give the exact
+            # route (_dense_route, sparse.py:184-233).
+            output, _, stats = ops.bsa_fwd_tile_stats(q, k, v, None, tile_shape, scale=scale)
             mask, _ = ops.route_select(stats["mass"], c.mass_target, c.keep, sink_blocks=sink)
             route = {"mask": mask, "mass": stats["mass_f16"], "tile": layout.tile_tokens,
                      "grid": (layout.frames, layout.height, layout.width),

@@ -85,6 +85,7 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
   p->rs_mean = nullptr;
   p->rs_entries = 0;
   p->tile_h = p->tile_w = 0;
+  p->stat_tile = p->stat_pad = 0;
   p->scale = scale;
   p->scale_log2 = scale * 1.4426950408889634f;
   return DSA_OK;
@@ -142,7 +143,7 @@ int scratch_on(int device, void** out, const char* who) {
 namespace {
 
 // Cells of the fused statistics: one workgroup per (head, query tile) row.
-// For each key tile the row lists, query row r of the tile contributes
+// For each key tile the row lists (every tile when dense), query row r of the tile contributes
 // w_r = 2^(rs_logm - lse_r log2 e), its probability mass on that key tile:
 //   mass = sum w_r, q_y = sum w_r y(r), q_x = sum w_r x(r),
 //   k_y = sum w_r mean_y, k_x = sum w_r mean_x,
@@ -164,6 +165,7 @@ struct ReduceParams {
   __half* cky;
   __half* ckx;
   int32_t tokens, tiles, tile, tile_h, tile_w;
+  int32_t dense;  // 1: every key tile, rows at (h * tiles + kt) * tokens + token
 };
 
 __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) {
@@ -189,14 +191,16 @@ __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) 
   }
   // The zeros land before the listed cells are written (vmcnt(0) barrier).
   dsa::lds_barrier<true>();
-  const int start = p.row_ptr[row];
-  const int end = (int)min((int64_t)p.row_ptr[row + 1], p.entries);
+  const int start = p.dense ? 0 : p.row_ptr[row];
+  const int end = p.dense ? p.tiles : (int)min((int64_t)p.row_ptr[row + 1], p.entries);
   for (int e = start + wave; e < end; e += 4) {
-    const int kt = p.col_idx[e];
+    const int kt = p.dense ? e : p.col_idx[e];
     if ((unsigned)kt >= (unsigned)p.tiles) continue;
+    const int64_t at0 = p.dense ? ((int64_t)h * p.tiles + kt) * p.tokens + (int64_t)qt * p.tile
+                                : (int64_t)e * p.tile;
     float m = 0.f, qy = 0.f, qx = 0.f, ky = 0.f, kx = 0.f;
     for (int r = lane; r < p.tile; r += 64) {
-      const int64_t at = (int64_t)e * p.tile + r;
+      const int64_t at = at0 + r;
       const float w = __builtin_amdgcn_exp2f(p.rs_logm[at] - lse2[r]);
       const dsa_f16x2 mean = __builtin_bit_cast(dsa_f16x2, p.rs_mean[at]);
       m += w;
@@ -302,8 +306,9 @@ extern "C" size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t 
   const int32_t tile = tile_h * tile_w;
   if (tokens % tile != 0) return 0;
   const size_t attention = dsa_bsa_workspace_bytes_block(1, heads, tokens, head_dim, tile);
-  // Tiles that take the gathered key stream also hold the per-row statistics.
-  return attention + (gather_blocks(tile, tokens) ? row_stats_bytes(entries, tile) : 0);
+  // Tiles that can fuse the statistics (65..128 tokens) also hold the per-row
+  // statistics.
+  return attention + (tile > kHalfKeys ? row_stats_bytes(entries, tile) : 0);
 }
 
 extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* v, void* o,
@@ -317,9 +322,10 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
                                       size_t workspace_bytes, hipStream_t stream) {
   const char* who = "dsa_bsa_fwd_tile_stats";
   dsa::clear_error();
-  if (!row_ptr || !col_idx || !lse || !mass || !strides)
-    return dsa::set_error(DSA_EINVAL, "%s: row_ptr, col_idx, lse, mass and strides are required",
-                          who);
+  if (!lse || !mass || !strides)
+    return dsa::set_error(DSA_EINVAL, "%s: lse, mass and strides are required", who);
+  if ((row_ptr == nullptr) != (col_idx == nullptr))
+    return dsa::set_error(DSA_EINVAL, "%s: row_ptr and col_idx must both be set or null", who);
   if (tile_h <= 0 || tile_w <= 0 || (int64_t)tile_h * tile_w > 128)
     return dsa::set_error(DSA_EUNSUPPORTED, "%s: tile %dx%d unsupported (1..128 tokens)", who,
                           tile_h, tile_w);
@@ -328,9 +334,20 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
     return dsa::set_error(DSA_EINVAL, "%s: %d tokens are not whole %d-token tiles", who, tokens,
                           tile);
   if (entries < 0) return dsa::set_error(DSA_EINVAL, "%s: entries must be >= 0", who);
+  const int32_t tiles = tokens / tile;
+  const bool dense = row_ptr == nullptr;
+  // Dense calls run the attention on 128-token blocks; their statistics fuse
+  // for tiles of 65..128 tokens (at most one tile end per 64-key step) that
+  // are a multiple of 8 (so every step starts 16-aligned in the weight
+  // table's period of two tiles).
+  const bool fuse_dense = dense && tile > kHalfKeys && tile % 8 == 0;
+  if (fuse_dense && entries < (int64_t)heads * tiles * tiles)
+    return dsa::set_error(DSA_EINVAL, "%s: dense statistics need entries >= heads * tiles^2",
+                          who);
   BsaParams p;
-  int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim, tile,
-                       row_ptr, col_idx, 1, scale, 0, deterministic, lse, who, &p);
+  int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim,
+                       dense ? 128 : tile, row_ptr, col_idx, 1, scale, 0, deterministic, lse, who,
+                       &p);
   if (status != DSA_OK) return status;
   if (workspace_bytes > 0 && (!workspace || !aligned16(workspace)))
     return dsa::set_error(DSA_EINVAL, "%s: workspace must be 16-byte aligned", who);
@@ -339,23 +356,24 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
   if (workspace_bytes < need)
     return dsa::set_error(DSA_EINVAL, "%s: workspace of %zu bytes, %zu needed", who,
                           workspace_bytes, need);
-  const size_t rs = gather_blocks(tile, tokens) ? row_stats_bytes(entries, tile) : 0;
-  if (!use_gather(tile, tokens, strides[4], strides[7])) {
-    // Tiles outside the gathered stream: the attention, then a second pass.
-    status = launch(dtype, p, static_cast<unsigned char*>(workspace) + rs, workspace_bytes - rs,
-                    stream, who);
+  const size_t rs = tile > kHalfKeys ? row_stats_bytes(entries, tile) : 0;
+  unsigned char* base = static_cast<unsigned char*>(workspace);
+  if (!fuse_dense && (dense || !use_gather(tile, tokens, strides[4], strides[7]))) {
+    // The attention, then the statistics pass.
+    status = launch(dtype, p, base + rs, workspace_bytes - rs, stream, who);
     if (status != DSA_OK) return status;
     const int64_t stat_strides[4] = {strides[1], strides[2], strides[4], strides[5]};
     return dsa_tile_stats(q, k, dtype, stat_strides, tokens, heads, head_dim, tile_h, tile_w, lse,
                           tokens, row_ptr, col_idx, scale, mass, mass_f16, centroid_q_y,
                           centroid_q_x, centroid_k_y, centroid_k_x, stream);
   }
-  unsigned char* base = static_cast<unsigned char*>(workspace);
   p.rs_logm = reinterpret_cast<float*>(base);
   p.rs_mean = reinterpret_cast<uint32_t*>(base + (size_t)entries * tile * sizeof(float));
   p.rs_entries = entries;
   p.tile_h = tile_h;
   p.tile_w = tile_w;
+  p.stat_tile = tile;
+  p.stat_pad = dense ? tile : p.block_pad;
   status = launch(dtype, p, base + rs, workspace_bytes - rs, stream, who);
   if (status != DSA_OK) return status;
   ReduceParams r;
@@ -372,11 +390,12 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
   r.cky = static_cast<__half*>(centroid_k_y);
   r.ckx = static_cast<__half*>(centroid_k_x);
   r.tokens = tokens;
-  r.tiles = tokens / tile;
+  r.tiles = tiles;
   r.tile = tile;
   r.tile_h = tile_h;
   r.tile_w = tile_w;
-  hipLaunchKernelGGL(tile_stats_reduce_kernel, dim3((unsigned)(heads * r.tiles)), dim3(256), 0,
+  r.dense = dense ? 1 : 0;
+  hipLaunchKernelGGL(tile_stats_reduce_kernel, dim3((unsigned)(heads * tiles)), dim3(256), 0,
                      stream, r);
   return dsa::check_launch(who);
 }

@@ -78,15 +78,19 @@ struct BsaParams {
   int32_t split_from;
   int32_t parts;
   float* part;
-  // Fused tile statistics (the kStats instances): for CSR entry e (a kept key
-  // tile) and query row r of its row's query tile, at e * block + r,
-  // rs_logm = log2 of the row's unnormalised probability mass on that key
-  // tile, sum 2^(scale_log2 s), and rs_mean = its mass-weighted mean key
-  // offsets (y, x) as two fp16.  Entries at or past rs_entries are not written.
+  // Fused tile statistics (the kStats instances), per query row and key tile
+  // of stat_tile = tile_h * tile_w tokens: rs_logm = log2 of the row's
+  // unnormalised probability mass on the key tile, sum 2^(scale_log2 s), and
+  // rs_mean = its mass-weighted mean key offsets (y, x) as two fp16.  Routed
+  // (gathered stream): at e * block + r for CSR entry e and query row r of
+  // the tile, entries at or past rs_entries not written.  Dense: at
+  // (h * tiles + key tile) * q_tokens + query token.
   float* rs_logm;
   uint32_t* rs_mean;
   int64_t rs_entries;
-  int32_t tile_h, tile_w;  // the tile shape, tile_h * tile_w = block
+  int32_t tile_h, tile_w;
+  int32_t stat_tile;  // tokens per statistics tile (65..128)
+  int32_t stat_pad;   // stream slots per statistics tile (gathered: block_pad; dense: stat_tile)
 };
 
 // One split partial: O [128 rows][128 dims] relative to the row's reference
@@ -198,8 +202,9 @@ __device__ __forceinline__ int walk_start(const uint64_t* tab, int lane, int bh,
 // at most 64 tokens, whose rows two waves cover: smaller workgroups spread
 // over the four SIMDs instead of leaving two waves per workgroup idle).
 //
-// kStats (gathered stream only): the workgroup also writes the per-row tile
-// statistics (rs_logm, rs_mean) from the probabilities of its own softmax.
+// kStats (the gathered stream, or dense calls of 128-token blocks): the
+// workgroup also writes the per-row tile statistics (rs_logm, rs_mean) from
+// the probabilities of its own softmax.
 // The key-side sums run on the matrix cores beside O^T = V^T P^T: with the
 // same P^T operand, C += W^T P^T where W^T (kStatRows x keys, an LDS table)
 // holds, for the key tiles of each parity (stream tile index mod 2), the
@@ -207,9 +212,11 @@ __device__ __forceinline__ int walk_start(const uint64_t* tab, int lane, int bh,
 // an input-type high part and the remainder.  The rows sit at C rows 0-3, 8
 // (even tiles) and 4-7, 12 (odd tiles), so each lane's accumulators 0..4
 // are its query row's five sums for the key tiles of its own half's parity.
-// Tiles span two chunks at most (65..127 keys against 64-key chunks) and two
+// Tiles span two chunks at most (65..128 keys against 64-key chunks) and two
 // tiles of one parity never share a chunk, so each lane carries the five sums
-// of one open tile across chunks and closes it in the chunk where it ends.
+// of one open tile across chunks and closes it in the chunk where it ends.  A
+// dense call's key stream is the token sequence itself, 64 keys per step, so
+// the same table serves with tiles of stat_tile slots.
 constexpr int kStatRows = 11;    // 2 parities x 5 kinds, then a zero row
 constexpr int kStatCols = 392;   // >= 2 * 120 + 64 positions; = 8 mod 128 spreads the rows' banks
 
@@ -219,7 +226,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     bsa_fwd_kernel(BsaParams p) {
   typedef dsa::Elem<T> E;
   typedef typename E::x8 x8;
-  static_assert(!kStats || (kRouted && kGather), "fused statistics: gathered stream only");
+  static_assert(!kStats || (kRouted && kGather) || (!kRouted && kNh == 2 && !kSkip && !kGather),
+                "fused statistics: the gathered stream or dense 128-token blocks");
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
@@ -402,14 +410,14 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   const T* wrow = wtab;
   float carry[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
   if constexpr (kStats) {
-    const int bp = p.block_pad;
+    const int bp = p.stat_pad;
     for (int i = tid; i < kStatRows * kStatCols; i += kWaves * 64) {
       const int r = i / kStatCols, si = i % kStatCols;
       const int pos = (si & ~12) | ((si & 4) << 1) | ((si & 8) >> 1);
       const int q2 = pos % (2 * bp);
       const int par = q2 / bp, off = q2 % bp;
       float w = 0.f;
-      if (r < 10 && r / 5 == par && off < p.block) {
+      if (r < 10 && r / 5 == par && off < p.stat_tile) {
         const float y = dsa::tile_axis(off / p.tile_w, p.tile_h);
         const float x = dsa::tile_axis(off % p.tile_w, p.tile_w);
         const float yh = (float)(T)y, xh = (float)(T)x;
@@ -567,6 +575,23 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     }
   };
 
+  // Fused statistics: a tile of parity par has ended; the lanes of that parity
+  // write their query row's entry at `at` (when `ok`) and start the next tile
+  // of that parity from zero.
+  auto close_tile = [&](int par, int64_t at, bool ok) __attribute__((always_inline)) {
+    if (g == par) {
+      if (ok) {
+        const float mass = carry[0];
+        const float inv = mass > 0.f ? 1.f / mass : 0.f;
+        const dsa_f32x2 mean = {(carry[1] + carry[3]) * inv, (carry[2] + carry[4]) * inv};
+        const dsa_f16x2 hm = __builtin_convertvector(mean, dsa_f16x2);
+        p.rs_logm[at] = mass > 0.f ? __log2f(mass) + m_run : -INFINITY;
+        p.rs_mean[at] = __builtin_bit_cast(uint32_t, hm);
+      }
+#pragma unroll
+      for (int i = 0; i < 5; ++i) carry[i] = 0.f;
+    }
+  };
   // One pipelined step: wait for the current stage, prefetch the next
   // half-tile (next_kb == -2: none), then compute on the current one
   // (skip_c: this step may hold at most 32 valid keys).
@@ -582,34 +607,31 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       const int valid = valid_of(kb, half);
       // Causal (dense): keys past this lane's query row are masked.
       const int lim = !kRouted && p.causal ? tq - (kb * p.block + half * kHalfKeys) + 1 : kHalfKeys;
+      // Dense statistics: this step's keys are tokens pos .. pos + 63.
+      const int pos = kb * p.block + half * kHalfKeys;
+      const int wbase = kStats ? pos % (2 * p.stat_pad) : 0;
       if (decltype(skip_c)::value && valid <= 32)
-        compute(kc, vc, valid, lim, 0ull, 0, std::integral_constant<int, 1>{});
+        compute(kc, vc, valid, lim, 0ull, wbase, std::integral_constant<int, 1>{});
       else
-        compute(kc, vc, valid, lim, 0ull, 0, std::integral_constant<int, 2>{});
+        compute(kc, vc, valid, lim, 0ull, wbase, std::integral_constant<int, 2>{});
+      if constexpr (kStats) {
+        // The tile ending in (pos, pos + 64] (the sequence end included), if any.
+        const int m = min(pos + kHalfKeys, p.kv_tokens) / p.stat_tile;
+        if (m >= 1 && m * p.stat_tile > pos)
+          close_tile((m - 1) & 1,
+                     ((int64_t)h * (p.kv_tokens / p.stat_tile) + (m - 1)) * p.q_tokens + tq,
+                     row_ok);
+      }
     }
   };
   // Gathered stream step: chunk at slot o0 of stream block j0 (whose block
   // index is kb0; kb0 < 0 or kb1 < 0: out of range), `left` valid stream
   // slots from the chunk start to the row's last key; next_kb0 == -2: no
   // next chunk.
-  // Fused statistics: tile j (stream index) has ended; the lanes of its
-  // parity write their query row's entry and start the next tile of that
-  // parity from zero.
-  auto close_tile = [&](int j) __attribute__((always_inline)) {
-    if (g == (j & 1)) {
-      const int64_t e = walked(j);
-      if (row_ok && e < p.rs_entries) {
-        const float mass = carry[0];
-        const float inv = mass > 0.f ? 1.f / mass : 0.f;
-        const dsa_f32x2 mean = {(carry[1] + carry[3]) * inv, (carry[2] + carry[4]) * inv};
-        const dsa_f16x2 h = __builtin_convertvector(mean, dsa_f16x2);
-        const int64_t at = e * p.block + local_row;
-        p.rs_logm[at] = mass > 0.f ? __log2f(mass) + m_run : -INFINITY;
-        p.rs_mean[at] = __builtin_bit_cast(uint32_t, h);
-      }
-#pragma unroll
-      for (int i = 0; i < 5; ++i) carry[i] = 0.f;
-    }
+  // Gathered stream: stream tile j closes into its CSR entry.
+  auto close_stream_tile = [&](int j) __attribute__((always_inline)) {
+    const int64_t e = walked(j);
+    close_tile(j & 1, e * p.block + local_row, row_ok && e < p.rs_entries);
   };
   auto step_gather = [&](int kb0, int kb1, int o0, int left, int next_kb0, int next_kb1,
                          int next_o0, const unsigned char* kc, const unsigned char* vc,
@@ -639,7 +661,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         compute(kc, vc, 0, kHalfKeys, invalid, wbase, std::integral_constant<int, 2>{});
       // Block j0 ends in this chunk (the row's last block closes after the walk).
       if constexpr (kStats) {
-        if (second <= 64 && j0 + 1 < nblk) close_tile(j0);
+        if (second <= 64 && j0 + 1 < nblk) close_stream_tile(j0);
       }
     }
   };
@@ -680,7 +702,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       w0 = next_w(w1);
     }
     if constexpr (kStats) {
-      if (wave_active) close_tile(nblk - 1);
+      if (wave_active) close_stream_tile(nblk - 1);
     }
   } else if (!kGather && nblk > 0) {
     int kb = block_of(0);
@@ -969,7 +991,10 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
     }
   }
   float* part = reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + used);
-  const int64_t part_groups = (int64_t)((scratch_bytes - used) / kPartBytes);
+  // Dense statistics tiles need not align with the split's key ranges: such
+  // calls run unsplit.
+  const int64_t part_groups =
+      p.rs_logm && !p.row_ptr ? 0 : (int64_t)((scratch_bytes - used) / kPartBytes);
   int parts = 1;
   const int split = choose_split(grid, device_slots(stream), max_parts_for(p.kv_blocks),
                                  std::min<int64_t>(part_groups, kMaxPartGroups), &parts);
@@ -991,6 +1016,8 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
     if (nh == 2) skip ? four(bsa_fwd_kernel<T, true, 2, true>) : four(bsa_fwd_kernel<T, true, 2, false>);
     else skip ? two(bsa_fwd_kernel<T, true, 1, true, false, 2>)
               : two(bsa_fwd_kernel<T, true, 1, false, false, 2>);
+  } else if (p.rs_logm && nh == 2 && !skip) {
+    four(bsa_fwd_kernel<T, false, 2, false, false, 4, true>);
   } else {
     if (nh == 2) skip ? four(bsa_fwd_kernel<T, false, 2, true>) : four(bsa_fwd_kernel<T, false, 2, false>);
     else skip ? four(bsa_fwd_kernel<T, false, 1, true>) : four(bsa_fwd_kernel<T, false, 1, false>);

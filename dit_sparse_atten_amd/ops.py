@@ -331,14 +331,15 @@ def tile_stats(q, k, lse, tile_shape, csr=None, scale=None, centroids=True):
 
 def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False,
                        centroids=True):
-    """One routed matrix-sparse step: block-sparse attention of tile-major
-    q/k/v [1, T, H, D] over the CSR of kept tiles and the statistics of that
-    same softmax (the reference's ``sparse_chunk``, attention_backends/
-    sparse.py:670-751).  Returns ``(out, lse, stats)`` with ``out`` as
-    :func:`bsa_fwd` returns it, ``lse`` [1, H, T] and ``stats`` as
-    :func:`tile_stats` returns them.  Tiles that take the gathered key stream
-    (e.g. 9 x 8) get their statistics from the attention launch itself; other
-    tiles run the attention and then :func:`tile_stats`.
+    """One matrix-sparse step: attention of tile-major q/k/v [1, T, H, D] over
+    the CSR of kept tiles (``csr=None``: every tile, dense) and the statistics
+    of that same softmax (the reference's ``sparse_chunk``, attention_backends/
+    sparse.py:670-751; dense: ``_dense_route``, 184-233).  Returns
+    ``(out, lse, stats)`` with ``out`` as :func:`bsa_fwd` returns it, ``lse``
+    [1, H, T] and ``stats`` as :func:`tile_stats` returns them.  Routed calls
+    whose tiles take the gathered key stream (e.g. 9 x 8) and dense calls with
+    tiles of 65..128 tokens get their statistics from the attention launch
+    itself; other calls run the attention and then :func:`tile_stats`.
     """
     lib = _lib.load()
     q = _kernel_view("q", q)
@@ -354,16 +355,17 @@ def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False
     if tile <= 0 or tile > 128 or tokens % tile:
         raise ValueError("the tile shape must divide the token count (1..128 tokens per tile)")
     tiles = tokens // tile
-    if csr is None:
-        raise ValueError("a route CSR is required")
-    if (csr.route_batches, csr.heads, csr.q_blocks, csr.k_blocks, csr.block_size) != (
-            1, heads, tiles, tiles, tile):
-        raise ValueError("route shape does not match the tile layout")
-    if csr.row_ptr.device != q.device or csr.col_idx.device != q.device:
-        raise ValueError("route must live on the attention device")
+    if csr is not None:
+        if (csr.route_batches, csr.heads, csr.q_blocks, csr.k_blocks, csr.block_size) != (
+                1, heads, tiles, tiles, tile):
+            raise ValueError("route shape does not match the tile layout")
+        if csr.row_ptr.device != q.device or csr.col_idx.device != q.device:
+            raise ValueError("route must live on the attention device")
+        entries = csr.nnz_value() if csr.nnz is not None else int(csr.row_ptr[-1].item())
+    else:
+        entries = heads * tiles * tiles
     if scale is None:
         scale = head_dim ** -0.5
-    entries = csr.nnz_value() if csr.nnz is not None else int(csr.row_ptr[-1].item())
     out = torch.empty((1, tokens, heads, head_dim), dtype=q.dtype, device=q.device)
     lse = torch.empty((1, heads, tokens), dtype=torch.float32, device=q.device)
     shape = (heads, tiles, tiles)
@@ -383,8 +385,10 @@ def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False
     with torch.cuda.device(q.device):
         status = lib.dsa_bsa_fwd_tile_stats(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dtype_code(q.dtype),
-            strides, tokens, heads, head_dim, tile_h, tile_w, csr.row_ptr.data_ptr(),
-            csr.col_idx.data_ptr(), entries, float(scale), int(bool(deterministic)),
+            strides, tokens, heads, head_dim, tile_h, tile_w,
+            csr.row_ptr.data_ptr() if csr is not None else None,
+            csr.col_idx.data_ptr() if csr is not None else None,
+            entries, float(scale), int(bool(deterministic)),
             lse.data_ptr(), stats["mass"].data_ptr(), stats["mass_f16"].data_ptr(),
             *[stats[name].data_ptr() if name in stats else None for name in names],
             workspace.data_ptr() if workspace is not None else None, workspace_bytes,

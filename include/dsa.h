@@ -183,27 +183,33 @@ int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const int64_t* s
                    void* centroid_k_x, hipStream_t stream);
 
 /*
- * One routed step of the matrix-sparse backend: block-sparse attention over
- * spatial tiles together with that attention's tile statistics.  Replaces
- * `sparse_chunk` (attention_backends/sparse.py:670-751: output plus the
- * statistics of the same softmax) and `_sparse_stats_kernel`
- * (sparse.py:498-578, the Triton path's second pass over QK^T).  The
+ * One step of the matrix-sparse backend: attention over spatial tiles
+ * together with that attention's tile statistics.  Replaces `sparse_chunk`
+ * (attention_backends/sparse.py:670-751: output plus the statistics of the
+ * same softmax), `_sparse_stats_kernel` (sparse.py:498-578, the Triton path's
+ * second pass over QK^T) and, with row_ptr == col_idx == NULL, the dense
+ * attention and statistics of `_dense_route` (sparse.py:184-233).  The
  * arguments are those of dsa_bsa_fwd with batch 1, q_tokens = kv_tokens =
  * tokens (tile-major, a whole number of tile_h x tile_w tiles of at most 128
- * tokens) and the CSR of the kept tiles (route_batches 1; required), and
- * those of dsa_tile_stats with lse required (written: [heads, tokens] fp32)
- * and lse_head_stride = tokens.
+ * tokens) and the CSR of the kept tiles (route_batches 1) or none, and those
+ * of dsa_tile_stats with lse required (written: [heads, tokens] fp32) and
+ * lse_head_stride = tokens.
  *   entries: at least the CSR's entry count row_ptr[heads * tiles] (the
- *            cells of entries past it read as zeros).
- * Tiles that take the gathered key stream (65..127 tokens whose 8-rounded
- * size is below the plain layout's key slots, e.g. 9 x 8) have their
- * statistics taken from the attention's own probabilities in the same launch
- * (the key-side sums on the matrix cores beside P V, per query row and key
- * tile, into the workspace), then combined per cell by a short second
- * launch; other tiles run dsa_bsa_fwd and then dsa_tile_stats.
+ *            cells of entries past it read as zeros); dense: at least
+ *            heads * tiles * tiles for tiles of 72..128 tokens, a multiple
+ *            of 8.
+ * The statistics come from the attention's own probabilities in the same
+ * launch (the key-side sums on the matrix cores beside P V, per query row
+ * and key tile, into the workspace), combined per cell by a short second
+ * launch, when the call is routed and its tiles take the gathered key stream
+ * (65..127 tokens whose 8-rounded size is below the plain layout's key
+ * slots, e.g. 9 x 8), or dense with tiles of 72..128 tokens, a multiple of
+ * 8 (the attention then runs on 128-token blocks, unsplit).  Other calls run
+ * dsa_bsa_fwd and then dsa_tile_stats.
  *   workspace: dsa_bsa_fwd_tile_stats_workspace_bytes(...) bytes, 16-byte
- *            aligned: entries * tile * 8 bytes of per-row statistics when
- *            fused (rounded up to 256), then dsa_bsa_fwd's workspace.
+ *            aligned: entries * tile * 8 bytes of per-row statistics for
+ *            tiles of 65..128 tokens (rounded up to 256), then dsa_bsa_fwd's
+ *            workspace.
  */
 int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                            const int64_t* strides, int32_t tokens, int32_t heads,

@@ -205,6 +205,29 @@ def test_fused_step_matches_two_pass_and_oracle(ops, cuda_device, grid, tile, de
                                rtol=2e-3)
 
 
+@pytest.mark.parametrize("grid,tile", [((2, 18, 32), 64), ((2, 15, 26), 64), ((1, 20, 30), 100),
+                                       ((2, 16, 32), 128), ((4, 16, 16), 64)])
+def test_fused_dense_step_matches_oracle(ops, cuda_device, grid, tile):
+    """The dense bootstrap through dsa_bsa_fwd_tile_stats (no CSR): 9 x 8
+    and 8 x 16 tiles take their statistics from the dense attention launch
+    (128-token blocks, unsplit); 5 x 13 and 10 x 10 (not a multiple of 8) and
+    8 x 8 tiles run the second pass; all against the oracle's _dense_route
+    statistics and output."""
+    case, q, k, v = _tile_major_inputs(grid, 3, seed=sum(grid) + 1, tile=tile)
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    out, lse, got = ops.bsa_fwd_tile_stats(qd, kd, vd, None, case.tile_shape)
+    ref_out, ref_lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out) or (out.float() - ref_out.float()).abs().max().item() <= 8e-3
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse.cpu().numpy(), atol=1e-4)
+    expected, expected_out = _oracle_stats(case, q, k, v)
+    _compare_stats(got, expected)
+    metrics = A.summarize(out.float().cpu().numpy(), expected_out)
+    assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
+    np.testing.assert_allclose(got["mass"].sum(-1).cpu().numpy(), case.tile / q.shape[1],
+                               rtol=2e-3)
+
+
 def test_fused_step_at_720p_tile_shape(ops, cuda_device):
     """The bench's 720p matrix-sparse step shape (9 x 8 tiles, 800 tiles
     per head) at 4 heads: fused statistics against the two-pass statistics on
