@@ -101,14 +101,15 @@ int launch(int32_t dtype, BsaParams p, void* scratch, size_t scratch_bytes, hipS
 
 }  // namespace
 
-// Scratch of dsa_bsa_fwd_noalloc: the launch order of up to kMaxOrderItems
-// work items (1 MiB) and the aligned-walk table (4 KiB), then kMaxPartGroups
-// split partials (68,157,440 bytes).
+// Scratch of dsa_bsa_fwd_noalloc: the work-queue counter (256 bytes), the
+// launch order of up to kMaxOrderItems work items (1 MiB) and the
+// aligned-walk table (4 KiB), then kMaxPartGroups split partials (68,157,440
+// bytes).
 // Every device the library runs on holds its own copy until the process
 // ends; host code reaches it only through the address hipGetSymbolAddress
 // returns on that device (scratch_on).
-constexpr size_t kScratchBytes = (size_t)kMaxOrderItems * sizeof(int32_t) + kWalkBytes +
-                                 (size_t)kMaxPartGroups * kPartBytes;
+constexpr size_t kScratchBytes = kQueueBytes + (size_t)kMaxOrderItems * sizeof(int32_t) +
+                                 kWalkBytes + (size_t)kMaxPartGroups * kPartBytes;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {

@@ -63,6 +63,7 @@ struct BsaParams {
   const int32_t* row_ptr;  // null: every key block (dense)
   const int32_t* col_idx;
   const int32_t* order;    // routed: work item of each launch slot (null: identity)
+  int32_t* queue;          // work-queue counter, zero at launch (null: slot = blockIdx.x)
   uint64_t* walk;          // routed: aligned-walk position table (null: plain walk)
   int32_t batch, heads, q_tokens, kv_tokens, q_blocks, kv_blocks, route_batches;
   int32_t block;     // tokens per query block and per key block (1..128)
@@ -248,7 +249,23 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // the dense heads working alone), and `order` (launch_order_kernel) puts
   // each head's rows longest first, so the workgroups resident side by side
   // run rows of similar length and stay in step through the L2.
-  const int wg = (int)blockIdx.x;
+  //
+  // With a work queue, each workgroup takes the next launch slot from a
+  // counter when it starts, rather than the slot of its dispatch index: the
+  // dispatcher deals workgroups to the XCDs round-robin, and the XCDs do not
+  // run equally fast (on one box the odd ones took 5% longer over the same
+  // work), so fixed slots leave the fast XCDs idle at the end.  Slots are then
+  // taken in start order across the whole chip (dense calls walk them in
+  // order: all XCDs read one head's keys at a time).  A row's result does not
+  // depend on which workgroup computes it.
+  int wg = (int)blockIdx.x;
+  if (p.queue != nullptr) {
+    __shared__ int wg_lds;
+    if (tid == 0)
+      wg_lds = __hip_atomic_fetch_add(p.queue, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    wg = __builtin_amdgcn_readfirstlane(wg_lds);
+  }
   const bool split = wg >= p.split_from;
   int slot = wg, part = 0;
   if (split) {
@@ -258,7 +275,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   }
   int work = slot;
   if (kRouted && p.order) work = ((dsa_const_i32)p.order)[slot];
-  else if (!kRouted && !split) work = dsa::xcd_remap(wg, p.split_from);
+  else if (!kRouted && !split && !p.queue) work = dsa::xcd_remap(wg, p.split_from);
   const int qb = work % p.q_blocks;
   const int bh = work / p.q_blocks;
   const int h = bh % p.heads;
@@ -780,13 +797,16 @@ constexpr int kMaxOrderBlocks = 8192;     // query blocks per (batch, head) grou
 constexpr int64_t kMaxOrderItems = 262144;  // work items per call (1 MiB of order)
 
 // Internal linkage: each translation unit that launches it has its own copy.
+// Workgroup 0 also clears the work-queue counter (when there is one).
 static __global__ void __launch_bounds__(256) launch_order_kernel(const int32_t* row_ptr,
                                                            int32_t* order, int32_t heads,
                                                            int32_t q_blocks,
-                                                           int32_t route_batches, int32_t n) {
+                                                           int32_t route_batches, int32_t n,
+                                                           int32_t* queue) {
   __shared__ uint64_t keys[kMaxOrderBlocks];
   const int tid = threadIdx.x;
   const int bh = blockIdx.x;
+  if (queue != nullptr && bh == 0 && tid == 0) queue[0] = 0;
   const int rb = route_batches == 1 ? 0 : bh / heads;
   const int32_t* rp = row_ptr + ((int64_t)rb * heads + bh % heads) * q_blocks;
   for (int i = tid; i < n; i += 256) {
@@ -816,12 +836,20 @@ static __global__ void __launch_bounds__(256) launch_order_kernel(const int32_t*
     order[base + i] = base + (int32_t)~(uint32_t)keys[i];
 }
 
-// Bytes of the launch order of a routed call of `items` work items, rounded
-// up to 256, plus the aligned-walk table after it (0 when the call is not
-// ordered).
+constexpr size_t kQueueBytes = 256;
+
+// Clears the work-queue counter of a call that has no launch order kernel.
+static __global__ void __launch_bounds__(64) queue_reset_kernel(int32_t* queue) {
+  if (threadIdx.x == 0) queue[0] = 0;
+}
+
+// Bytes at the front of a call's scratch: the work-queue counter (256), the
+// launch order of `items` work items rounded up to 256, and the aligned-walk
+// table; 0 when the call has too many items to order (it then runs in
+// dispatch order without a queue).
 inline size_t order_bytes(int64_t items, int32_t q_blocks) {
   if (items > kMaxOrderItems || q_blocks > kMaxOrderBlocks) return 0;
-  return (((size_t)items * sizeof(int32_t) + 255) & ~(size_t)255) + kWalkBytes;
+  return kQueueBytes + (((size_t)items * sizeof(int32_t) + 255) & ~(size_t)255) + kWalkBytes;
 }
 
 // Combines the `parts` partials of each split query block: with M the largest
@@ -964,8 +992,9 @@ inline bool use_gather(int32_t block, int32_t kv_tokens, int64_t k_token_stride,
 }
 
 // Launches a prepared call.  `scratch` (null when `scratch_bytes` is 0)
-// holds, for a routed call, the launch order first (order_bytes, when there
-// is room for it), then the split partials of the last round.
+// holds, when there is room for them (order_bytes), the work-queue counter
+// and, for a routed call, the launch order and the aligned-walk table; then
+// the split partials of the last round.
 template <typename T>
 int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
                  const char* who) {
@@ -973,21 +1002,28 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
   size_t used = 0;
   p.order = nullptr;
   p.walk = nullptr;
-  if (p.row_ptr) {
-    const size_t need = order_bytes(grid, p.q_blocks);
-    if (need > 0 && scratch_bytes >= need) {
-      int32_t* order = static_cast<int32_t*>(scratch);
+  p.queue = nullptr;
+  const size_t lead = order_bytes(grid, p.q_blocks);
+  if (lead > 0 && scratch_bytes >= lead) {
+    unsigned char* base = static_cast<unsigned char*>(scratch);
+    used = lead;
+    // Calls of more than one round of workgroups take their slots from the
+    // work queue.
+    if (grid > device_slots(stream)) p.queue = reinterpret_cast<int32_t*>(base);
+    if (p.row_ptr) {
+      int32_t* order = reinterpret_cast<int32_t*>(base + kQueueBytes);
       p.order = order;
-      used = need;
       // The walk table needs no clearing: stale entries are too old to count
       // and any entry only moves where a row's walk starts.
       if (!p.deterministic && p.kv_blocks <= kWalkMaxBlocks)
-        p.walk = reinterpret_cast<uint64_t*>(static_cast<unsigned char*>(scratch) + need -
-                                             kWalkBytes);
+        p.walk = reinterpret_cast<uint64_t*>(base + lead - kWalkBytes);
       int n = 2;
       while (n < p.q_blocks) n <<= 1;
       hipLaunchKernelGGL(launch_order_kernel, dim3((unsigned)(p.batch * p.heads)), dim3(256), 0,
-                         stream, p.row_ptr, order, p.heads, p.q_blocks, p.route_batches, n);
+                         stream, p.row_ptr, order, p.heads, p.q_blocks, p.route_batches, n,
+                         p.queue);
+    } else if (p.queue) {
+      hipLaunchKernelGGL(queue_reset_kernel, dim3(1), dim3(64), 0, stream, p.queue);
     }
   }
   float* part = reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + used);

@@ -68,12 +68,15 @@ const char* dsa_last_error(void);
  *                always reproducible.
  *   lse: optional [batch, heads, q_tokens] fp32 natural-log LSE, or NULL.
  *   workspace: optional device scratch (NULL with workspace_bytes == 0, or
- *                16-byte aligned).  A routed call first takes the launch
- *                order of its query blocks from it (batch * heads * q_blocks
- *                int32, rounded up to 256 bytes, then 4,096 bytes of
- *                aligned-walk positions; only with q_blocks <= 8,192 and at
- *                most 262,144 blocks in all): each (batch, head)'s
- *                blocks, longest row first.  The rest holds the fp32 partials
+ *                16-byte aligned).  Its front (only with q_blocks <= 8,192
+ *                and at most 262,144 blocks in all) holds a 256-byte work
+ *                queue, from which the workgroups of a call of more than one
+ *                round take their slots in start order (the XCDs do not run
+ *                equally fast), then the launch order of the query blocks
+ *                (batch * heads * q_blocks int32, rounded up to 256 bytes;
+ *                routed calls: each (batch, head)'s blocks, longest row
+ *                first) and 4,096 bytes of aligned-walk positions.  The rest
+ *                holds the fp32 partials
  *                of the query blocks in the last, partial round of workgroups
  *                (two per CU of the stream's device), which then run as 2..8
  *                key ranges merged by a second launch: at most rest / 66,560
@@ -93,8 +96,9 @@ int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, int32_t dt
 
 /* Workspace bytes that let a self-attention dsa_bsa_fwd with 128-token
  * blocks order its launch and split its last round as far as it ever does:
- * the launch order (batch * heads * kv_blocks int32 rounded up to 256, plus
- * 4,096 bytes of aligned-walk positions, or 0 where the call is not ordered)
+ * the front (256 bytes of work queue, batch * heads * kv_blocks int32 of
+ * launch order rounded up to 256, and 4,096 bytes of aligned-walk positions;
+ * 0 where the call is not ordered)
  * plus 68,157,440 (1,024 partials of 128 x 130 fp32) when the key range holds
  * at least 16 blocks (two parts of at least 8 key blocks each; none
  * otherwise, e.g. over 512 text tokens); 0 for invalid sizes.  No counterpart in the reference, whose FlexAttention
@@ -112,15 +116,17 @@ size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_to
  * that forbid hipMalloc).  No counterpart in the reference.  Same arguments,
  * semantics and results as dsa_bsa_fwd given a workspace of
  * dsa_bsa_workspace_bytes_block() bytes; it calls no hipMalloc / hipFree.  The
- * launch order, the aligned-walk positions and the split partials live in a
- * library-owned device array of 69,210,112 bytes (1 MiB of order, 4 KiB of
- * positions, then 1,024 partials of 128 x 130 fp32), one per device the
+ * work queue, the launch order, the aligned-walk positions and the split
+ * partials live in a library-owned device array of 69,210,368 bytes (256
+ * bytes of queue, 1 MiB of order, 4 KiB of positions, then 1,024 partials of
+ * 128 x 130 fp32), one per device the
  * library runs on, held until the process ends; no call ever needs more, so
  * no call size is refused for want of scratch.  Every call on a device
  * shares that device's array: calls that overlap on one device (on
  * different streams) race; calls ordered on one stream do not.  Nothing in
- * the array needs clearing: a call writes every order entry and partial it
- * reads, and a stale walk position only moves where a row's walk starts.
+ * the array needs clearing: a call clears its queue and writes every order
+ * entry and partial it reads, and a stale walk position only moves where a
+ * row's walk starts.
  */
 int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                         const int64_t* strides, int32_t batch, int32_t q_tokens,

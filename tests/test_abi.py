@@ -37,14 +37,14 @@ def test_header_symbols_are_exported_and_bound(lib):
 
 def test_version_and_workspace_size(lib):
     assert lib.dsa_version() == 1
-    # The workspace holds the launch order of a routed call (4 bytes per
-    # (batch, head, query block) work item, rounded up to 256) and the
-    # aligned-walk table (8 XCDs x 64 entries of 8 bytes), then the split
-    # partials of the last round, 1,024 workgroups of 128 x (128 + 2) fp32,
-    # when the key range can be split (at least 16 key blocks, 2 parts of 8).
-    # V is read in place.
+    # The workspace holds the work-queue counter (256 bytes), the launch order
+    # of a routed call (4 bytes per (batch, head, query block) work item,
+    # rounded up to 256) and the aligned-walk table (8 XCDs x 64 entries of 8
+    # bytes), then the split partials of the last round, 1,024 workgroups of
+    # 128 x (128 + 2) fp32, when the key range can be split (at least 16 key
+    # blocks, 2 parts of 8).  V is read in place.
     def order(items):
-        return (items * 4 + 255) // 256 * 256 + 8 * 64 * 8
+        return 256 + (items * 4 + 255) // 256 * 256 + 8 * 64 * 8
 
     split = 1024 * (128 * 128 + 256) * 4
     assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == order(2 * 12 * 256) + split
