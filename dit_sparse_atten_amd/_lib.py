@@ -85,6 +85,13 @@ SIGNATURES = {
     "dsa_bsa_fwd_tile_stats_workspace_bytes": (_c_size, (
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,  # heads, tokens, head_dim, tile_h, tile_w, entries
     )),
+    "dsa_bsa_fwd_block_mass": (_c_int, (
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,  # q, k, v, o, dtype
+        ctypes.POINTER(_c_i64),                    # strides[12]
+        _c_int, _c_int, _c_int, _c_float,          # tokens, heads, head_dim, scale
+        _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr,   # lse, mass, workspace, workspace_bytes, stream
+    )),
+    "dsa_bsa_fwd_block_mass_workspace_bytes": (_c_size, (_c_int, _c_int, _c_int)),
     "dsa_route_select": (_c_int, (
         _c_ptr, _c_ptr, _c_int, _c_int,            # mass, previous, rows, keys
         _c_float, _c_float, _c_int, _c_int,        # rho, target, cap, sink_blocks

@@ -103,13 +103,22 @@ def _sampled_block_mass(q, k, block_size, samples=2, scale=None, query_block_chu
     return ops.sampled_block_mass(q, k, block_size, samples, scale)
 
 
+def _dense_with_block_mass(q, k, v, block_size, scale=None):
+    """Dense output and its exact block mass (flex.py:254-272 then 158-202),
+    in one attention launch for 128-token blocks."""
+    if block_size == 128 and q.shape[0] == 1 and q.shape[1] == k.shape[1]:
+        output, _, mass = ops.bsa_fwd_block_mass(q, k, v, scale=scale)
+        return output, mass
+    output, lse = ops.bsa_fwd(q, k, v, scale=scale, return_lse=True)
+    return output, _block_attention_mass(q, k, lse, block_size, scale=scale)
+
+
 def _dense_bootstrap(q, k, v, block_size, mass_target, keep, compile_kernel, scale=None):
     """Return exact dense output and its block-quantized top-mass route."""
     del compile_kernel
     if q.shape[0] != 1 or q.shape[1] != k.shape[1]:
         raise ValueError("Flex bootstrap supports batch-1 self-attention")
-    output, lse = ops.bsa_fwd(q, k, v, scale=scale, return_lse=True)
-    mass = _block_attention_mass(q, k, lse, block_size, scale=scale)
+    output, mass = _dense_with_block_mass(q, k, v, block_size, scale)
     return output, _top_mass_route(mass, mass_target, keep)
 
 
@@ -465,10 +474,9 @@ class FlexReuseBackend:
             }
             self.state[key] = state
             if self.config.bootstrap_mode == "exact":
-                # Dense output with its LSE, then one exact block-mass pass.
-                output, lse = ops.bsa_fwd(q, k, v, scale=softmax_scale, return_lse=True)
-                mass = _block_attention_mass(q, k, lse, self.config.block_size,
-                                             scale=softmax_scale)
+                # Dense output with its exact block mass.
+                output, mass = _dense_with_block_mass(q, k, v, self.config.block_size,
+                                                      softmax_scale)
                 self._install_route(state, self._exact_route(state, mass), q.shape[1])
                 self._update_dispatch(state)
                 self.phase_counts["dense_bootstrap"] += 1
@@ -492,8 +500,8 @@ class FlexReuseBackend:
         if (self.config.update_interval > 0
                 and (step - state["step"]) >= self.config.update_interval
                 and not self._is_final_step(step)):
-            output, lse = ops.bsa_fwd(q, k, v, scale=softmax_scale, return_lse=True)
-            mass = _block_attention_mass(q, k, lse, self.config.block_size, scale=softmax_scale)
+            output, mass = _dense_with_block_mass(q, k, v, self.config.block_size,
+                                                  softmax_scale)
             state["block_mask"] = None
             self._install_route(state, self._exact_route(state, mass), q.shape[1])
             state["step"] = step

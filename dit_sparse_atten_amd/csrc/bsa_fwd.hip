@@ -167,6 +167,7 @@ struct ReduceParams {
   __half* ckx;
   int32_t tokens, tiles, tile, tile_h, tile_w;
   int32_t dense;  // 1: every key tile, rows at (h * tiles + kt) * tokens + token
+  int32_t raw;    // 1: mass32 holds the plain sum (the exact block mass), not sum / tokens
 };
 
 __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) {
@@ -217,7 +218,7 @@ __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) 
     kx = dsa::wave_total(kx);
     if (lane == 0) {
       const int64_t cell = cell0 + kt;
-      const float normalized = m / (float)p.tokens;
+      const float normalized = p.raw ? m : m / (float)p.tokens;
       const float den = fmaxf(m, 1e-12f);
       p.mass32[cell] = normalized;
       if (p.mass16) p.mass16[cell] = __float2half(normalized);
@@ -396,7 +397,78 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
   r.tile_h = tile_h;
   r.tile_w = tile_w;
   r.dense = dense ? 1 : 0;
+  r.raw = 0;
   hipLaunchKernelGGL(tile_stats_reduce_kernel, dim3((unsigned)(heads * tiles)), dim3(256), 0,
+                     stream, r);
+  return dsa::check_launch(who);
+}
+
+extern "C" size_t dsa_bsa_fwd_block_mass_workspace_bytes(int32_t heads, int32_t tokens,
+                                                         int32_t head_dim) {
+  if (heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
+  const size_t attention = dsa_bsa_workspace_bytes_block(1, heads, tokens, head_dim, 128);
+  if (tokens % 128 != 0) return attention;
+  const int64_t blocks = tokens / 128;
+  return attention + row_stats_bytes((int64_t)heads * blocks * blocks, 128);
+}
+
+extern "C" int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* v, void* o,
+                                      int32_t dtype, const int64_t* strides, int32_t tokens,
+                                      int32_t heads, int32_t head_dim, float scale, float* lse,
+                                      float* mass, void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
+  const char* who = "dsa_bsa_fwd_block_mass";
+  dsa::clear_error();
+  if (!lse || !mass || !strides)
+    return dsa::set_error(DSA_EINVAL, "%s: lse, mass and strides are required", who);
+  BsaParams p;
+  int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim, 128,
+                       nullptr, nullptr, 1, scale, 0, 1, lse, who, &p);
+  if (status != DSA_OK) return status;
+  if (workspace_bytes > 0 && (!workspace || !aligned16(workspace)))
+    return dsa::set_error(DSA_EINVAL, "%s: workspace must be 16-byte aligned", who);
+  const size_t need = dsa_bsa_fwd_block_mass_workspace_bytes(heads, tokens, head_dim);
+  if (workspace_bytes < need)
+    return dsa::set_error(DSA_EINVAL, "%s: workspace of %zu bytes, %zu needed", who,
+                          workspace_bytes, need);
+  unsigned char* base = static_cast<unsigned char*>(workspace);
+  if (tokens % 128 != 0) {
+    // A partial last block: the dense attention, then the block-mass pass.
+    status = launch(dtype, p, base, workspace_bytes, stream, who);
+    if (status != DSA_OK) return status;
+    const int64_t mass_strides[4] = {strides[1], strides[2], strides[4], strides[5]};
+    return dsa_block_mass(q, k, dtype, mass_strides, tokens, heads, head_dim, 128, lse, tokens,
+                          scale, mass, stream);
+  }
+  const int32_t blocks = tokens / 128;
+  const int64_t entries = (int64_t)heads * blocks * blocks;
+  const size_t rs = row_stats_bytes(entries, 128);
+  p.rs_logm = reinterpret_cast<float*>(base);
+  p.rs_mean = reinterpret_cast<uint32_t*>(base + (size_t)entries * 128 * sizeof(float));
+  p.rs_entries = entries;
+  p.tile_h = 1;
+  p.tile_w = 128;
+  p.stat_tile = 128;
+  p.stat_pad = 128;
+  status = launch(dtype, p, base + rs, workspace_bytes - rs, stream, who);
+  if (status != DSA_OK) return status;
+  ReduceParams r;
+  r.rs_logm = p.rs_logm;
+  r.rs_mean = p.rs_mean;
+  r.entries = entries;
+  r.lse = lse;
+  r.row_ptr = nullptr;
+  r.col_idx = nullptr;
+  r.mass32 = mass;
+  r.mass16 = r.cqy = r.cqx = r.cky = r.ckx = nullptr;
+  r.tokens = tokens;
+  r.tiles = blocks;
+  r.tile = 128;
+  r.tile_h = 1;
+  r.tile_w = 128;
+  r.dense = 1;
+  r.raw = 1;
+  hipLaunchKernelGGL(tile_stats_reduce_kernel, dim3((unsigned)(heads * blocks)), dim3(256), 0,
                      stream, r);
   return dsa::check_launch(who);
 }

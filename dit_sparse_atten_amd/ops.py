@@ -270,6 +270,47 @@ def block_mass(q, k, lse, block_size=128, scale=None):
     return mass
 
 
+def bsa_fwd_block_mass(q, k, v, scale=None):
+    """Dense attention of batch-1 self-attention q/k/v [1, T, H, D] with its
+    exact 128-token block mass: returns ``(out, lse, mass)`` with ``out`` and
+    ``lse`` [1, H, T] as :func:`bsa_fwd` returns them and ``mass`` as
+    :func:`block_mass` does (the reference's ``_dense_bootstrap`` pair of
+    dense attention and ``_block_attention_mass``, attention_backends/
+    flex.py:254-272, 158-202).  With T a multiple of 128 the mass comes from
+    the attention launch's own probabilities; otherwise the call runs the
+    attention and then the block-mass pass.
+    """
+    lib = _lib.load()
+    q = _kernel_view("q", q)
+    k = _kernel_view("k", k, q.dtype)
+    v = _kernel_view("v", v, q.dtype)
+    batch, tokens, heads, head_dim = q.shape
+    if batch != 1 or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("Flex bootstrap supports batch-1 self-attention")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q, k and v must be on the same device")
+    if scale is None:
+        scale = head_dim ** -0.5
+    blocks = math.ceil(tokens / 128)
+    out = torch.empty((1, tokens, heads, head_dim), dtype=q.dtype, device=q.device)
+    lse = torch.empty((1, heads, tokens), dtype=torch.float32, device=q.device)
+    mass = torch.empty((heads, blocks, blocks), dtype=torch.float32, device=q.device)
+    strides = _lib.int64_array(
+        list(q.stride()[:3]) + list(k.stride()[:3]) + list(v.stride()[:3])
+        + list(out.stride()[:3]))
+    workspace_bytes = lib.dsa_bsa_fwd_block_mass_workspace_bytes(heads, tokens, head_dim)
+    workspace = (torch.empty(workspace_bytes, dtype=torch.uint8, device=q.device)
+                 if workspace_bytes else None)
+    with torch.cuda.device(q.device):
+        status = lib.dsa_bsa_fwd_block_mass(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dtype_code(q.dtype),
+            strides, tokens, heads, head_dim, float(scale), lse.data_ptr(), mass.data_ptr(),
+            workspace.data_ptr() if workspace is not None else None, workspace_bytes,
+            _stream_handle(q.device))
+    _lib.check(status, "dsa_bsa_fwd_block_mass")
+    return out, lse, mass
+
+
 def tile_stats(q, k, lse, tile_shape, csr=None, scale=None, centroids=True):
     """Spatial-tile attention statistics of tile-major q/k [1, T, H, 128].
 

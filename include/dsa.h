@@ -232,6 +232,32 @@ size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t tokens, int
                                               int32_t tile_h, int32_t tile_w, int64_t entries);
 
 /*
+ * Dense attention with its exact block mass, for the exact route estimate:
+ * the reference's `_dense_bootstrap` / exact refresh pair of a dense
+ * FlexAttention with `return_lse=True` (attention_backends/flex.py:254-272,
+ * 776-801) and `_block_attention_mass` (flex.py:158-202).  The arguments are
+ * those of dsa_bsa_fwd for a dense batch-1 self-attention (q_tokens =
+ * kv_tokens = tokens), with lse required (written: [heads, tokens] fp32) and
+ * mass [heads, blocks, blocks] fp32 (blocks = ceil(tokens / 128)): the sum of
+ * exp(scale * <q, k> - lse) over each pair of 128-token blocks, as
+ * dsa_block_mass writes it.  When tokens is a multiple of 128 the mass comes
+ * from the attention launch's own probabilities (the key-side sums beside P V
+ * per query row and key block, then a short second launch); otherwise the
+ * call runs the attention and then dsa_block_mass.
+ *   workspace: dsa_bsa_fwd_block_mass_workspace_bytes(...) bytes, 16-byte
+ *            aligned: heads * blocks^2 * 128 * 8 bytes of per-row sums when
+ *            fused (rounded up to 256), then dsa_bsa_fwd's workspace.
+ */
+int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* v, void* o, int32_t dtype,
+                           const int64_t* strides, int32_t tokens, int32_t heads,
+                           int32_t head_dim, float scale, float* lse, float* mass,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes dsa_bsa_fwd_block_mass needs (0 for invalid sizes).  No
+ * counterpart in the reference. */
+size_t dsa_bsa_fwd_block_mass_workspace_bytes(int32_t heads, int32_t tokens, int32_t head_dim);
+
+/*
  * Persistence prior + top-mass selection + first-frame sink, per row.
  * Replaces the prior of `_sampled_route` (flex.py:535-541), `_top_mass_route`
  * (flex.py:83-94, == sparse.py:171-181 `_row_mask`) and `_add_first_frame_sink`

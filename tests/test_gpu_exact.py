@@ -63,6 +63,31 @@ def test_block_mass_matches_oracle(ops, cuda_device, tokens):
     np.testing.assert_allclose(got.sum(-1), np.broadcast_to(valid, got.shape[:2]), rtol=1e-4)
 
 
+@pytest.mark.parametrize("tokens", [128, 1024, 1000])
+def test_dense_with_block_mass_matches_oracle(ops, cuda_device, tokens):
+    """dsa_bsa_fwd_block_mass: the dense output, its LSE and the exact block
+    mass in one call (fused for whole 128-token blocks, the separate pass for
+    1,000 tokens) against the oracle and the two-call path."""
+    q, k, v = _inputs(tokens, 3, seed=11 + tokens, group=64)
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    out, lse, mass = ops.bsa_fwd_block_mass(qd, kd, vd)
+    ref_out, ref_lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
+    ref_mass = ops.block_mass(qd, kd, ref_lse)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse.cpu().numpy(), atol=LSE_ATOL)
+    assert (out.float() - ref_out.float()).abs().max().item() <= 8e-3
+    expected = E.exact_block_mass(q.float().numpy(), k.float().numpy(),
+                                  lse[0].cpu().numpy(), 128)
+    # P enters the fused sums in bf16, as it enters P V (unbiased rounding,
+    # at most 2^-9 per term).
+    np.testing.assert_allclose(mass.cpu().numpy(), expected, rtol=5e-4, atol=MASS_ATOL)
+    np.testing.assert_allclose(mass.cpu().numpy(), ref_mass.cpu().numpy(), rtol=5e-4,
+                               atol=MASS_ATOL)
+    valid = np.minimum(128, tokens - 128 * np.arange(mass.shape[1]))
+    np.testing.assert_allclose(mass.sum(-1).cpu().numpy(),
+                               np.broadcast_to(valid, mass.shape[:2]), rtol=2e-4)
+
+
 def test_block_mass_explicit_softmax_reference_test(ops, cuda_device):
     """tests/test_flex_backend.py:78-99 at head_dim 128: 250 tokens, 2 heads;
     LSE from an fp32 logsumexp rather than the attention kernel."""
