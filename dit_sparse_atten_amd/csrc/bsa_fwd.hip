@@ -102,14 +102,15 @@ int launch(int32_t dtype, BsaParams p, void* scratch, size_t scratch_bytes, hipS
 }  // namespace
 
 // Scratch of dsa_bsa_fwd_noalloc: the work-queue counter (256 bytes), the
-// launch order of up to kMaxOrderItems work items (1 MiB) and the
-// aligned-walk table (4 KiB), then kMaxPartGroups split partials (68,157,440
-// bytes).
+// launch order of up to kMaxOrderItems work items (1 MiB), the aligned-walk
+// table (4 KiB) and the key-norm maxima of up to kMaxNormPairs (batch, head)
+// pairs (1 MiB), then kMaxPartGroups split partials (68,157,440 bytes).
 // Every device the library runs on holds its own copy until the process
 // ends; host code reaches it only through the address hipGetSymbolAddress
 // returns on that device (scratch_on).
 constexpr size_t kScratchBytes = kQueueBytes + (size_t)kMaxOrderItems * sizeof(int32_t) +
-                                 kWalkBytes + (size_t)kMaxPartGroups * kPartBytes;
+                                 kWalkBytes + (size_t)kMaxNormPairs * kNormParts * sizeof(float) +
+                                 (size_t)kMaxPartGroups * kPartBytes;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {
@@ -247,7 +248,8 @@ extern "C" size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads,
   const int32_t kv_blocks = (kv_tokens + block_size - 1) / block_size;
   // Routed calls are self-attention (q_tokens == kv_tokens): batch x heads x
   // kv_blocks work items to order.
-  const size_t order = order_bytes((int64_t)batch * heads * kv_blocks, kv_blocks);
+  const size_t order =
+      order_bytes((int64_t)batch * heads * kv_blocks, kv_blocks, (int64_t)batch * heads);
   return order + (max_parts_for(kv_blocks) >= 2 ? (size_t)kMaxPartGroups * kPartBytes : 0);
 }
 

@@ -65,6 +65,10 @@ struct BsaParams {
   const int32_t* order;    // routed: work item of each launch slot (null: identity)
   int32_t* queue;          // work-queue counter, zero at launch (null: slot = blockIdx.x)
   uint64_t* walk;          // routed: aligned-walk position table (null: plain walk)
+  // Per (batch, head): kNormParts maxima of the key norms over consecutive
+  // token ranges, from key_norm_kernel (null: every half-tile takes its row
+  // max).
+  const float* kv_norm;
   int32_t batch, heads, q_tokens, kv_tokens, q_blocks, kv_blocks, route_batches;
   int32_t block;     // tokens per query block and per key block (1..128)
   int32_t head_dim;  // 8..128, a multiple of 8; dims past it are zero in the stages
@@ -110,6 +114,13 @@ using dsa::make_rsrc;
 typedef dsa::const_i32 dsa_const_i32;
 
 constexpr float kRescaleLog2 = 8.0f;  // move the max once p could exceed 2^8
+// Half-tiles whose scores provably stay within 2^kBoundLog2 of the reference
+// max (key-norm bound) skip the row max: p <= 2^32 leaves fp32 sums and O
+// accumulators of up to 2^20 keys finite for |v| < 2^76.
+constexpr float kBoundLog2 = 32.0f;
+constexpr float kRaiseLog2 = 16.0f;
+constexpr int kNormParts = 64;        // key-norm maxima per (batch, head), one per lane
+constexpr int64_t kMaxNormPairs = 4096;  // (batch, head) pairs with norms (1 MiB)
 
 // V stage [64 keys][128 dims], row-major like K: the 16-byte chunk c of key
 // row r sits at chunk position c ^ v_swz_mask(r), masks 0, 6, 10, 12 for
@@ -229,6 +240,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   typedef typename E::x8 x8;
   static_assert(!kStats || (kRouted && kGather) || (!kRouted && kNh == 2 && !kSkip && !kGather),
                 "fused statistics: the gathered stream or dense 128-token blocks");
+  // The key-norm bound (compute) in the instances with registers to spare:
+  // in the gathered and sub-tile-skipping ones the extra live value makes the
+  // register allocator copy the O accumulators around the rescale branch.
+  constexpr bool kNormBound = !kGather && !kSkip;
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
@@ -333,6 +348,25 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   const T* qrow = static_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh + (int64_t)tq_c * p.q_st;
   x8 qf[8];
   dsa::load_q_fragments(qrow, g, p.head_dim, qf);
+  // Key-norm bound of the lane's row: |scale_log2 s| <= |scale_log2| |q| kmax
+  // (Cauchy-Schwarz) over every key of the (batch, head), with kmax the
+  // largest key norm (from its kNormParts partial maxima, one per lane) and
+  // |q| from the row's fragments (lanes l and l ^ 32 hold its two halves),
+  // rounded up.  thr = bound - kBoundLog2 (+inf without norms): while the
+  // reference max m_run >= thr, no p of the row can exceed 2^kBoundLog2.
+  float thr = INFINITY;
+  if (kNormBound && p.kv_norm != nullptr) {
+    float kmax = p.kv_norm[(int64_t)bh * kNormParts + lane];
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) kmax = fmaxf(kmax, __shfl_xor(kmax, m));
+    float qq = 0.f;
+#pragma unroll
+    for (int dc = 0; dc < 8; ++dc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[dc][e], (float)qf[dc][e], qq);
+    const float qn = sqrtf(dsa::pair32_sum(qq)) * fabsf(p.scale_log2) * 1.0001f;
+    thr = fmaf(qn, kmax, -kBoundLog2);
+  }
 
   const T* kbase = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh;
   const T* vbase = static_cast<const T*>(p.v) + b * p.v_sb + h * p.v_sh;
@@ -506,32 +540,49 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         }
       }
     } else if (valid < NKT * 32 || lim < NKT * 32) {
-      const int bound = min(valid, lim);
+      // Position 32 kt + 8 (r >> 2) + 4 g + (r & 3) against the bound, with
+      // the lane's 4 g moved to the bound so each test is against a literal.
+      const int bound = min(valid, lim) - 4 * g;
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= bound) sacc[kt][r] = -INFINITY;
+          if (kt * 32 + 8 * (r >> 2) + (r & 3) >= bound) sacc[kt][r] = -INFINITY;
     }
-    float mx = -INFINITY;
+    // The row max only matters when the reference max may have to move: while
+    // m_run >= thr in every lane, no p of the half-tile exceeds 2^kBoundLog2
+    // and the max is not taken (a row's first half-tile, with m_run = -inf,
+    // always takes it).
+    const bool take_max = !kNormBound || __any(!(m_run >= thr));
+    if (take_max) {
+      float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < NKT; ++kt)
+      for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    mx = dsa::pair32_max(mx);
-    const float mx2 = mx * p.scale_log2;
-    const bool up = mx2 > m_run + kRescaleLog2;
-    if (__any(up)) {
-      const float alpha = up ? __builtin_amdgcn_exp2f(m_run - mx2) : 1.0f;
-      m_run = up ? mx2 : m_run;
-      l_run *= alpha;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+      mx = dsa::pair32_max(mx);
+      const float mx2 = mx * p.scale_log2;
+      float m_new = mx2 > m_run + kRescaleLog2 ? mx2 : m_run;
+      bool up = mx2 > m_run + kRescaleLog2;
+      if constexpr (kNormBound) {
+        // Raise the reference to thr when that costs this half-tile at most
+        // 2^-kRaiseLog2 of its largest p: the bound test then holds for the
+        // rest of the row.
+        if (thr > m_new && thr <= mx2 + kRaiseLog2) m_new = thr;
+        up = m_new != m_run;
+      }
+      if (__any(up)) {
+        const float alpha = up ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        m_run = m_new;
+        l_run *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+        for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-      if constexpr (kStats) {
+          for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        if constexpr (kStats) {
 #pragma unroll
-        for (int i = 0; i < 5; ++i) carry[i] *= alpha;
+          for (int i = 0; i < 5; ++i) carry[i] *= alpha;
+        }
       }
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
@@ -844,12 +895,57 @@ static __global__ void __launch_bounds__(64) queue_reset_kernel(int32_t* queue) 
 }
 
 // Bytes at the front of a call's scratch: the work-queue counter (256), the
-// launch order of `items` work items rounded up to 256, and the aligned-walk
-// table; 0 when the call has too many items to order (it then runs in
-// dispatch order without a queue).
-inline size_t order_bytes(int64_t items, int32_t q_blocks) {
+// launch order of `items` work items rounded up to 256, the aligned-walk
+// table, and the key-norm maxima of `pairs` (batch, head) pairs (none above
+// kMaxNormPairs: every half-tile then takes its row max); 0 when the call has
+// too many items to order (it then runs in dispatch order without a queue,
+// and without norms).
+inline size_t round256(size_t bytes) { return (bytes + 255) & ~(size_t)255; }
+inline size_t norm_bytes(int64_t pairs) {
+  return pairs > kMaxNormPairs ? 0 : round256((size_t)pairs * kNormParts * sizeof(float));
+}
+inline size_t order_bytes(int64_t items, int32_t q_blocks, int64_t pairs) {
   if (items > kMaxOrderItems || q_blocks > kMaxOrderBlocks) return 0;
-  return kQueueBytes + (((size_t)items * sizeof(int32_t) + 255) & ~(size_t)255) + kWalkBytes;
+  return kQueueBytes + round256((size_t)items * sizeof(int32_t)) + kWalkBytes + norm_bytes(pairs);
+}
+
+// Key-norm maxima per (batch, head): workgroup (s, bh) takes the s-th of
+// kNormParts consecutive token ranges of the head's keys, 16 lanes per key row
+// (one 16-byte chunk of 8 dims each, dims past head_dim not read), and writes
+// the largest norm of its range.  The attention kernels bound a half-tile's
+// scores by it (compute); the bound only decides whether the row max is
+// taken, so it may exceed the true largest norm but never fall below it.
+
+template <typename T>
+__global__ void __launch_bounds__(256) key_norm_kernel(BsaParams p, float* out) {
+  const int part = blockIdx.x, bh = blockIdx.y;
+  const int h = bh % p.heads, b = bh / p.heads;
+  const int tid = threadIdx.x, c = tid & 15;
+  const int per = (p.kv_tokens + kNormParts - 1) / kNormParts;
+  const int t0 = part * per, t1 = min(t0 + per, p.kv_tokens);
+  const T* kb = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh + c * 8;
+  const bool live = c * 8 < p.head_dim;
+  float best = 0.f;
+  for (int t = t0 + (tid >> 4); t < t1; t += 16) {
+    float ss = 0.f;
+    if (live) {
+      const typename dsa::Elem<T>::x8 x =
+          *reinterpret_cast<const typename dsa::Elem<T>::x8*>(kb + (int64_t)t * p.k_st);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf((float)x[e], (float)x[e], ss);
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m);
+    best = fmaxf(best, ss);
+  }
+  best = fmaxf(best, __shfl_xor(best, 16));
+  best = fmaxf(best, __shfl_xor(best, 32));
+  __shared__ float wave_max[4];
+  if ((tid & 63) == 0) wave_max[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0)
+    out[(int64_t)bh * kNormParts + part] =
+        sqrtf(fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3])));
 }
 
 // Combines the `parts` partials of each split query block: with M the largest
@@ -1003,10 +1099,24 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
   p.order = nullptr;
   p.walk = nullptr;
   p.queue = nullptr;
-  const size_t lead = order_bytes(grid, p.q_blocks);
+  p.kv_norm = nullptr;
+  const int64_t norms = (int64_t)p.batch * p.heads;
+  const size_t lead = order_bytes(grid, p.q_blocks, norms);
+  const int32_t nh = p.block > kHalfKeys ? 2 : 1;
+  // Blocks whose last half-tile holds 1..32 keys run it as one sub-tile.
+  const int rem = p.block % kHalfKeys;
+  const bool skip = rem != 0 && rem <= 32;
+  const bool gather = p.row_ptr && use_gather(p.block, p.kv_tokens, p.k_st, p.v_st);
   if (lead > 0 && scratch_bytes >= lead) {
     unsigned char* base = static_cast<unsigned char*>(scratch);
     used = lead;
+    unsigned char* const walk_end = base + lead - norm_bytes(norms);
+    if (norm_bytes(norms) > 0 && !gather && !skip) {
+      float* kv_norm = reinterpret_cast<float*>(walk_end);
+      hipLaunchKernelGGL(key_norm_kernel<T>, dim3(kNormParts, (unsigned)norms), dim3(256), 0,
+                         stream, p, kv_norm);
+      p.kv_norm = kv_norm;
+    }
     // Calls of more than one round of workgroups take their slots from the
     // work queue.
     if (grid > device_slots(stream)) p.queue = reinterpret_cast<int32_t*>(base);
@@ -1016,7 +1126,7 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
       // The walk table needs no clearing: stale entries are too old to count
       // and any entry only moves where a row's walk starts.
       if (!p.deterministic && p.kv_blocks <= kWalkMaxBlocks)
-        p.walk = reinterpret_cast<uint64_t*>(base + lead - kWalkBytes);
+        p.walk = reinterpret_cast<uint64_t*>(walk_end - kWalkBytes);
       int n = 2;
       while (n < p.q_blocks) n <<= 1;
       hipLaunchKernelGGL(launch_order_kernel, dim3((unsigned)(p.batch * p.heads)), dim3(256), 0,
@@ -1039,13 +1149,9 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
   p.part = part;
   const dim3 blocks((unsigned)(grid - split + (int64_t)split * parts)), threads(256),
       two_waves(128);
-  const int32_t nh = p.block > kHalfKeys ? 2 : 1;
-  // Blocks whose last half-tile holds 1..32 keys run it as one sub-tile.
-  const int rem = p.block % kHalfKeys;
-  const bool skip = rem != 0 && rem <= 32;
   auto four = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p); };
   auto two = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, two_waves, 0, stream, p); };
-  if (p.row_ptr && use_gather(p.block, p.kv_tokens, p.k_st, p.v_st)) {
+  if (gather) {
     if (p.rs_logm) four(bsa_fwd_kernel<T, true, 2, true, true, 4, true>);
     else four(bsa_fwd_kernel<T, true, 2, true, true>);
   } else if (p.row_ptr) {

@@ -12,6 +12,7 @@ constexpr int kHalfKeys = 64;                  // keys per pipelined half-tile
 constexpr int kKStage = kHalfKeys * kRowBytes; // 16 KB LDS stage (K or V^T)
 
 typedef const __attribute__((address_space(4))) int32_t* const_i32;
+typedef const __attribute__((address_space(4))) float* const_f32;
 
 // K stage [64 keys][128 dims]: 16-byte chunk XOR (row & 15), so the 32 rows a
 // fragment load reads at one chunk hit distinct banks.

@@ -75,7 +75,15 @@ const char* dsa_last_error(void);
  *                equally fast), then the launch order of the query blocks
  *                (batch * heads * q_blocks int32, rounded up to 256 bytes;
  *                routed calls: each (batch, head)'s blocks, longest row
- *                first) and 4,096 bytes of aligned-walk positions.  The rest
+ *                first), 4,096 bytes of aligned-walk positions, and 64 fp32
+ *                key-norm maxima per (batch, head) (rounded up to 256 bytes;
+ *                at most 4,096 pairs), written by a pre-pass over K: with
+ *                them a row skips its max on every 64-key half-tile whose
+ *                scores the Cauchy-Schwarz bound |q| max|k| keeps within 2^32
+ *                of its running reference (the same softmax; fp32 rounding
+ *                can differ in the last bits).  Not used by the gathered
+ *                stream of routed 65..127-token blocks nor by blocks whose
+ *                last half-tile holds 1..32 keys.  The rest
  *                holds the fp32 partials
  *                of the query blocks in the last, partial round of workgroups
  *                (two per CU of the stream's device), which then run as 2..8
@@ -97,8 +105,9 @@ int dsa_bsa_fwd(const void* q, const void* k, const void* v, void* o, int32_t dt
 /* Workspace bytes that let a self-attention dsa_bsa_fwd with 128-token
  * blocks order its launch and split its last round as far as it ever does:
  * the front (256 bytes of work queue, batch * heads * kv_blocks int32 of
- * launch order rounded up to 256, and 4,096 bytes of aligned-walk positions;
- * 0 where the call is not ordered)
+ * launch order rounded up to 256, 4,096 bytes of aligned-walk positions, and
+ * batch * heads * 64 fp32 of key-norm maxima rounded up to 256, none above
+ * 4,096 (batch, head) pairs; 0 where the call is not ordered)
  * plus 68,157,440 (1,024 partials of 128 x 130 fp32) when the key range holds
  * at least 16 blocks (two parts of at least 8 key blocks each; none
  * otherwise, e.g. over 512 text tokens); 0 for invalid sizes.  No counterpart in the reference, whose FlexAttention
@@ -116,17 +125,17 @@ size_t dsa_bsa_workspace_bytes_block(int32_t batch, int32_t heads, int32_t kv_to
  * that forbid hipMalloc).  No counterpart in the reference.  Same arguments,
  * semantics and results as dsa_bsa_fwd given a workspace of
  * dsa_bsa_workspace_bytes_block() bytes; it calls no hipMalloc / hipFree.  The
- * work queue, the launch order, the aligned-walk positions and the split
- * partials live in a library-owned device array of 69,210,368 bytes (256
- * bytes of queue, 1 MiB of order, 4 KiB of positions, then 1,024 partials of
- * 128 x 130 fp32), one per device the
+ * work queue, the launch order, the aligned-walk positions, the key-norm
+ * maxima and the split partials live in a library-owned device array of
+ * 70,258,944 bytes (256 bytes of queue, 1 MiB of order, 4 KiB of positions,
+ * 1 MiB of norms, then 1,024 partials of 128 x 130 fp32), one per device the
  * library runs on, held until the process ends; no call ever needs more, so
  * no call size is refused for want of scratch.  Every call on a device
  * shares that device's array: calls that overlap on one device (on
  * different streams) race; calls ordered on one stream do not.  Nothing in
  * the array needs clearing: a call clears its queue and writes every order
- * entry and partial it reads, and a stale walk position only moves where a
- * row's walk starts.
+ * entry, norm and partial it reads, and a stale walk position only moves
+ * where a row's walk starts.
  */
 int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                         const int64_t* strides, int32_t batch, int32_t q_tokens,

@@ -39,23 +39,27 @@ def test_version_and_workspace_size(lib):
     assert lib.dsa_version() == 1
     # The workspace holds the work-queue counter (256 bytes), the launch order
     # of a routed call (4 bytes per (batch, head, query block) work item,
-    # rounded up to 256) and the aligned-walk table (8 XCDs x 64 entries of 8
-    # bytes), then the split partials of the last round, 1,024 workgroups of
-    # 128 x (128 + 2) fp32, when the key range can be split (at least 16 key
-    # blocks, 2 parts of 8).  V is read in place.
-    def order(items):
-        return 256 + (items * 4 + 255) // 256 * 256 + 8 * 64 * 8
+    # rounded up to 256), the aligned-walk table (8 XCDs x 64 entries of 8
+    # bytes) and 64 key-norm maxima per (batch, head) (fp32, rounded up to
+    # 256; none above 4,096 pairs), then the split partials of the last round,
+    # 1,024 workgroups of 128 x (128 + 2) fp32, when the key range can be
+    # split (at least 16 key blocks, 2 parts of 8).  V is read in place.
+    def order(items, pairs):
+        norms = (pairs * 64 * 4 + 255) // 256 * 256 if pairs <= 4096 else 0
+        return 256 + (items * 4 + 255) // 256 * 256 + 8 * 64 * 8 + norms
 
     split = 1024 * (128 * 128 + 256) * 4
-    assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == order(2 * 12 * 256) + split
-    assert lib.dsa_bsa_workspace_bytes(1, 40, 57600, 128) == order(40 * 450) + split
-    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 16 * 72, 128, 72) == order(16) + split
-    # Key ranges too short to split need the order only: 512 text tokens (4
+    assert lib.dsa_bsa_workspace_bytes(2, 12, 32760, 128) == order(2 * 12 * 256, 24) + split
+    assert lib.dsa_bsa_workspace_bytes(1, 40, 57600, 128) == order(40 * 450, 40) + split
+    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 16 * 72, 128, 72) == order(16, 1) + split
+    # Key ranges too short to split need the front only: 512 text tokens (4
     # blocks), 10 blocks of 72 tokens, one 1-token block.
-    assert lib.dsa_bsa_workspace_bytes(1, 12, 512, 128) == order(12 * 4)
-    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 720, 128, 72) == order(10)
-    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 1, 128, 1) == order(1)
-    # More than 262,144 work items run in launch order: no order bytes.
+    assert lib.dsa_bsa_workspace_bytes(1, 12, 512, 128) == order(12 * 4, 12)
+    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 720, 128, 72) == order(10, 1)
+    assert lib.dsa_bsa_workspace_bytes_block(1, 1, 1, 128, 1) == order(1, 1)
+    # 8,192 (batch, head) pairs: ordered, without norms.
+    assert lib.dsa_bsa_workspace_bytes(64, 128, 256, 128) == order(64 * 128 * 2, 8192)
+    # More than 262,144 work items run in launch order: no front bytes.
     assert lib.dsa_bsa_workspace_bytes_block(1, 64, 8192 * 8, 128, 8) == split
     assert lib.dsa_bsa_workspace_bytes(0, 12, 10, 128) == 0
 

@@ -348,3 +348,73 @@ def test_aligned_walk_and_deterministic_calls(cuda_device, block, tokens, heads)
     np.testing.assert_allclose(aligned[1].cpu().numpy(), first[1].cpu().numpy(), atol=1e-4)
     rows = [(0, h, qb) for h in range(heads) for qb in (0, 1, blocks // 2, blocks - 1)]
     _check(aligned[0], q, k, v, route, block=block, rows=rows)
+
+
+def _outlier_keys(tokens, heads, head_dim, seed, scale_rows=None):
+    """randn q, k, v [1, T, H, D] with a few keys stretched to a large norm and
+    aligned with one query each, at the first and last token and at both
+    sides of the key-norm pre-pass's 64 token ranges (ceil(T / 64) each)."""
+    generator = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(1, tokens, heads, head_dim, generator=generator) for _ in range(3))
+    per = -(-tokens // 64)
+    spots = sorted({0, tokens - 1, per - 1, per, 17 * per - 1, 17 * per} & set(range(tokens)))
+    for i, t in enumerate(spots):
+        h = i % heads
+        k[0, t, h] = q[0, (t * 7 + 3) % tokens, h] * 6.0
+    if scale_rows is not None:
+        q[0, scale_rows] *= 5.0
+    return [x.to(torch.bfloat16) for x in (q, k, v)], spots
+
+
+@pytest.mark.parametrize("routed", [False, True])
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_key_norm_bound_with_outlier_keys(cuda_device, routed, head_dim):
+    """Keys of large norm in every pre-pass range edge: the bound must cover
+    them (a missed one overflows p), and rows whose bound stays loose take
+    their row max on every half-tile."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    tokens, heads = 1000, 2
+    (q, k, v), spots = _outlier_keys(tokens, heads, head_dim, seed=head_dim + routed)
+    route, csr = None, None
+    if routed:
+        blocks = math.ceil(tokens / 128)
+        generator = torch.Generator().manual_seed(11)
+        route = torch.rand(1, heads, blocks, blocks, generator=generator) < 0.7
+        route[..., 0] = True
+        csr = csr_from_route(route.to(cuda_device))
+    # BHSD storage, [B, T, H, D] views (the key-norm pre-pass walks k's strides).
+    qd, kd, vd = (x.transpose(1, 2).contiguous().to(cuda_device).transpose(1, 2)
+                  for x in (q, k, v))
+    out, lse = bsa_fwd(qd, kd, vd, csr, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    _check(out, q, k, v, route)
+    _, expected_lse = block_sparse_attention(
+        q.float().numpy(), k.float().numpy(), v.float().numpy(),
+        None if route is None else route.numpy(), 128)
+    np.testing.assert_allclose(lse.cpu().numpy(), expected_lse, atol=2e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_key_norm_bound_mixed_rows(cuda_device, dtype):
+    """Some query rows five times longer than the rest (their bound loose,
+    the others' tight) inside the same waves, dense and routed, bf16 and
+    fp16, deterministic and not."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    tokens, heads = 1280, 2
+    rows = torch.arange(3, tokens, 7)
+    generator = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn(1, tokens, heads, 128, generator=generator) for _ in range(3))
+    q[0, rows] *= 5.0
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    blocks = tokens // 128
+    route = torch.rand(1, heads, blocks, blocks, generator=generator) < 0.6
+    route[..., 0] = True
+    csr = csr_from_route(route.to(cuda_device))
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    for deterministic in (True, False):
+        dense = bsa_fwd(qd, kd, vd, deterministic=deterministic)
+        routed = bsa_fwd(qd, kd, vd, csr, deterministic=deterministic)
+        torch.cuda.synchronize()
+        _check(dense, q, k, v, None)
+        _check(routed, q, k, v, route)
