@@ -243,10 +243,12 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   typedef typename E::x8 x8;
   static_assert(!kStats || (kRouted && kGather) || (!kRouted && kNh == 2 && !kSkip && !kGather),
                 "fused statistics: the gathered stream or dense 128-token blocks");
-  // The key-norm bound (compute) in the instances with registers to spare:
-  // in the gathered and sub-tile-skipping ones the extra live value makes the
-  // register allocator copy the O accumulators around the rescale branch.
-  constexpr bool kNormBound = !kGather && !kSkip;
+  // The key-norm bound (compute), except in the plain-stream instances that
+  // skip empty sub-tiles (65..96-key blocks): there the extra live value made
+  // the register allocator copy the O accumulators around the rescale branch
+  // on every step.  (The gathered stream lost the same way until the wave
+  // priority below freed its registers: 720p 67.4 -> 66.0 ms with it now.)
+  constexpr bool kNormBound = kGather || !kSkip;
   // Wave priority (s_setprio) over one phase of each step, so that the two
   // waves sharing a SIMD fall into opposite phases and one's VALU work runs
   // beside the other's MFMAs: the gathered stream raises it for the softmax,
@@ -1128,7 +1130,7 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
     unsigned char* base = static_cast<unsigned char*>(scratch);
     used = lead;
     unsigned char* const walk_end = base + lead - norm_bytes(norms);
-    if (norm_bytes(norms) > 0 && !gather && !skip) {
+    if (norm_bytes(norms) > 0 && (gather || !skip)) {
       float* kv_norm = reinterpret_cast<float*>(walk_end);
       hipLaunchKernelGGL(key_norm_kernel<T>, dim3(kNormParts, (unsigned)norms), dim3(256), 0,
                          stream, p, kv_norm);

@@ -81,9 +81,8 @@ const char* dsa_last_error(void);
  *                them a row skips its max on every 64-key half-tile whose
  *                scores the Cauchy-Schwarz bound |q| max|k| keeps within 2^32
  *                of its running reference (the same softmax; fp32 rounding
- *                can differ in the last bits).  Not used by the gathered
- *                stream of routed 65..127-token blocks nor by blocks whose
- *                last half-tile holds 1..32 keys.  The rest
+ *                can differ in the last bits).  Not used by plain-stream
+ *                blocks whose last half-tile holds 1..32 keys.  The rest
  *                holds the fp32 partials
  *                of the query blocks in the last, partial round of workgroups
  *                (two per CU of the stream's device), which then run as 2..8

@@ -418,3 +418,24 @@ def test_key_norm_bound_mixed_rows(cuda_device, dtype):
         torch.cuda.synchronize()
         _check(dense, q, k, v, None)
         _check(routed, q, k, v, route)
+
+
+@pytest.mark.parametrize("block", [72, 80])
+def test_key_norm_bound_gathered_stream(cuda_device, block):
+    """The gathered key stream (routed 65..127-token blocks) under the
+    key-norm bound: outlier keys at the pre-pass range edges and query rows
+    five times longer than the rest."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    blocks, heads = 12, 2
+    tokens = blocks * block
+    rows = torch.arange(5, tokens, 9)
+    (q, k, v), _ = _outlier_keys(tokens, heads, 128, seed=block, scale_rows=rows)
+    generator = torch.Generator().manual_seed(block + 1)
+    route = torch.rand(1, heads, blocks, blocks, generator=generator) < 0.6
+    route[..., 0] = True
+    csr = csr_from_route(route.to(cuda_device), block_size=block)
+    out = bsa_fwd(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device), csr,
+                  block_size=block)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check(out, q, k, v, route, block=block)
