@@ -117,11 +117,17 @@ using dsa::make_rsrc;
 typedef dsa::const_i32 dsa_const_i32;
 
 constexpr float kRescaleLog2 = 8.0f;  // move the max once p could exceed 2^8
-// Half-tiles whose scores provably stay within 2^kBoundLog2 of the reference
-// max (key-norm bound) skip the row max: p <= 2^32 leaves fp32 sums and O
-// accumulators of up to 2^20 keys finite for |v| < 2^76.
-constexpr float kBoundLog2 = 32.0f;
-constexpr float kRaiseLog2 = 16.0f;
+// Half-tiles whose scores provably stay within 2^bound_log2 of the reference
+// max (key-norm bound) skip the row max.  The P operand carries p in the
+// input type: bf16 (fp32's exponent range) takes p <= 2^32, which leaves fp32
+// sums and O accumulators of up to 2^20 keys finite for |v| < 2^76; fp16
+// overflows at 65,504, so it takes p <= 2^15.  raise_log2: how far below its
+// largest p a row's first half-tile may be scaled to meet the bound (fp16
+// keeps that p a normal number).
+template <typename T>
+constexpr float bound_log2() { return std::is_same<T, _Float16>::value ? 15.0f : 32.0f; }
+template <typename T>
+constexpr float raise_log2() { return std::is_same<T, _Float16>::value ? 4.0f : 16.0f; }
 constexpr int kNormParts = 64;        // key-norm maxima per (batch, head), one per lane
 constexpr int64_t kMaxNormPairs = 4096;  // (batch, head) pairs with norms (1 MiB)
 
@@ -367,8 +373,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // (Cauchy-Schwarz) over every key of the (batch, head), with kmax the
   // largest key norm (from its kNormParts partial maxima, one per lane) and
   // |q| from the row's fragments (lanes l and l ^ 32 hold its two halves),
-  // rounded up.  thr = bound - kBoundLog2 (+inf without norms): while the
-  // reference max m_run >= thr, no p of the row can exceed 2^kBoundLog2.
+  // rounded up.  thr = bound - bound_log2 (+inf without norms): while the
+  // reference max m_run >= thr, no p of the row can exceed 2^bound_log2.
   float thr = INFINITY;
   if (kNormBound && p.kv_norm != nullptr) {
     float kmax = p.kv_norm[(int64_t)bh * kNormParts + lane];
@@ -380,7 +386,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
 #pragma unroll
       for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[dc][e], (float)qf[dc][e], qq);
     const float qn = sqrtf(dsa::pair32_sum(qq)) * fabsf(p.scale_log2) * 1.0001f;
-    thr = fmaf(qn, kmax, -kBoundLog2);
+    thr = fmaf(qn, kmax, -bound_log2<T>());
   }
 
   const T* kbase = static_cast<const T*>(p.k) + b * p.k_sb + h * p.k_sh;
@@ -566,7 +572,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
           if (kt * 32 + 8 * (r >> 2) + (r & 3) >= bound) sacc[kt][r] = -INFINITY;
     }
     // The row max only matters when the reference max may have to move: while
-    // m_run >= thr in every lane, no p of the half-tile exceeds 2^kBoundLog2
+    // m_run >= thr in every lane, no p of the half-tile exceeds 2^bound_log2
     // and the max is not taken (a row's first half-tile, with m_run = -inf,
     // always takes it).
     const bool take_max = !kNormBound || __any(!(m_run >= thr));
@@ -582,9 +588,9 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       bool up = mx2 > m_run + kRescaleLog2;
       if constexpr (kNormBound) {
         // Raise the reference to thr when that costs this half-tile at most
-        // 2^-kRaiseLog2 of its largest p: the bound test then holds for the
+        // 2^-raise_log2 of its largest p: the bound test then holds for the
         // rest of the row.
-        if (thr > m_new && thr <= mx2 + kRaiseLog2) m_new = thr;
+        if (thr > m_new && thr <= mx2 + raise_log2<T>()) m_new = thr;
         up = m_new != m_run;
       }
       if (__any(up)) {

@@ -80,8 +80,8 @@ const char* dsa_last_error(void);
  *                at most 4,096 pairs), written by a pre-pass over K: with
  *                them a row skips its max on every 64-key half-tile whose
  *                scores the Cauchy-Schwarz bound |q| max|k| keeps within 2^32
- *                of its running reference (the same softmax; fp32 rounding
- *                can differ in the last bits).  Not used by plain-stream
+ *                (bf16) or 2^15 (fp16) of its running reference (the same
+ *                softmax; fp32 rounding can differ in the last bits).  Not used by plain-stream
  *                blocks whose last half-tile holds 1..32 keys.  The rest
  *                holds the fp32 partials
  *                of the query blocks in the last, partial round of workgroups

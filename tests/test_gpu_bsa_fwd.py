@@ -439,3 +439,29 @@ def test_key_norm_bound_gathered_stream(cuda_device, block):
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
     _check(out, q, k, v, route, block=block)
+
+
+@pytest.mark.parametrize("routed", [False, True])
+def test_key_norm_bound_fp16_late_large_scores(cuda_device, routed):
+    """fp16 P overflows above 65,504: a row whose walk starts on keys it barely
+    matches and later meets keys it matches strongly (scores about 25 log2
+    units above the first block's) must still stay finite and exact."""
+    from dit_sparse_atten_amd.ops import bsa_fwd, csr_from_route
+    tokens, heads, blocks = 1024, 2, 8
+    generator = torch.Generator().manual_seed(77)
+    q = torch.randn(1, tokens, heads, 128, generator=generator)
+    q = q / q.norm(dim=-1, keepdim=True) * 14.0
+    k = torch.randn(1, tokens, heads, 128, generator=generator) * 0.05
+    # Keys of block 5 copy the queries of every block (aligned, norm 14).
+    k[0, 640:768] = q[0, torch.arange(128) * 8 % tokens]
+    v = torch.randn(1, tokens, heads, 128, generator=generator)
+    q, k, v = (x.to(torch.float16) for x in (q, k, v))
+    route, csr = None, None
+    if routed:
+        route = torch.ones(1, heads, blocks, blocks, dtype=torch.bool)
+        csr = csr_from_route(route.to(cuda_device))
+    out = bsa_fwd(q.to(cuda_device), k.to(cuda_device), v.to(cuda_device), csr,
+                  deterministic=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check(out, q, k, v, route)
