@@ -196,37 +196,63 @@ __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) 
   dsa::lds_barrier<true>();
   const int start = p.dense ? 0 : p.row_ptr[row];
   const int end = p.dense ? p.tiles : (int)min((int64_t)p.row_ptr[row + 1], p.entries);
-  for (int e = start + wave; e < end; e += 4) {
-    const int kt = p.dense ? e : p.col_idx[e];
-    if ((unsigned)kt >= (unsigned)p.tiles) continue;
-    const int64_t at0 = p.dense ? ((int64_t)h * p.tiles + kt) * p.tokens + (int64_t)qt * p.tile
-                                : (int64_t)e * p.tile;
-    float m = 0.f, qy = 0.f, qx = 0.f, ky = 0.f, kx = 0.f;
-    for (int r = lane; r < p.tile; r += 64) {
-      const int64_t at = at0 + r;
-      const float w = __builtin_amdgcn_exp2f(p.rs_logm[at] - lse2[r]);
-      const dsa_f16x2 mean = __builtin_bit_cast(dsa_f16x2, p.rs_mean[at]);
-      m += w;
-      qy = fmaf(w, uy[r], qy);
-      qx = fmaf(w, ux[r], qx);
-      ky = fmaf(w, (float)mean[0], ky);
-      kx = fmaf(w, (float)mean[1], kx);
+  // Each wave reduces kCells listed cells at a time (cells e, e + 4, ...), so
+  // that their row loads are in flight together: one cell at a time left the
+  // kernel waiting on load latency.
+  constexpr int kCells = 4;
+  for (int e0 = start + wave; e0 < end; e0 += 4 * kCells) {
+    int kt[kCells];
+    int64_t at0[kCells];
+    bool ok[kCells];
+#pragma unroll
+    for (int u = 0; u < kCells; ++u) {
+      const int e = e0 + 4 * u;
+      kt[u] = e < end ? (p.dense ? e : p.col_idx[e]) : -1;
+      ok[u] = (unsigned)kt[u] < (unsigned)p.tiles;
+      at0[u] = p.dense ? ((int64_t)h * p.tiles + kt[u]) * p.tokens + (int64_t)qt * p.tile
+                       : (int64_t)e * p.tile;
     }
-    m = dsa::wave_total(m);
-    qy = dsa::wave_total(qy);
-    qx = dsa::wave_total(qx);
-    ky = dsa::wave_total(ky);
-    kx = dsa::wave_total(kx);
-    if (lane == 0) {
-      const int64_t cell = cell0 + kt;
-      const float normalized = p.raw ? m : m / (float)p.tokens;
-      const float den = fmaxf(m, 1e-12f);
-      p.mass32[cell] = normalized;
-      if (p.mass16) p.mass16[cell] = __float2half(normalized);
-      if (p.cqy) p.cqy[cell] = __float2half(qy / den);
-      if (p.cqx) p.cqx[cell] = __float2half(qx / den);
-      if (p.cky) p.cky[cell] = __float2half(ky / den);
-      if (p.ckx) p.ckx[cell] = __float2half(kx / den);
+    float m[kCells], qy[kCells], qx[kCells], ky[kCells], kx[kCells];
+#pragma unroll
+    for (int u = 0; u < kCells; ++u) m[u] = qy[u] = qx[u] = ky[u] = kx[u] = 0.f;
+    for (int r = lane; r < p.tile; r += 64) {
+      float lg[kCells];
+      uint32_t mn[kCells];
+#pragma unroll
+      for (int u = 0; u < kCells; ++u) {
+        lg[u] = ok[u] ? p.rs_logm[at0[u] + r] : -INFINITY;
+        mn[u] = ok[u] ? p.rs_mean[at0[u] + r] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < kCells; ++u) {
+        const float w = __builtin_amdgcn_exp2f(lg[u] - lse2[r]);
+        const dsa_f16x2 mean = __builtin_bit_cast(dsa_f16x2, mn[u]);
+        m[u] += w;
+        qy[u] = fmaf(w, uy[r], qy[u]);
+        qx[u] = fmaf(w, ux[r], qx[u]);
+        ky[u] = fmaf(w, (float)mean[0], ky[u]);
+        kx[u] = fmaf(w, (float)mean[1], kx[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kCells; ++u) {
+      if (!ok[u]) continue;
+      const float mu = dsa::wave_total(m[u]);
+      const float qyu = dsa::wave_total(qy[u]);
+      const float qxu = dsa::wave_total(qx[u]);
+      const float kyu = dsa::wave_total(ky[u]);
+      const float kxu = dsa::wave_total(kx[u]);
+      if (lane == 0) {
+        const int64_t cell = cell0 + kt[u];
+        const float normalized = p.raw ? mu : mu / (float)p.tokens;
+        const float den = fmaxf(mu, 1e-12f);
+        p.mass32[cell] = normalized;
+        if (p.mass16) p.mass16[cell] = __float2half(normalized);
+        if (p.cqy) p.cqy[cell] = __float2half(qyu / den);
+        if (p.cqx) p.cqx[cell] = __float2half(qxu / den);
+        if (p.cky) p.cky[cell] = __float2half(kyu / den);
+        if (p.ckx) p.ckx[cell] = __float2half(kxu / den);
+      }
     }
   }
 }
