@@ -31,8 +31,8 @@
 //  * online softmax with a lazily moved reference max (rescale only when a
 //    score exceeds it by 2^8); with key norms from key_norm_kernel, a row
 //    takes its max only while the Cauchy-Schwarz bound |q| max|k| could put a
-//    score more than 2^32 above the reference (in practice on its first
-//    half-tile only); row sums add the fp32 P in plain VALU adds
+//    score more than 2^32 (bf16; fp16: 2^15) above the reference (in practice
+//    on its first half-tile only); row sums add the fp32 P in plain VALU adds
 //    (v_dot2 would contend with the matrix core for issue); the row max and
 //    the final row sum pair lanes l and l ^ 32 with v_permlane32_swap;
 //  * query / key blocks of 1..128 tokens (the matrix-sparse backend's spatial
