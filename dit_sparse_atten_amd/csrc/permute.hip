@@ -5,9 +5,11 @@
 //       layout_ops.py:86-125, its three index_select fallback 100-101)
 //   SpatialTokenLayout.restore     -> index_select(1, inverse) (spatial.py:91-93)
 // Up to three tensors move in one launch.  Each (b, t, h) row is a contiguous
-// run of head_dim elements; it is copied as 16-byte chunks so that the 16
-// lanes covering one row read and write one contiguous segment, whatever the
+// run of head_dim elements; it is copied as 16-byte chunks so that the lanes
+// covering one row read and write one contiguous segment, whatever the
 // token / head strides of source and destination are.  Bit-exact data movement.
+// The bound is the device copy rate: at 57,600 tokens x 40 heads x 128 bf16
+// a head-major reorder of three tensors moves 5.4 TB/s, a plain copy 5.3.
 #include "dsa_common.h"
 
 namespace {
@@ -23,23 +25,59 @@ struct PermuteParams {
   int32_t tensors, batch, tokens, heads, chunks_per_row;
 };
 
-// Grid: x = destination token, y = tensor * batch + b.  The 256 threads of a
-// workgroup stride over the heads * chunks_per_row chunks of that token.
+// Head-major destination tokens per workgroup.  Measured at 57,600 tokens x 40
+// heads: 2 is fastest; 4, 8 and 16 lose up to 7% (the larger groups leave a
+// single-tensor launch too few workgroups to fill the chip evenly).
+constexpr int kGroupTokens = 2;
+constexpr int kUnroll = 4;  // 16-byte chunks in flight per thread
+
+// Grid: x = group of kGroup destination tokens, y = tensor * batch + b.  The
+// group's chunks are numbered so that consecutive threads cover consecutive
+// destination bytes.  A head-major destination (kGroup = kGroupTokens) is
+// walked head-outer: each head contributes kGroup consecutive 256-byte rows.
+// A token-major one (kGroup = 1) is walked as the token's contiguous
+// heads * row_bytes.  Each thread issues kUnroll loads before its stores.
+template <int kGroup>
 __global__ void __launch_bounds__(256) permute_rows_kernel(PermuteParams p) {
-  const int t = blockIdx.x;
+  __shared__ int32_t source[kGroup];
+  const int t0 = blockIdx.x * kGroup;
+  const int rows = min(kGroup, p.tokens - t0);
   const int n = blockIdx.y / p.batch;
   const int b = blockIdx.y % p.batch;
-  const int s = p.perm[t];
-  if ((unsigned)s >= (unsigned)p.tokens) return;  // invalid index: row left untouched
-  const unsigned char* src = p.src[n] + b * p.src_sb[n] + (int64_t)s * p.src_st[n];
-  unsigned char* dst = p.dst[n] + b * p.dst_sb[n] + (int64_t)t * p.dst_st[n];
-  const int per_token = p.heads * p.chunks_per_row;
-  for (int i = threadIdx.x; i < per_token; i += 256) {
-    const int h = i / p.chunks_per_row;
-    const int c = i - h * p.chunks_per_row;
-    const dsa_u32x4 value =
-        *reinterpret_cast<const dsa_u32x4*>(src + h * p.src_sh[n] + c * 16);
-    *reinterpret_cast<dsa_u32x4*>(dst + h * p.dst_sh[n] + c * 16) = value;
+  if constexpr (kGroup > 1) {
+    if (threadIdx.x < rows) source[threadIdx.x] = p.perm[t0 + threadIdx.x];
+    __syncthreads();
+  } else {
+    if ((unsigned)p.perm[t0] >= (unsigned)p.tokens) return;  // invalid index: row left untouched
+  }
+  const unsigned char* src = p.src[n] + b * p.src_sb[n];
+  unsigned char* dst = p.dst[n] + b * p.dst_sb[n] + (int64_t)t0 * p.dst_st[n];
+  const int64_t src_st = p.src_st[n], src_sh = p.src_sh[n];
+  const int64_t dst_st = p.dst_st[n], dst_sh = p.dst_sh[n];
+  const int cpr = p.chunks_per_row;
+  const int total = rows * p.heads * cpr;
+  for (int base = 0; base < total; base += 256 * kUnroll) {
+    dsa_u32x4 value[kUnroll];
+    unsigned char* out[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = base + u * 256 + (int)threadIdx.x;
+      out[u] = nullptr;
+      if (i < total) {
+        const int row = i / cpr;
+        const int c = i - row * cpr;
+        const int h = kGroup > 1 ? row / rows : row;
+        const int t = kGroup > 1 ? row - h * rows : 0;
+        const int s = kGroup > 1 ? source[t] : p.perm[t0];
+        if ((unsigned)s < (unsigned)p.tokens) {  // invalid index: row left untouched
+          value[u] = *reinterpret_cast<const dsa_u32x4*>(src + s * src_st + h * src_sh + c * 16);
+          out[u] = dst + t * dst_st + h * dst_sh + c * 16;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (out[u] != nullptr) *reinterpret_cast<dsa_u32x4*>(out[u]) = value[u];
   }
 }
 
@@ -84,9 +122,17 @@ extern "C" int dsa_permute_rows(int32_t tensors, const void* const* src, void* c
   p.chunks_per_row = row_bytes / 16;
   if ((int64_t)tensors * batch > 65535)
     return dsa::set_error(DSA_EUNSUPPORTED, "dsa_permute_rows: batch too large");
-  if ((int64_t)heads * p.chunks_per_row > 0x7fffffff)
+  if ((int64_t)kGroupTokens * heads * p.chunks_per_row > (1 << 30))
     return dsa::set_error(DSA_EUNSUPPORTED, "dsa_permute_rows: rows too wide");
-  hipLaunchKernelGGL(permute_rows_kernel, dim3((unsigned)tokens, (unsigned)(tensors * batch)),
-                     dim3(256), 0, stream, p);
+  bool head_major = true;  // every destination has its token stride below its head stride
+  for (int n = 0; n < tensors; ++n) head_major = head_major && p.dst_st[n] < p.dst_sh[n];
+  if (head_major) {
+    const unsigned groups = (unsigned)((tokens + kGroupTokens - 1) / kGroupTokens);
+    hipLaunchKernelGGL(permute_rows_kernel<kGroupTokens>,
+                       dim3(groups, (unsigned)(tensors * batch)), dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(permute_rows_kernel<1>, dim3((unsigned)tokens, (unsigned)(tensors * batch)),
+                       dim3(256), 0, stream, p);
+  }
   return dsa::check_launch("dsa_permute_rows");
 }
