@@ -221,6 +221,33 @@ def test_permute_tokens_bit_exact(ops, cuda_device, grid, head_major):
         assert torch.equal(restored.cpu(), src.transpose(1, 2))
 
 
+@pytest.mark.parametrize("tokens,heads,dim", [(1001, 3, 64), (7, 40, 128), (33, 1, 8)])
+def test_permute_tokens_ragged_layouts_and_invalid_indices(ops, cuda_device, tokens, heads, dim):
+    """Odd token counts (a last head-major group of one token), 16-byte rows,
+    batch 2, a mix of head-major and token-major destinations in one launch,
+    and out-of-range indices, whose destination rows stay untouched."""
+    generator = torch.Generator().manual_seed(tokens)
+    sources = [torch.randn(2, tokens, heads, dim, generator=generator).to(torch.bfloat16)
+               for _ in range(3)]
+    perm = torch.randperm(tokens, generator=generator).to(torch.int32)
+    perm[::5] = -1
+    perm[2::7] = tokens + 3
+    valid = (perm >= 0) & (perm < tokens)
+    for layouts in (("head", "head", "head"), ("token", "token", "token"),
+                    ("head", "token", "head")):
+        out = []
+        for layout in layouts:
+            shape = (2, heads, tokens, dim) if layout == "head" else (2, tokens, heads, dim)
+            t = torch.full(shape, 7.0, dtype=torch.bfloat16, device=cuda_device)
+            out.append(t.transpose(1, 2) if layout == "head" else t)
+        ops.permute_tokens([s.to(cuda_device) for s in sources], perm.to(cuda_device), out=out)
+        torch.cuda.synchronize()
+        for got, src in zip(out, sources):
+            expected = torch.full_like(src, 7.0)
+            expected[:, valid] = src[:, perm[valid].long()]
+            assert torch.equal(got.cpu(), expected), layouts
+
+
 @pytest.mark.parametrize("keys", [591, 1339, 2048])
 def test_route_select_beyond_1024_keys(ops, cuda_device, keys):
     """Longer videos: 81 frames at 720p (591 blocks), 1080p x 81 frames
