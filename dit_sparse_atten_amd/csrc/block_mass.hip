@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
   uint32_t koff[4];
   dsa::k_tile_offsets(wave, lane, p.k_st, p.head_dim, koff);
   auto issue = [&](int key0, unsigned char* dst) __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t rsrc = dsa::k_tile_rsrc(kbase, p.k_st, key0, p.tokens);
+    const __amdgpu_buffer_rsrc_t rsrc = dsa::k_tile_rsrc(kbase, p.k_st, key0, p.tokens, p.head_dim);
 #pragma unroll
     for (int j = 0; j < 4; ++j) dsa::lds_load16(rsrc, dst + (wave * 4 + j) * 1024, koff[j], 0);
   };

@@ -432,8 +432,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   auto issue = [&](int kb, int half, unsigned char* kdst, unsigned char* vdst) {
     const int kbc = kb < 0 ? 0 : kb;
     const int key0 = kbc * p.block + half * kHalfKeys;
-    const __amdgpu_buffer_rsrc_t k_rsrc = k_tile_rsrc(kbase, p.k_st, key0, p.kv_tokens);
-    const __amdgpu_buffer_rsrc_t v_rsrc = k_tile_rsrc(vbase, p.v_st, key0, p.kv_tokens);
+    const __amdgpu_buffer_rsrc_t k_rsrc = k_tile_rsrc(kbase, p.k_st, key0, p.kv_tokens, p.head_dim);
+    const __amdgpu_buffer_rsrc_t v_rsrc = k_tile_rsrc(vbase, p.v_st, key0, p.kv_tokens, p.head_dim);
 #pragma unroll
     for (int j = 0; j < kSlices; ++j)
       lds_load16(k_rsrc, kdst + (wave * kSlices + j) * 1024, koff[j], 0);
@@ -445,9 +445,9 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // runs on into kb1 (the blocks are in range; pad and tail slots load
   // whatever they address, or zeros past the end, and are masked).
   const __amdgpu_buffer_rsrc_t k_all_rsrc = make_rsrc(
-      kbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.k_st * 2 + kRowBytes));
+      kbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.k_st * 2 + p.head_dim * 2));
   const __amdgpu_buffer_rsrc_t v_all_rsrc = make_rsrc(
-      vbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.v_st * 2 + kRowBytes));
+      vbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.v_st * 2 + p.head_dim * 2));
   auto issue_gather = [&](int kb0, int kb1, int o0, unsigned char* kdst, unsigned char* vdst)
       __attribute__((always_inline)) {
 #pragma unroll

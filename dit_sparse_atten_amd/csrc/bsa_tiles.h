@@ -38,12 +38,14 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rsrc, unsigned
 }
 
 // Resource covering the 64 K rows (16-bit elements, token stride k_st) of a
-// half-tile starting at key0; rows at or past kv_tokens read as zeros (a half-tile wholly past the end has no
-// records).  The host keeps 64 rows of K within 2^31 bytes.
+// half-tile starting at key0; rows at or past kv_tokens read as zeros (a
+// half-tile wholly past the end has no records), and the last row ends at its
+// head_dim-th element.  The host keeps 64 rows of K within 2^31 bytes.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t k_tile_rsrc(const void* kbase, int64_t k_st,
-                                                             int key0, int kv_tokens) {
+                                                             int key0, int kv_tokens,
+                                                             int head_dim) {
   const int rows = min(kHalfKeys, kv_tokens - key0);
-  const uint32_t bytes = rows > 0 ? (uint32_t)((rows - 1) * k_st * 2 + kRowBytes) : 0u;
+  const uint32_t bytes = rows > 0 ? (uint32_t)((rows - 1) * k_st * 2 + head_dim * 2) : 0u;
   return make_rsrc(static_cast<const unsigned char*>(kbase) + (int64_t)key0 * k_st * 2, bytes);
 }
 

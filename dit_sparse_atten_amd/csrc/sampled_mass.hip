@@ -181,11 +181,16 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
         float mx = m2;
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaf(sc[r], kLog2e, cw[r]));
+        // While every key this lane has seen is masked (mx = -inf, as for
+        // the lanes past the last sampled key when blocks * S <= 4), the
+        // terms and the rescale take a finite reference and are exactly
+        // zero, where -inf - (-inf) would make them NaN.
+        const float mref = mx == -INFINITY ? 0.f : mx;
         float sum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          sum += __builtin_amdgcn_exp2f(fmaf(sc[r], kLog2e, cw[r] - mx));
-        l2 = l2 * __builtin_amdgcn_exp2f(m2 - mx) + sum;
+          sum += __builtin_amdgcn_exp2f(fmaf(sc[r], kLog2e, cw[r] - mref));
+        l2 = l2 * __builtin_amdgcn_exp2f(m2 - mref) + sum;
         m2 = mx;
       } else if constexpr (kWide) {
         float sum = 0.f;

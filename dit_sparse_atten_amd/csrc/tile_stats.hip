@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(kWaves * 64, 3) tile_stats_kernel(TileStatsPar
   dsa::k_tile_offsets(wave, lane, p.k_st, p.head_dim, koff);
   auto issue = [&](int kt, int half, unsigned char* dst) __attribute__((always_inline)) {
     const int key0 = (kt < 0 ? 0 : kt) * p.tile + half * kHalfKeys;
-    const __amdgpu_buffer_rsrc_t rsrc = dsa::k_tile_rsrc(kbase, p.k_st, key0, p.tokens);
+    const __amdgpu_buffer_rsrc_t rsrc = dsa::k_tile_rsrc(kbase, p.k_st, key0, p.tokens, p.head_dim);
     if constexpr (kWaves == 4) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) dsa::lds_load16(rsrc, dst + (wave * 4 + j) * 1024, koff[j], 0);
@@ -337,7 +337,7 @@ __global__ void __launch_bounds__(kWaves * 64, 3) tile_stats_kernel(TileStatsPar
   if constexpr (kGather) {
     const int bp = p.tile_pad;
     const __amdgpu_buffer_rsrc_t k_all = dsa::make_rsrc(
-        kbase, (uint32_t)((int64_t)(p.tokens - 1) * p.k_st * 2 + kRowBytes));
+        kbase, (uint32_t)((int64_t)(p.tokens - 1) * p.k_st * 2 + p.head_dim * 2));
     const uint32_t kst2 = (uint32_t)(p.k_st * 2);
     // Per-lane part of a slice's offsets: slice i stages stream rows 4 i +
     // (lane >> 4) at 16-byte column k2_swz(row, lane & 15), which depends on

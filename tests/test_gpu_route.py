@@ -66,6 +66,25 @@ def test_sampled_mass_sample_counts(ops, cuda_device, samples, dtype):
     assert torch.equal(again, got)
 
 
+@pytest.mark.parametrize("tokens,samples", [(128, 1), (128, 2), (128, 3), (128, 4), (512, 1),
+                                            (256, 2), (300, 1)])
+def test_sampled_mass_few_sampled_keys(ops, cuda_device, tokens, samples):
+    """At most 4 sampled keys in all (blocks * samples <= 4, or a padded
+    sample count): lanes whose keys are all masked must contribute zero, not
+    NaN, so the mass is finite, rows sum to 1 and match the oracle."""
+    block, heads = 128, 2
+    q, k, _ = clustered_qkv(tokens, heads, 128, group=block, seed=tokens + samples,
+                            dtype=torch.bfloat16)
+    got = ops.sampled_block_mass(q.to(cuda_device), k.to(cuda_device), block, samples)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    assert np.isfinite(got).all()
+    oracle = R.sampled_block_mass(q.float().numpy(), k.float().numpy(), block, samples,
+                                  score_dtype="bf16")
+    np.testing.assert_allclose(got, oracle, atol=2e-3, rtol=2e-3)
+    np.testing.assert_allclose(got.sum(-1), 1.0, atol=1e-5)
+
+
 def test_full_sampling_at_block_128_matches_exact_block_mass(ops, cuda_device):
     """samples == block == 128 (the reference's identity, test_flex_backend.py:
     43-53, at the production block size): mass = exact mass / block, up to
