@@ -41,6 +41,7 @@ TOKENS, HEADS, HEAD_DIM, BLOCK = 57600, 40, 128, 128
 GRID = (16, 45, 80)
 KEEP = 0.625
 TRAFFIC_FILE = ROOT / "profiles" / "bsa_fwd_config2_traffic.json"
+SHARE_FILE = ROOT / "profiles" / "bsa_fwd_config2_share.json"
 # The sources of the config-2 kernel: a counter file taken on other sources
 # does not describe this build.
 KERNEL_SOURCES = ("dit_sparse_atten_amd/csrc/bsa_kernel.h", "dit_sparse_atten_amd/csrc/bsa_fwd.hip",
@@ -87,6 +88,20 @@ def measured_traffic():
     if data.get("sources_sha16") != kernel_sources_sha16():
         return None, "counter runs predate these kernel sources"
     return data.get("fabric_bytes_per_launch"), str(TRAFFIC_FILE.relative_to(ROOT))
+
+
+def kernel_share():
+    """(share, note): the dominant kernel's mean dispatch time over the bench
+    line's mean event window (which also holds key_norm_kernel,
+    launch_order_kernel and bsa_merge_kernel), both from one committed
+    rocprofv3 --kernel-trace run of this config, or None when that run
+    predates the kernel's current sources."""
+    if not SHARE_FILE.exists():
+        return None, "no kernel-trace share file"
+    data = json.loads(SHARE_FILE.read_text())
+    if data.get("sources_sha16") != kernel_sources_sha16():
+        return None, "kernel-trace run predates these kernel sources"
+    return data.get("kernel_share"), str(SHARE_FILE.relative_to(ROOT))
 
 
 def copy_calibration(mib):
@@ -567,6 +582,16 @@ def main():
         "launch_ms_mean": round(kernel_ms, 4),
         "launch_ms_median": round(sorted(per_call)[len(per_call) // 2], 4),
     }
+    share, share_source = kernel_share()
+    if share:
+        # The dominant kernel alone: the event window scaled by its share of
+        # that window in the committed kernel trace of this config.
+        kernel_est = kernel_ms * share
+        result["roofline"]["kernel_share"] = share
+        result["roofline"]["kernel_share_source"] = share_source
+        result["roofline"]["kernel_ms_est"] = round(kernel_est, 4)
+        result["roofline"]["frac_kernel_est"] = round(
+            flops / (kernel_est * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
     if traffic:
         # L2 <-> memory-fabric rate (MALL hits included), not an HBM rate.
         result["roofline"]["l2_fabric_gbs"] = round(traffic / (kernel_ms * 1e-3) / 1e9, 1)

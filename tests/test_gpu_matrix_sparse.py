@@ -5,6 +5,7 @@ on the same bf16 inputs, routes bit-exact given the same mass,
 outputs within max-abs 2e-2 / cosine 0.9995."""
 
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -430,3 +431,50 @@ def test_backend_steps_match_oracle(ops, cuda_device, policy):
             previous = state
     finally:
         context.reset_runtime_state()
+
+
+def _config0_call(cuda_device, dtype):
+    """BASELINE config 0 through the GPU ``sparse`` backend as the reference's
+    fixture ran it (tests/golden/make_golden.py): 12 heads, grid (4, 16, 16),
+    8x8 tiles, the step-0 dense bootstrap (top-mass 0.95, cap 10 of 16, the
+    4 frame-0 tiles as key sink), then step 1 on that route.  Returns the
+    fixture, both outputs and the bootstrap route."""
+    from dit_sparse_atten_amd.attention_backends import context
+    from dit_sparse_atten_amd.attention_backends.sparse import MatrixSparseBackend, SparseConfig
+    from tests.golden.inputs import clustered_qkv
+    data = np.load(Path(__file__).resolve().parent / "golden" / "sparse_config0.npz",
+                   allow_pickle=False)
+    order = torch.as_tensor(data["order"], dtype=torch.long)
+    q, k, v = clustered_qkv(1024, 12, 128, group=64, seed=0, permutation=order)
+    np.testing.assert_allclose([q.double().sum().item(), k.double().sum().item(),
+                                v.double().sum().item()], data["checksum"])
+    qd, kd, vd = (x.to(cuda_device, dtype) for x in (q, k, v))
+    backend = MatrixSparseBackend(SparseConfig(tile=64, keep=0.625, mass_target=0.95,
+                                               prefetch_route=False))
+    context.reset_runtime_state()
+    try:
+        context.set_routing_context(attention_id=1, step=0, branch=0, grid=(4, 16, 16))
+        out0 = backend(qd, kd, vd, dtype=dtype)
+        route = next(iter(backend.state.values()))["mask"].clone()
+        context.set_routing_context(step=1)
+        out1 = backend(qd, kd, vd, dtype=dtype)
+        torch.cuda.synchronize()
+    finally:
+        context.reset_runtime_state()
+    return data, out0, out1, route
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16])
+def test_config0_full_call_matches_reference_outputs(cuda_device, dtype):
+    """The whole config-0 call, bootstrap route included, against the
+    reference's own float32 outputs (sparse_config0.npz: heads 0 and 7, the
+    first 256 tokens of step 0 and step 1), at max-abs 2e-2 / cosine 0.9995."""
+    data, out0, out1, route = _config0_call(cuda_device, dtype)
+    heads = [int(h) for h in data["heads"]]
+    # The bootstrap route (the 4 frame-0 tiles included) is the reference's.
+    np.testing.assert_array_equal(route.cpu().numpy(), data["route"])
+    for got, name in ((out0, "out0"), (out1, "out1")):
+        sample = got[0, :256][:, heads].float().cpu().numpy()
+        metrics = A.summarize(sample, data[name])
+        assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995, (
+            name, metrics)

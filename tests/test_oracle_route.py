@@ -287,6 +287,16 @@ def compare_config3(route, primed, margins, expected, value_sum):
     return int((~safe).sum()), int(tie_order.sum()), int((~same).sum())
 
 
+# Rows of the route_config3 fixture (18,000 rows each) that are near ties
+# (decision margin <= 4 fp32 ulp), that select tied values in another order
+# (same count, same selected sum), and that differ from the reference's own
+# route at all.  Bootstrap: the one differing row is (head 18, query block
+# 376), 228 blocks here against 227, at a 1-ulp margin, where the reference's
+# count depends on torch's fp32 summation order.  Prior: the one differing row
+# is (11, 199), the same 294 blocks and selected sum in another tie order.
+CONFIG3_DIFFERENCES = {"bootstrap": (16, 0, 1), "prior": (10, 1, 1)}
+
+
 @pytest.mark.parametrize("name", ["bootstrap", "prior"])
 def test_oracle_matches_reference_route_at_config3_scale(name):
     """All 18,000 rows of a 40 x 450 x 450 selection (target .95, cap 282,
@@ -297,8 +307,7 @@ def test_oracle_matches_reference_route_at_config3_scale(name):
     route, margins = R.top_mass_route(primed, 0.95, 0.625, return_margins=True)
     route[..., :29] = True
     near, tie_order, differing = compare_config3(route, primed, margins, expected, value_sum)
-    assert near <= 40, near
-    print(f"{name}: near-tie rows {near}, tie-order rows {tie_order}, differing rows {differing}")
+    assert (near, tie_order, differing) == CONFIG3_DIFFERENCES[name]
 
 
 @pytest.mark.parametrize("prior", [False, True])
