@@ -263,6 +263,12 @@ size_t row_stats_bytes(int64_t entries, int32_t tile) {
   return ((size_t)entries * tile * 2 * sizeof(float) + 255) & ~(size_t)255;
 }
 
+// Dense statistics calls of 64..128-token tiles that are a multiple of 8 run
+// the attention on 128-token blocks: each 64-key step then holds at most one
+// tile end and starts 16-aligned in the weight table's period of two tiles.
+// Other dense calls, and routed ones, run blocks of one tile each.
+bool token_stream(int32_t tile) { return tile >= kHalfKeys && tile % 8 == 0; }
+
 
 }  // namespace
 
@@ -335,10 +341,12 @@ extern "C" size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t 
   if ((int64_t)tile_h * tile_w > 128) return 0;
   const int32_t tile = tile_h * tile_w;
   if (tokens % tile != 0) return 0;
-  const size_t attention = dsa_bsa_workspace_bytes_block(1, heads, tokens, head_dim, tile);
-  // Tiles that can fuse the statistics (65..128 tokens) also hold the per-row
-  // statistics.
-  return attention + (tile > kHalfKeys ? row_stats_bytes(entries, tile) : 0);
+  // The attention runs on blocks of one tile, or (dense, token_stream) on
+  // 128-token blocks; every call writes the per-row statistics.
+  size_t attention = dsa_bsa_workspace_bytes_block(1, heads, tokens, head_dim, tile);
+  if (token_stream(tile))
+    attention = std::max(attention, dsa_bsa_workspace_bytes_block(1, heads, tokens, head_dim, 128));
+  return attention + row_stats_bytes(entries, tile);
 }
 
 extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* v, void* o,
@@ -366,17 +374,13 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
   if (entries < 0) return dsa::set_error(DSA_EINVAL, "%s: entries must be >= 0", who);
   const int32_t tiles = tokens / tile;
   const bool dense = row_ptr == nullptr;
-  // Dense calls run the attention on 128-token blocks; their statistics fuse
-  // for tiles of 65..128 tokens (at most one tile end per 64-key step) that
-  // are a multiple of 8 (so every step starts 16-aligned in the weight
-  // table's period of two tiles).
-  const bool fuse_dense = dense && tile > kHalfKeys && tile % 8 == 0;
-  if (fuse_dense && entries < (int64_t)heads * tiles * tiles)
+  if (dense && entries < (int64_t)heads * tiles * tiles)
     return dsa::set_error(DSA_EINVAL, "%s: dense statistics need entries >= heads * tiles^2",
                           who);
+  const bool blocks128 = dense && token_stream(tile);
   BsaParams p;
   int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim,
-                       dense ? 128 : tile, row_ptr, col_idx, 1, scale, 0, deterministic, lse, who,
+                       blocks128 ? 128 : tile, row_ptr, col_idx, 1, scale, 0, deterministic, lse, who,
                        &p);
   if (status != DSA_OK) return status;
   if (workspace_bytes > 0 && (!workspace || !aligned16(workspace)))
@@ -386,24 +390,15 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
   if (workspace_bytes < need)
     return dsa::set_error(DSA_EINVAL, "%s: workspace of %zu bytes, %zu needed", who,
                           workspace_bytes, need);
-  const size_t rs = tile > kHalfKeys ? row_stats_bytes(entries, tile) : 0;
+  const size_t rs = row_stats_bytes(entries, tile);
   unsigned char* base = static_cast<unsigned char*>(workspace);
-  if (!fuse_dense && (dense || !use_gather(tile, tokens, strides[4], strides[7]))) {
-    // The attention, then the statistics pass.
-    status = launch(dtype, p, base + rs, workspace_bytes - rs, stream, who);
-    if (status != DSA_OK) return status;
-    const int64_t stat_strides[4] = {strides[1], strides[2], strides[4], strides[5]};
-    return dsa_tile_stats(q, k, dtype, stat_strides, tokens, heads, head_dim, tile_h, tile_w, lse,
-                          tokens, row_ptr, col_idx, scale, mass, mass_f16, centroid_q_y,
-                          centroid_q_x, centroid_k_y, centroid_k_x, stream);
-  }
   p.rs_logm = reinterpret_cast<float*>(base);
   p.rs_mean = reinterpret_cast<uint32_t*>(base + (size_t)entries * tile * sizeof(float));
   p.rs_entries = entries;
   p.tile_h = tile_h;
   p.tile_w = tile_w;
   p.stat_tile = tile;
-  p.stat_pad = dense ? tile : p.block_pad;
+  p.stat_pad = tile;  // the token stream's; launch_typed sets that of tile blocks
   status = launch(dtype, p, base + rs, workspace_bytes - rs, stream, who);
   if (status != DSA_OK) return status;
   ReduceParams r;

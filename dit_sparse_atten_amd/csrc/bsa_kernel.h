@@ -89,16 +89,18 @@ struct BsaParams {
   // Fused tile statistics (the kStats instances), per query row and key tile
   // of stat_tile = tile_h * tile_w tokens: rs_logm = log2 of the row's
   // unnormalised probability mass on the key tile, sum 2^(scale_log2 s), and
-  // rs_mean = its mass-weighted mean key offsets (y, x) as two fp16.  Routed
-  // (gathered stream): at e * block + r for CSR entry e and query row r of
-  // the tile, entries at or past rs_entries not written.  Dense: at
-  // (h * tiles + key tile) * q_tokens + query token.
+  // rs_mean = its mass-weighted mean key offsets (y, x) as two fp16.  Routed:
+  // at e * block + r for CSR entry e and query row r of the tile, entries at
+  // or past rs_entries not written.  Dense: at (h * tiles + key tile) *
+  // q_tokens + query token.
   float* rs_logm;
   uint32_t* rs_mean;
   int64_t rs_entries;
   int32_t tile_h, tile_w;
-  int32_t stat_tile;  // tokens per statistics tile (65..128)
-  int32_t stat_pad;   // stream slots per statistics tile (gathered: block_pad; dense: stat_tile)
+  int32_t stat_tile;  // tokens per statistics tile (1..128)
+  // Stream slots per statistics tile: gathered stream block_pad, plain
+  // stream 64 kNh (a tile per key block), dense token stream stat_tile.
+  int32_t stat_pad;
 };
 
 // One split partial: O [128 rows][128 dims] relative to the row's reference
@@ -223,9 +225,11 @@ __device__ __forceinline__ int walk_start(const uint64_t* tab, int lane, int bh,
 // at most 64 tokens, whose rows two waves cover: smaller workgroups spread
 // over the four SIMDs instead of leaving two waves per workgroup idle).
 //
-// kStats (the gathered stream, or dense calls of 128-token blocks): the
-// workgroup also writes the per-row tile statistics (rs_logm, rs_mean) from
-// the probabilities of its own softmax.
+// kStats: the workgroup also writes the per-row tile statistics (rs_logm,
+// rs_mean) from the probabilities of its own softmax.  Either every key block
+// is one statistics tile (stat_tile == block: routed calls in either stream,
+// and dense calls of tile-sized blocks), or a dense call runs 128-token
+// blocks over tiles of 64..128 tokens, a multiple of 8 (the token stream).
 // The key-side sums run on the matrix cores beside O^T = V^T P^T: with the
 // same P^T operand, C += W^T P^T where W^T (kStatRows x keys, an LDS table)
 // holds, for the key tiles of each parity (stream tile index mod 2), the
@@ -235,9 +239,13 @@ __device__ __forceinline__ int walk_start(const uint64_t* tab, int lane, int bh,
 // are its query row's five sums for the key tiles of its own half's parity.
 // Tiles span two chunks at most (65..128 keys against 64-key chunks) and two
 // tiles of one parity never share a chunk, so each lane carries the five sums
-// of one open tile across chunks and closes it in the chunk where it ends.  A
-// dense call's key stream is the token sequence itself, 64 keys per step, so
-// the same table serves with tiles of stat_tile slots.
+// of one open tile across chunks and closes it in the chunk where it ends.
+// In the plain stream a key block is staged as kNh half-tiles from its first
+// key, so tile j's half-tile `half` reads the table from position
+// (j & 1) stat_pad + 64 half with stat_pad = 64 kNh, and the tile closes
+// after its last half-tile.  A dense token stream is the token sequence
+// itself, 64 keys per step, so the table serves with tiles of stat_tile
+// slots (every step 16-aligned in its period, at most one tile end each).
 constexpr int kStatRows = 11;    // 2 parities x 5 kinds, then a zero row
 constexpr int kStatCols = 392;   // >= 2 * 120 + 64 positions; = 8 mod 128 spreads the rows' banks
 
@@ -247,8 +255,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     bsa_fwd_kernel(BsaParams p) {
   typedef dsa::Elem<T> E;
   typedef typename E::x8 x8;
-  static_assert(!kStats || (kRouted && kGather) || (!kRouted && kNh == 2 && !kSkip && !kGather),
-                "fused statistics: the gathered stream or dense 128-token blocks");
+  static_assert(!kGather || kRouted, "the gathered stream takes a block route");
+  // Only the dense 128-token instance may run the token stream; every other
+  // statistics instance has one tile per key block.
+  constexpr bool kTokenStream = kStats && !kRouted && kNh == 2 && !kSkip;
   // The key-norm bound (compute), except in the plain-stream instances that
   // skip empty sub-tiles (65..96-key blocks): there the extra live value made
   // the register allocator copy the O accumulators around the rescale branch
@@ -688,9 +698,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // One pipelined step: wait for the current stage, prefetch the next
   // half-tile (next_kb == -2: none), then compute on the current one
   // (skip_c: this step may hold at most 32 valid keys).
+  // (j: the walk index of block kb, for the statistics of tile blocks.)
   auto step = [&](int kb, int half, int next_kb, int next_half, const unsigned char* kc,
                   const unsigned char* vc, unsigned char* kn, unsigned char* vn,
-                  auto skip_c) __attribute__((always_inline)) {
+                  auto skip_c, int j) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     if (next_kb != -2) issue(next_kb, next_half, kn, vn);
@@ -700,20 +711,37 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       const int valid = valid_of(kb, half);
       // Causal (dense): keys past this lane's query row are masked.
       const int lim = !kRouted && p.causal ? tq - (kb * p.block + half * kHalfKeys) + 1 : kHalfKeys;
-      // Dense statistics: this step's keys are tokens pos .. pos + 63.
+      // Statistics: tile blocks read the table from the tile's parity and
+      // this half-tile's offset in it; the token stream from its first token
+      // pos (keys pos .. pos + 63).
       const int pos = kb * p.block + half * kHalfKeys;
-      const int wbase = kStats ? pos % (2 * p.stat_pad) : 0;
+      const bool tile_blocks = !kTokenStream || p.stat_tile == p.block;
+      int wbase = 0;
+      if constexpr (kStats)
+        wbase = tile_blocks ? (j & 1) * p.stat_pad + half * kHalfKeys : pos % (2 * p.stat_pad);
       if (decltype(skip_c)::value && valid <= 32)
         compute(kc, vc, valid, lim, 0ull, wbase, std::integral_constant<int, 1>{});
       else
         compute(kc, vc, valid, lim, 0ull, wbase, std::integral_constant<int, 2>{});
       if constexpr (kStats) {
-        // The tile ending in (pos, pos + 64] (the sequence end included), if any.
-        const int m = min(pos + kHalfKeys, p.kv_tokens) / p.stat_tile;
-        if (m >= 1 && m * p.stat_tile > pos)
-          close_tile((m - 1) & 1,
-                     ((int64_t)h * (p.kv_tokens / p.stat_tile) + (m - 1)) * p.q_tokens + tq,
-                     row_ok);
+        if (tile_blocks) {
+          // Block kb is tile j of the walk: it ends with its last half-tile.
+          if (half == kNh - 1) {
+            if constexpr (kRouted) {
+              const int64_t e = walked(j);
+              close_tile(j & 1, e * p.block + local_row, row_ok && e < p.rs_entries);
+            } else {
+              close_tile(j & 1, ((int64_t)h * p.kv_blocks + kb) * p.q_tokens + tq, row_ok);
+            }
+          }
+        } else {
+          // The tile ending in (pos, pos + 64] (the sequence end included), if any.
+          const int m = min(pos + kHalfKeys, p.kv_tokens) / p.stat_tile;
+          if (m >= 1 && m * p.stat_tile > pos)
+            close_tile((m - 1) & 1,
+                       ((int64_t)h * (p.kv_tokens / p.stat_tile) + (m - 1)) * p.q_tokens + tq,
+                       row_ok);
+        }
       }
     }
   };
@@ -805,17 +833,17 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       // only at the sequence end, which the masked two-sub-tile path covers).
       for (int j = 0; j < nblk; ++j) {
         const int kb_after = j + 1 < nblk ? block_of(j + 1) : -2;
-        step(kb, 0, kb, 1, lds_k0, lds_v0, lds_k1, lds_v1, no_skip);
-        step(kb, 1, kb_after, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip);
+        step(kb, 0, kb, 1, lds_k0, lds_v0, lds_k1, lds_v1, no_skip, j);
+        step(kb, 1, kb_after, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip, j);
         kb = kb_after;
       }
     } else {
       for (int j = 0; j < nblk; j += 2) {
         const int kb1 = j + 1 < nblk ? block_of(j + 1) : -2;
-        step(kb, 0, kb1, 0, lds_k0, lds_v0, lds_k1, lds_v1, may_skip);
+        step(kb, 0, kb1, 0, lds_k0, lds_v0, lds_k1, lds_v1, may_skip, j);
         if (kb1 == -2) break;
         const int kb2 = j + 2 < nblk ? block_of(j + 2) : -2;
-        step(kb1, 0, kb2, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip);
+        step(kb1, 0, kb2, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip, j + 1);
         kb = kb2;
       }
     }
@@ -1162,10 +1190,13 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
     }
   }
   float* part = reinterpret_cast<float*>(static_cast<unsigned char*>(scratch) + used);
-  // Dense statistics tiles need not align with the split's key ranges: such
-  // calls run unsplit.
-  const int64_t part_groups =
-      p.rs_logm && !p.row_ptr ? 0 : (int64_t)((scratch_bytes - used) / kPartBytes);
+  // Statistics of tile blocks: the tile's slots in the stream.
+  if (p.rs_logm && p.stat_tile == p.block) p.stat_pad = gather ? p.block_pad : nh * kHalfKeys;
+  // The tiles of a dense token stream need not align with the split's key
+  // ranges: such calls run unsplit (tile blocks always align).
+  const int64_t part_groups = p.rs_logm && !p.row_ptr && p.stat_tile != p.block
+                                  ? 0
+                                  : (int64_t)((scratch_bytes - used) / kPartBytes);
   int parts = 1;
   const int split = choose_split(grid, device_slots(stream), max_parts_for(p.kv_blocks),
                                  std::min<int64_t>(part_groups, kMaxPartGroups), &parts);
@@ -1179,12 +1210,24 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
   if (gather) {
     if (p.rs_logm) four(bsa_fwd_kernel<T, true, 2, true, true, 4, true>);
     else four(bsa_fwd_kernel<T, true, 2, true, true>);
+  } else if (p.row_ptr && p.rs_logm) {
+    if (nh == 2)
+      skip ? four(bsa_fwd_kernel<T, true, 2, true, false, 4, true>)
+           : four(bsa_fwd_kernel<T, true, 2, false, false, 4, true>);
+    else skip ? two(bsa_fwd_kernel<T, true, 1, true, false, 2, true>)
+              : two(bsa_fwd_kernel<T, true, 1, false, false, 2, true>);
   } else if (p.row_ptr) {
     if (nh == 2) skip ? four(bsa_fwd_kernel<T, true, 2, true>) : four(bsa_fwd_kernel<T, true, 2, false>);
     else skip ? two(bsa_fwd_kernel<T, true, 1, true, false, 2>)
               : two(bsa_fwd_kernel<T, true, 1, false, false, 2>);
-  } else if (p.rs_logm && nh == 2 && !skip) {
-    four(bsa_fwd_kernel<T, false, 2, false, false, 4, true>);
+  } else if (p.rs_logm) {
+    // Dense statistics: 128-token blocks (the token stream, or tiles of 128),
+    // or blocks of one tile each, in 2-wave workgroups up to 64 tokens.
+    if (nh == 2)
+      skip ? four(bsa_fwd_kernel<T, false, 2, true, false, 4, true>)
+           : four(bsa_fwd_kernel<T, false, 2, false, false, 4, true>);
+    else skip ? two(bsa_fwd_kernel<T, false, 1, true, false, 2, true>)
+              : two(bsa_fwd_kernel<T, false, 1, false, false, 2, true>);
   } else {
     if (nh == 2) skip ? four(bsa_fwd_kernel<T, false, 2, true>) : four(bsa_fwd_kernel<T, false, 2, false>);
     else skip ? four(bsa_fwd_kernel<T, false, 1, true>) : four(bsa_fwd_kernel<T, false, 1, false>);

@@ -377,10 +377,10 @@ def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False
     of that same softmax (the reference's ``sparse_chunk``, attention_backends/
     sparse.py:670-751; dense: ``_dense_route``, 184-233).  Returns
     ``(out, lse, stats)`` with ``out`` as :func:`bsa_fwd` returns it, ``lse``
-    [1, H, T] and ``stats`` as :func:`tile_stats` returns them.  Routed calls
-    whose tiles take the gathered key stream (e.g. 9 x 8) and dense calls with
-    tiles of 65..128 tokens get their statistics from the attention launch
-    itself; other calls run the attention and then :func:`tile_stats`.
+    [1, H, T] and ``stats`` as :func:`tile_stats` returns them.  Every call
+    gets its statistics from the attention launch itself (per query row and
+    key tile), which a short second launch combines per cell; no second QK
+    pass runs.
     """
     lib = _lib.load()
     q = _kernel_view("q", q)

@@ -210,20 +210,17 @@ int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const int64_t* s
  * lse_head_stride = tokens.
  *   entries: at least the CSR's entry count row_ptr[heads * tiles] (the
  *            cells of entries past it read as zeros); dense: at least
- *            heads * tiles * tiles for tiles of 72..128 tokens, a multiple
- *            of 8.
+ *            heads * tiles * tiles.
  * The statistics come from the attention's own probabilities in the same
  * launch (the key-side sums on the matrix cores beside P V, per query row
  * and key tile, into the workspace), combined per cell by a short second
- * launch, when the call is routed and its tiles take the gathered key stream
- * (65..127 tokens whose 8-rounded size is below the plain layout's key
- * slots, e.g. 9 x 8), or dense with tiles of 72..128 tokens, a multiple of
- * 8 (the attention then runs on 128-token blocks, unsplit).  Other calls run
- * dsa_bsa_fwd and then dsa_tile_stats.
+ * launch; no second QK pass runs.  Routed calls attend over blocks of one
+ * tile.  Dense calls with tiles of 64..128 tokens, a multiple of 8, attend
+ * over 128-token blocks and run unsplit; other dense calls attend over
+ * blocks of one tile.
  *   workspace: dsa_bsa_fwd_tile_stats_workspace_bytes(...) bytes, 16-byte
- *            aligned: entries * tile * 8 bytes of per-row statistics for
- *            tiles of 65..128 tokens (rounded up to 256), then dsa_bsa_fwd's
- *            workspace.
+ *            aligned: entries * tile * 8 bytes of per-row statistics
+ *            (rounded up to 256), then dsa_bsa_fwd's workspace.
  */
 int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                            const int64_t* strides, int32_t tokens, int32_t heads,

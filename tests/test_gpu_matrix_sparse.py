@@ -62,11 +62,11 @@ def _oracle_stats(case, q, k, v, route=None):
     return expected, out
 
 
-def _compare_stats(got, expected):
+def _compare_stats(got, expected, rtol=2e-3):
     np.testing.assert_allclose(got["mass"].cpu().numpy(), expected["mass"], atol=STAT_ATOL,
-                               rtol=2e-3)
+                               rtol=rtol)
     np.testing.assert_allclose(got["mass_f16"].float().cpu().numpy(), expected["mass"],
-                               atol=STAT_ATOL, rtol=2e-3)
+                               atol=STAT_ATOL, rtol=rtol)
     for name in ("q_y", "q_x", "k_y", "k_x"):
         key = f"centroid_{name}"
         np.testing.assert_allclose(got[key].float().cpu().numpy(), expected[key],
@@ -169,11 +169,16 @@ def test_routed_tile_stats_skip_out_of_range_tiles(ops, cuda_device):
 
 
 @pytest.mark.parametrize("grid,tile,deterministic", [
-    ((2, 18, 32), 64, True),    # 9 x 8 = 72 tokens: gathered stream, fused
+    ((2, 18, 32), 64, True),    # 9 x 8 = 72 tokens: gathered stream
     ((2, 18, 32), 64, False),   # the same with the aligned walk
-    ((2, 15, 26), 64, True),    # 5 x 13 = 65 tokens padded to 72, fused
-    ((1, 20, 30), 100, False),  # 10 x 10 = 100 tokens padded to 104, fused
-    ((4, 16, 16), 64, True),    # 8 x 8 = 64 tokens: attention, then the statistics pass
+    ((2, 15, 26), 64, True),    # 5 x 13 = 65 tokens padded to 72
+    ((1, 20, 30), 100, False),  # 10 x 10 = 100 tokens padded to 104
+    ((4, 16, 16), 64, True),    # 8 x 8 = 64 tokens: plain stream, 2-wave workgroups
+    ((4, 16, 16), 64, False),   # the same with the aligned walk
+    ((2, 14, 21), 49, True),    # 7 x 7 = 49 tokens: 2-wave workgroups
+    ((2, 12, 16), 96, True),    # 12 x 8 = 96 tokens: 64 + 32 key slots per tile
+    ((2, 22, 22), 121, False),  # 11 x 11 = 121 tokens: two 64-key half-tiles per tile
+    ((2, 16, 32), 128, True),   # 8 x 16 = 128 tokens
 ])
 def test_fused_step_matches_two_pass_and_oracle(ops, cuda_device, grid, tile, deterministic):
     """dsa_bsa_fwd_tile_stats (attention and the statistics of the same
@@ -207,13 +212,16 @@ def test_fused_step_matches_two_pass_and_oracle(ops, cuda_device, grid, tile, de
 
 
 @pytest.mark.parametrize("grid,tile", [((2, 18, 32), 64), ((2, 15, 26), 64), ((1, 20, 30), 100),
-                                       ((2, 16, 32), 128), ((4, 16, 16), 64)])
+                                       ((2, 16, 32), 128), ((4, 16, 16), 64), ((2, 12, 16), 96),
+                                       ((1, 18, 27), 81), ((2, 22, 22), 121), ((2, 14, 21), 49),
+                                       ((2, 12, 12), 36)])
 def test_fused_dense_step_matches_oracle(ops, cuda_device, grid, tile):
-    """The dense bootstrap through dsa_bsa_fwd_tile_stats (no CSR): 9 x 8
-    and 8 x 16 tiles take their statistics from the dense attention launch
-    (128-token blocks, unsplit); 5 x 13 and 10 x 10 (not a multiple of 8) and
-    8 x 8 tiles run the second pass; all against the oracle's _dense_route
-    statistics and output."""
+    """The dense bootstrap through dsa_bsa_fwd_tile_stats (no CSR), every
+    tile shape with its statistics from the attention launch: 9 x 8, 8 x 8,
+    12 x 8 and 8 x 16 tiles (a multiple of 8 of 64..128 tokens) on 128-token
+    blocks, unsplit; 5 x 13, 10 x 10, 9 x 9 and 11 x 11 on blocks of one tile
+    (4 waves); 7 x 7 and 6 x 6 on blocks of one tile in 2-wave workgroups; all
+    against the oracle's _dense_route statistics and output."""
     case, q, k, v = _tile_major_inputs(grid, 3, seed=sum(grid) + 1, tile=tile)
     qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
     out, lse, got = ops.bsa_fwd_tile_stats(qd, kd, vd, None, case.tile_shape)
@@ -227,6 +235,43 @@ def test_fused_dense_step_matches_oracle(ops, cuda_device, grid, tile):
     assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
     np.testing.assert_allclose(got["mass"].sum(-1).cpu().numpy(), case.tile / q.shape[1],
                                rtol=2e-3)
+
+
+@pytest.mark.parametrize("routed", [True, False])
+def test_fused_step_every_tile_size(ops, cuda_device, routed):
+    """dsa_bsa_fwd_tile_stats at tiles of 1..128 tokens (as 1 x t rows, 5
+    tiles per head), routed and dense, through every statistics instance they
+    select (2 or 4 waves; one or two half-tiles, the second of at most 32
+    keys or not; the gathered stream for 65..88 and 97..120; dense 128-token
+    blocks for multiples of 8 from 64) against the oracle: the statistics and
+    the output.  The fused sums take each probability in bf16, as P V does
+    (relative error up to 2^-8 per term), so cells of a few keys, such as the
+    one-key cells of 1-token tiles, are held to rtol 4e-3."""
+    import types
+    failures = []
+    for t in range(1, 129):
+        tiles = 5
+        tokens = tiles * t
+        q, k, v = clustered_qkv(tokens, 2, 128, group=t, seed=t, dtype=torch.bfloat16)
+        case = types.SimpleNamespace(tile=t, tile_shape=(1, t))
+        qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+        route = None
+        csr = None
+        if routed:
+            route = random_route(2, tiles, seed=t, keep=0.6).numpy()
+            route[..., tiles - 1] = True
+            csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=t)
+        out, _, got = ops.bsa_fwd_tile_stats(qd, kd, vd, csr, (1, t), deterministic=True)
+        torch.cuda.synchronize()
+        expected, expected_out = _oracle_stats(case, q, k, v, route)
+        try:
+            _compare_stats(got, expected, rtol=4e-3)
+            metrics = A.summarize(out.float().cpu().numpy(), expected_out)
+            assert metrics["max_absolute_error"] <= 2e-2, metrics
+            assert metrics["cosine_similarity"] >= 0.9995, metrics
+        except AssertionError as error:
+            failures.append((t, str(error)[:200]))
+    assert not failures, failures
 
 
 def test_fused_step_at_720p_tile_shape(ops, cuda_device):
