@@ -23,6 +23,7 @@ DSA_ELAUNCH = -3
 # Element types of the attention inputs (DSA_DTYPE_* in dsa.h).
 DSA_DTYPE_BF16 = 0
 DSA_DTYPE_F16 = 1
+DSA_DTYPE_F32 = 2  # the attention entry points only
 
 _c_int = ctypes.c_int32
 _c_i64 = ctypes.c_int64

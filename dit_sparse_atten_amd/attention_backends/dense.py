@@ -1,11 +1,12 @@
 """Dense attention backend on the libdsa block-sparse kernel with a full route.
 
 Mirrors ``DenseBackend`` of the reference (attention_backends/dense.py:12-48):
-same name, call signature, dtype handling (compute in ``dtype``, bfloat16 or
-float16, and return the caller's dtype; float32 compute raises ValueError, as
-every libdsa backend does) and output layout (contiguous [B, T, H, D]).  The reference
-calls SDPA; here the same hand-written HIP kernel as the sparse path runs with
-every key block listed, so dense and sparse numerics agree by construction.
+same name, call signature, dtype handling (compute in ``dtype``: bfloat16,
+float16 or float32, and return the caller's dtype) and output layout
+(contiguous [B, T, H, D]).  The reference calls SDPA; here the same
+hand-written HIP kernel as the sparse path runs with every key block listed,
+so dense and sparse numerics agree by construction (float32 runs the fp32
+matrix-core kernel).
 """
 
 from __future__ import annotations
@@ -41,7 +42,7 @@ class DenseBackend:
             raise NotImplementedError("The dense backend only supports global attention")
         if dropout_p:
             raise NotImplementedError("The dense backend does not implement attention dropout")
-        ops.dtype_code(dtype)  # bfloat16 or float16, else ValueError
+        ops.dtype_code(dtype, attention=True)  # bfloat16, float16 or float32
         output_dtype = q.dtype
         q = q.to(dtype)
         k = k.to(dtype)

@@ -183,10 +183,9 @@ class MatrixSparseBackend:
 
     def _sparse_attention(self, q, k, v, scale, layout, deterministic=False):
         c = self.config
-        # The reference computes in the input dtype; so do the kernels, for
-        # bfloat16 and float16 (float32 raises ValueError, as in every
-        # libdsa backend).
-        ops.dtype_code(q.dtype)
+        # The reference computes in the input dtype (sparse.py:700-708); so do
+        # the kernels: bfloat16, float16, or float32 on the fp32 kernel.
+        ops.dtype_code(q.dtype, attention=True)
         output_dtype = q.dtype
         k, v = k.to(q.dtype), v.to(q.dtype)
         # Jointly permuting Q/K/V is attention-equivalent; it only changes

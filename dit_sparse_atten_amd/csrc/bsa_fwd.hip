@@ -23,8 +23,9 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
             int32_t deterministic, float* lse, const char* who, BsaParams* p) {
   if (!q || !k || !v || !o || !strides)
     return dsa::set_error(DSA_EINVAL, "%s: null tensor or stride pointer", who);
-  if (dtype != DSA_BF16 && dtype != DSA_F16)
-    return dsa::set_error(DSA_EUNSUPPORTED, "%s: dtype %d unsupported (bf16 or fp16)", who, dtype);
+  if (dtype != DSA_BF16 && dtype != DSA_F16 && dtype != DSA_F32)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: dtype %d unsupported (bf16, fp16 or fp32)", who,
+                          dtype);
   if (batch <= 0 || heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
     return dsa::set_error(DSA_EINVAL, "%s: batch/heads/tokens must be positive", who);
   if (head_dim <= 0 || head_dim > kHeadDim || head_dim % 8 != 0)
@@ -86,6 +87,9 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
   p->rs_entries = 0;
   p->tile_h = p->tile_w = 0;
   p->stat_tile = p->stat_pad = 0;
+  p->drop_thresh = 0;
+  p->drop_scale = 1.f;
+  p->drop_seed_lo = p->drop_seed_hi = p->drop_offset = 0;
   p->scale = scale;
   p->scale_log2 = scale * 1.4426950408889634f;
   return DSA_OK;
@@ -95,6 +99,8 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
 // (launch order, then split partials; see launch_typed).
 int launch(int32_t dtype, BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
            const char* who) {
+  // fp32 inputs and dropout run the fp32-compute kernel (no scratch).
+  if (dtype == DSA_F32 || p.drop_thresh != 0) return bsa_launch_f32(p, dtype, stream, who);
   return dtype == DSA_F16 ? bsa_launch_f16(p, scratch, scratch_bytes, stream, who)
                           : launch_typed<__bf16>(p, scratch, scratch_bytes, stream, who);
 }
@@ -377,7 +383,8 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
   if (dense && entries < (int64_t)heads * tiles * tiles)
     return dsa::set_error(DSA_EINVAL, "%s: dense statistics need entries >= heads * tiles^2",
                           who);
-  const bool blocks128 = dense && token_stream(tile);
+  // (The fp32-compute kernel always runs blocks of one tile.)
+  const bool blocks128 = dense && dtype != DSA_F32 && token_stream(tile);
   BsaParams p;
   int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim,
                        blocks128 ? 128 : tile, row_ptr, col_idx, 1, scale, 0, deterministic, lse, who,
@@ -444,6 +451,11 @@ extern "C" int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* 
   dsa::clear_error();
   if (!lse || !mass || !strides)
     return dsa::set_error(DSA_EINVAL, "%s: lse, mass and strides are required", who);
+  // fp32 inputs: the fp32-compute kernel takes the mass from its own
+  // probabilities, on whole 128-token blocks.
+  if (dtype == DSA_F32 && tokens % 128 != 0)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: fp32 needs tokens a multiple of 128, got %d", who,
+                          tokens);
   BsaParams p;
   int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim, 128,
                        nullptr, nullptr, 1, scale, 0, 1, lse, who, &p);

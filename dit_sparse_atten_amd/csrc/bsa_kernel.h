@@ -101,6 +101,12 @@ struct BsaParams {
   // Stream slots per statistics tile: gathered stream block_pad, plain
   // stream 64 kNh (a tile per key block), dense token stream stat_tile.
   int32_t stat_pad;
+  // Attention dropout (dense calls, the fp32-compute kernel): a probability
+  // is kept when its Philox uniform is >= drop_thresh (0: no dropout), then
+  // scaled by drop_scale = 1 / (1 - dropout_p).
+  uint32_t drop_thresh;
+  float drop_scale;
+  uint32_t drop_seed_lo, drop_seed_hi, drop_offset;
 };
 
 // One split partial: O [128 rows][128 dims] relative to the row's reference
@@ -1242,3 +1248,6 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
 // fp16 instances (bsa_fwd_f16.hip).
 int bsa_launch_f16(bsa::BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
                    const char* who);
+// fp32-compute kernel (bsa_fwd_f32.hip): fp32 inputs (dtype DSA_F32), and
+// dense calls with dropout of any input type.
+int bsa_launch_f32(bsa::BsaParams p, int32_t dtype, hipStream_t stream, const char* who);

@@ -25,6 +25,7 @@ SOURCES = (
     "dsa_api.hip",
     "bsa_fwd.hip",
     "bsa_fwd_f16.hip",
+    "bsa_fwd_f32.hip",
     "block_mass.hip",
     "tile_stats.hip",
     "sampled_mass.hip",

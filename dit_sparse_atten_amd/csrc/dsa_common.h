@@ -33,6 +33,7 @@ typedef short dsa_i16x4 __attribute__((ext_vector_type(4)));
 // Input element types (the dtype codes of dsa.h).
 #define DSA_BF16 0
 #define DSA_F16 1
+#define DSA_F32 2
 
 namespace dsa {
 

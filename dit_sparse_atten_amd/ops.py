@@ -26,25 +26,30 @@ def _require_cuda(name, tensor):
         raise ValueError(f"{name} must be a CUDA (HIP) tensor; libdsa has no CPU path")
 
 
-# The 16-bit element types the kernels compute in (dtype codes of dsa.h).
+# The 16-bit element types every kernel computes in (dtype codes of dsa.h).
 KERNEL_DTYPES = {torch.bfloat16: _lib.DSA_DTYPE_BF16, torch.float16: _lib.DSA_DTYPE_F16}
+# The attention (bsa_fwd, bsa_fwd_tile_stats) also computes in float32.
+ATTENTION_DTYPES = {**KERNEL_DTYPES, torch.float32: _lib.DSA_DTYPE_F32}
 
 
-def dtype_code(dtype):
+def dtype_code(dtype, attention=False):
     """The libdsa dtype code of a torch dtype; ValueError for any other than
-    bfloat16 and float16 (the kernels have no float32 path)."""
-    if dtype not in KERNEL_DTYPES:
-        raise ValueError(f"libdsa computes in bfloat16 or float16, not {dtype}")
-    return KERNEL_DTYPES[dtype]
+    bfloat16 and float16, or also float32 for the attention
+    (``attention=True``)."""
+    table = ATTENTION_DTYPES if attention else KERNEL_DTYPES
+    if dtype not in table:
+        kinds = "bfloat16, float16 or float32" if attention else "bfloat16 or float16"
+        raise ValueError(f"libdsa computes in {kinds} here, not {dtype}")
+    return table[dtype]
 
 
-def _kernel_view(name, tensor, dtype=None):
-    """Return a [B,T,H,D] 16-bit view the kernel can read (copying only if
-    needed); ``dtype``, when given, is the element type every operand must share."""
+def _kernel_view(name, tensor, dtype=None, attention=False):
+    """Return a [B,T,H,D] view the kernel can read (copying only if needed);
+    ``dtype``, when given, is the element type every operand must share."""
     _require_cuda(name, tensor)
     if tensor.ndim != 4:
         raise ValueError(f"{name} must have shape [batch, tokens, heads, head_dim]")
-    dtype_code(tensor.dtype)
+    dtype_code(tensor.dtype, attention)
     if dtype is not None and tensor.dtype != dtype:
         raise ValueError(f"{name} must be {dtype} like q, got {tensor.dtype}")
     ok = (
@@ -118,9 +123,9 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     block and per key block that the route addresses: 128 for ``flex_reuse``,
     the spatial tile size for the matrix-sparse backend.
 
-    q: [B,Tq,H,D], k/v: [B,Tk,H,D], D a multiple of 8 up to 128, all bf16 or
-    all fp16 (the compute type), on a HIP device, any strides with a
-    contiguous head dim.  ``causal`` (dense calls only): query t attends keys
+    q: [B,Tq,H,D], k/v: [B,Tk,H,D], D a multiple of 8 up to 128, all bf16,
+    all fp16 or all fp32 (the compute type; fp32 runs the fp32 matrix-core
+    kernel), on a HIP device, any strides with a contiguous head dim.  ``causal`` (dense calls only): query t attends keys
     k <= t, as SDPA's is_causal.  ``deterministic``: results reproducible bit
     for bit; otherwise a routed call may start each row's key walk where the
     other rows of its head are reading (better L2 reuse), which changes the
@@ -130,9 +135,9 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     natural-log LSE [B,H,Tq] fp32.
     """
     lib = _lib.load()
-    q = _kernel_view("q", q)
-    k = _kernel_view("k", k, q.dtype)
-    v = _kernel_view("v", v, q.dtype)
+    q = _kernel_view("q", q, attention=True)
+    k = _kernel_view("k", k, q.dtype, attention=True)
+    v = _kernel_view("v", v, q.dtype, attention=True)
     batch, q_tokens, heads, head_dim = q.shape
     if k.shape[0] != batch or v.shape[0] != batch or k.shape[2] != heads or v.shape[2] != heads:
         raise ValueError("q, k and v must agree on batch and heads")
@@ -174,15 +179,17 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
         + list(out.stride()[:3]))
     if not 1 <= block_size <= 128:
         raise ValueError(f"block_size {block_size} unsupported (1..128)")
-    workspace_bytes = lib.dsa_bsa_workspace_bytes_block(batch, heads, kv_tokens, head_dim,
-                                                        block_size)
     # Room for the split partials of the last round of workgroups (none when
-    # the key range is too short to split); the caching allocator recycles it.
+    # the key range is too short to split; the fp32 kernel takes none); the
+    # caching allocator recycles it.
+    workspace_bytes = 0 if q.dtype == torch.float32 else lib.dsa_bsa_workspace_bytes_block(
+        batch, heads, kv_tokens, head_dim, block_size)
     workspace = (torch.empty(workspace_bytes, dtype=torch.uint8, device=q.device)
                  if workspace_bytes else None)
     with torch.cuda.device(q.device):
         status = lib.dsa_bsa_fwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dtype_code(q.dtype), strides,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            dtype_code(q.dtype, attention=True), strides,
             batch, q_tokens, kv_tokens, heads, head_dim, block_size,
             row_ptr.data_ptr() if row_ptr is not None else None,
             col_idx.data_ptr() if col_idx is not None else None,
@@ -278,12 +285,13 @@ def bsa_fwd_block_mass(q, k, v, scale=None):
     dense attention and ``_block_attention_mass``, attention_backends/
     flex.py:254-272, 158-202).  With T a multiple of 128 the mass comes from
     the attention launch's own probabilities; otherwise the call runs the
-    attention and then the block-mass pass.
+    attention and then the block-mass pass (bf16 and fp16; float32 inputs
+    need T a multiple of 128).
     """
     lib = _lib.load()
-    q = _kernel_view("q", q)
-    k = _kernel_view("k", k, q.dtype)
-    v = _kernel_view("v", v, q.dtype)
+    q = _kernel_view("q", q, attention=True)
+    k = _kernel_view("k", k, q.dtype, attention=True)
+    v = _kernel_view("v", v, q.dtype, attention=True)
     batch, tokens, heads, head_dim = q.shape
     if batch != 1 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError("Flex bootstrap supports batch-1 self-attention")
@@ -303,7 +311,8 @@ def bsa_fwd_block_mass(q, k, v, scale=None):
                  if workspace_bytes else None)
     with torch.cuda.device(q.device):
         status = lib.dsa_bsa_fwd_block_mass(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dtype_code(q.dtype),
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            dtype_code(q.dtype, attention=True),
             strides, tokens, heads, head_dim, float(scale), lse.data_ptr(), mass.data_ptr(),
             workspace.data_ptr() if workspace is not None else None, workspace_bytes,
             _stream_handle(q.device))
@@ -383,9 +392,9 @@ def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False
     pass runs.
     """
     lib = _lib.load()
-    q = _kernel_view("q", q)
-    k = _kernel_view("k", k, q.dtype)
-    v = _kernel_view("v", v, q.dtype)
+    q = _kernel_view("q", q, attention=True)
+    k = _kernel_view("k", k, q.dtype, attention=True)
+    v = _kernel_view("v", v, q.dtype, attention=True)
     batch, tokens, heads, head_dim = q.shape
     if batch != 1 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError("tile statistics support batch-1 self-attention")
@@ -425,8 +434,8 @@ def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False
                  if workspace_bytes else None)
     with torch.cuda.device(q.device):
         status = lib.dsa_bsa_fwd_tile_stats(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dtype_code(q.dtype),
-            strides, tokens, heads, head_dim, tile_h, tile_w,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            dtype_code(q.dtype, attention=True), strides, tokens, heads, head_dim, tile_h, tile_w,
             csr.row_ptr.data_ptr() if csr is not None else None,
             csr.col_idx.data_ptr() if csr is not None else None,
             entries, float(scale), int(bool(deterministic)),

@@ -35,10 +35,15 @@ const char* dsa_last_error(void);
 /* Element types of the attention inputs (the `dtype` arguments). */
 #define DSA_DTYPE_BF16 0
 #define DSA_DTYPE_F16 1
+/* fp32: dsa_bsa_fwd, dsa_bsa_fwd_noalloc, dsa_bsa_fwd_tile_stats and
+ * dsa_bsa_fwd_block_mass (tokens a multiple of 128) only. */
+#define DSA_DTYPE_F32 2
 
 /*
- * Block-sparse attention forward, bf16 or fp16 in and out (dtype), fp32 online
- * softmax; the matrix products run in the input type with fp32 accumulation.
+ * Block-sparse attention forward, bf16, fp16 or fp32 in and out (dtype), fp32
+ * online softmax; the matrix products run in the input type with fp32
+ * accumulation (fp32 inputs: fp32 products on v_mfma_f32_32x32x2_f32, the
+ * probabilities unrounded).
  * Replaces FlexAttention over a BlockMask (attention_backends/flex.py:379-399
  * `_flex_output`, flex.py:360-376) and, with row_ptr == col_idx == NULL, dense
  * SDPA (attention_backends/dense.py:14-48).
