@@ -52,6 +52,14 @@ SIGNATURES = {
         _c_ptr, _c_ptr, _c_int,                    # row_ptr, col_idx, route_batches
         _c_float, _c_int, _c_int, _c_ptr, _c_ptr,  # scale, causal, deterministic, lse, stream
     )),
+    "dsa_bsa_fwd_dropout": (_c_int, (
+        _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,  # q, k, v, o, dtype
+        ctypes.POINTER(_c_i64),                    # strides[12]
+        _c_int, _c_int, _c_int, _c_int, _c_int,    # batch, q_tokens, kv_tokens, heads, head_dim
+        _c_float, _c_int, _c_float,                # scale, causal, dropout_p
+        ctypes.c_uint64, ctypes.c_uint32,          # seed, offset
+        _c_ptr, _c_ptr,                            # lse, stream
+    )),
     "dsa_bsa_workspace_bytes": (_c_size, (_c_int, _c_int, _c_int, _c_int)),
     "dsa_bsa_workspace_bytes_block": (_c_size, (_c_int, _c_int, _c_int, _c_int, _c_int)),
     "dsa_sampled_mass": (_c_int, (

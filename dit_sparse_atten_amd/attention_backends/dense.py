@@ -1,8 +1,9 @@
 """Dense attention backend on the libdsa block-sparse kernel with a full route.
 
 Mirrors ``DenseBackend`` of the reference (attention_backends/dense.py:12-48):
-same name, call signature, dtype handling (compute in ``dtype``: bfloat16,
-float16 or float32, and return the caller's dtype) and output layout
+same name, call signature, dropout (``dropout_p`` on the attention
+probabilities, as SDPA applies it), dtype handling (compute in ``dtype``:
+bfloat16, float16 or float32, and return the caller's dtype) and output layout
 (contiguous [B, T, H, D]).  The reference calls SDPA; here the same
 hand-written HIP kernel as the sparse path runs with every key block listed,
 so dense and sparse numerics agree by construction (float32 runs the fp32
@@ -40,8 +41,6 @@ class DenseBackend:
         del q_lens, k_lens, deterministic, version
         if window_size != (-1, -1):
             raise NotImplementedError("The dense backend only supports global attention")
-        if dropout_p:
-            raise NotImplementedError("The dense backend does not implement attention dropout")
         ops.dtype_code(dtype, attention=True)  # bfloat16, float16 or float32
         output_dtype = q.dtype
         q = q.to(dtype)
@@ -49,7 +48,10 @@ class DenseBackend:
         v = v.to(dtype)
         if q_scale is not None:
             q = q * q_scale
-        output = ops.bsa_fwd(q, k, v, scale=softmax_scale, causal=causal)
+        # dropout_p > 0: SDPA's dropout on the probabilities, drawn from a
+        # Philox stream seeded from torch's generator (not torch's own stream).
+        output = ops.bsa_fwd(q, k, v, scale=softmax_scale, causal=causal,
+                             dropout_p=float(dropout_p))
         return output.to(output_dtype)
 
 

@@ -339,6 +339,31 @@ extern "C" int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, 
   return launch(dtype, p, area, kScratchBytes, stream, "dsa_bsa_fwd_noalloc");
 }
 
+extern "C" int dsa_bsa_fwd_dropout(const void* q, const void* k, const void* v, void* o,
+                                   int32_t dtype, const int64_t* strides, int32_t batch,
+                                   int32_t q_tokens, int32_t kv_tokens, int32_t heads,
+                                   int32_t head_dim, float scale, int32_t causal, float dropout_p,
+                                   uint64_t seed, uint32_t offset, float* lse,
+                                   hipStream_t stream) {
+  const char* who = "dsa_bsa_fwd_dropout";
+  dsa::clear_error();
+  if (!(dropout_p > 0.f && dropout_p < 1.f))
+    return dsa::set_error(DSA_EINVAL, "%s: dropout_p must be in (0, 1), got %g", who,
+                          (double)dropout_p);
+  BsaParams p;
+  const int status = prepare(q, k, v, o, dtype, strides, batch, q_tokens, kv_tokens, heads,
+                             head_dim, 128, nullptr, nullptr, 1, scale, causal, 1, lse, who, &p);
+  if (status != DSA_OK) return status;
+  // keep = (u >= round(dropout_p 2^32)), at least 1 (no uniform is below 0).
+  const double thresh = std::nearbyint((double)dropout_p * 4294967296.0);
+  p.drop_thresh = (uint32_t)std::min(std::max(thresh, 1.0), 4294967295.0);
+  p.drop_scale = 1.f / (1.f - dropout_p);
+  p.drop_seed_lo = (uint32_t)(seed & 0xffffffffu);
+  p.drop_seed_hi = (uint32_t)(seed >> 32);
+  p.drop_offset = offset;
+  return launch(dtype, p, nullptr, 0, stream, who);
+}
+
 extern "C" size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t tokens,
                                                          int32_t head_dim, int32_t tile_h,
                                                          int32_t tile_w, int64_t entries) {

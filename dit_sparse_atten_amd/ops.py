@@ -116,7 +116,7 @@ def csr_from_route(route, block_size=128):
 
 
 def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_size=128,
-            causal=False, deterministic=False):
+            causal=False, deterministic=False, dropout_p=0.0, seed=None, offset=0):
     """Block-sparse (or, with ``csr=None``, dense) attention forward on the GPU.
 
     ``block_size`` (1..128) is the number of consecutive tokens per query
@@ -129,10 +129,14 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     k <= t, as SDPA's is_causal.  ``deterministic``: results reproducible bit
     for bit; otherwise a routed call may start each row's key walk where the
     other rows of its head are reading (better L2 reuse), which changes the
-    fp32 accumulation order and so the last bits from run to run.  Returns
-    O [B,Tq,H,D] in that type
-    (contiguous unless ``out`` is given) and, with ``return_lse``, the
-    natural-log LSE [B,H,Tq] fp32.
+    fp32 accumulation order and so the last bits from run to run.
+    ``dropout_p`` in (0, 1) (dense calls only): dropout on the attention
+    probabilities, as SDPA's ``dropout_p``, computed in fp32 with a
+    Philox4x32-10 mask drawn from ``seed`` (default: a seed from torch's CPU
+    generator) and ``offset`` (dsa_bsa_fwd_dropout).  Returns O [B,Tq,H,D]
+    in the input type (contiguous unless ``out`` is given) and, with
+    ``return_lse``, the natural-log LSE [B,H,Tq] fp32 (of the undropped
+    softmax).
     """
     lib = _lib.load()
     q = _kernel_view("q", q, attention=True)
@@ -177,6 +181,22 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     strides = _lib.int64_array(
         list(q.stride()[:3]) + list(k.stride()[:3]) + list(v.stride()[:3])
         + list(out.stride()[:3]))
+    if dropout_p:
+        if csr is not None:
+            raise ValueError("dropout takes dense attention only")
+        if not 0.0 < dropout_p < 1.0:
+            raise ValueError(f"dropout_p must be in (0, 1), got {dropout_p}")
+        if seed is None:
+            seed = int(torch.randint(0, 2 ** 63 - 1, (), dtype=torch.int64).item())
+        with torch.cuda.device(q.device):
+            status = lib.dsa_bsa_fwd_dropout(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                dtype_code(q.dtype, attention=True), strides, batch, q_tokens, kv_tokens,
+                heads, head_dim, float(scale), int(bool(causal)), float(dropout_p),
+                int(seed) & (2 ** 64 - 1), int(offset) & (2 ** 32 - 1),
+                lse.data_ptr() if lse is not None else None, _stream_handle(q.device))
+        _lib.check(status, "dsa_bsa_fwd_dropout")
+        return (out, lse) if return_lse else out
     if not 1 <= block_size <= 128:
         raise ValueError(f"block_size {block_size} unsupported (1..128)")
     # Room for the split partials of the last round of workgroups (none when

@@ -149,6 +149,28 @@ int dsa_bsa_fwd_noalloc(const void* q, const void* k, const void* v, void* o, in
                         hipStream_t stream);
 
 /*
+ * Dense attention with dropout on the attention probabilities: the
+ * reference's DenseBackend with dropout_p > 0, which hands dropout_p to SDPA
+ * (attention_backends/dense.py:40-47; flex_reuse sends such calls to dense,
+ * flex.py:655-668).  O[b,t,h] = sum_k keep[b,h,t,k] p[b,h,t,k] v[b,k,h] /
+ * (1 - dropout_p) with p the softmax of scale q.k (every key counts in the
+ * normaliser, as dropout after the softmax does) and keep = (u >=
+ * round(dropout_p 2^32)) for the uniform u of key k: word k % 4 of
+ * Philox4x32-10 with counter (k / 4, t, b * heads + h, offset) and key
+ * (seed & 0xffffffff, seed >> 32) (Salmon et al., SC 2011).  Arguments as
+ * dsa_bsa_fwd for a dense call (no route; causal allowed); dropout_p in
+ * (0, 1).  Computes in fp32 for every dtype (the fp32-compute kernel) and
+ * takes no workspace.  The reference's random stream is torch's and is not
+ * reproduced: the same seed gives the same mask here, not the same mask as
+ * SDPA.
+ */
+int dsa_bsa_fwd_dropout(const void* q, const void* k, const void* v, void* o, int32_t dtype,
+                        const int64_t* strides, int32_t batch, int32_t q_tokens,
+                        int32_t kv_tokens, int32_t heads, int32_t head_dim, float scale,
+                        int32_t causal, float dropout_p, uint64_t seed, uint32_t offset,
+                        float* lse, hipStream_t stream);
+
+/*
  * Sampled block-mass estimate for one batch-1 self-attention call, bf16 or
  * fp16 Q/K (dtype).  Replaces `_sampled_block_mass`
  * (attention_backends/flex.py:205-251): `samples` evenly spaced tokens per

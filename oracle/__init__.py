@@ -45,6 +45,11 @@ from the reference imported in the build container):
                and sparse_tile_shape / tile_major_permutation (sparse.py:51-138):
                reference golden (spatial_layout.npz, the full 57,600-token
                permutation and neighbour table), known answers, bijection.
+  dropout      philox4x32_10, keep_mask, dropout_attention (SDPA's dropout as
+               DenseBackend hands it on, dense.py:40-47; the mask from
+               Philox4x32-10, Salmon et al. 2011): Random123's three
+               known-answer vectors, keep fraction 1 - p, a planted wrong
+               multiplier, dropout_p -> 0 equal to the attention closed form.
   sparse_path  group_indices, sparse_chunk, dense_route, SparsePathCase
                (sparse.py:184-233, 376-406, 670-751, 794-930): reference golden
                on config 0 (bootstrap route, mass, outputs, one sparse step).
