@@ -125,8 +125,10 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
 
     q: [B,Tq,H,D], k/v: [B,Tk,H,D], D a multiple of 8 up to 128, all bf16,
     all fp16 or all fp32 (the compute type; fp32 runs the fp32 matrix-core
-    kernel), on a HIP device, any strides with a contiguous head dim.  ``causal`` (dense calls only): query t attends keys
-    k <= t, as SDPA's is_causal.  ``deterministic``: results reproducible bit
+    kernel), on a HIP device, any strides with a contiguous head dim.
+    ``causal`` (dense calls only): query t attends keys k <= t, as SDPA's
+    is_causal.  ``deterministic`` (or
+    ``torch.use_deterministic_algorithms(True)``): results reproducible bit
     for bit; otherwise a routed call may start each row's key walk where the
     other rows of its head are reading (better L2 reuse), which changes the
     fp32 accumulation order and so the last bits from run to run.
@@ -199,6 +201,7 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
         return (out, lse) if return_lse else out
     if not 1 <= block_size <= 128:
         raise ValueError(f"block_size {block_size} unsupported (1..128)")
+    deterministic = bool(deterministic) or torch.are_deterministic_algorithms_enabled()
     # Room for the split partials of the last round of workgroups (none when
     # the key range is too short to split; the fp32 kernel takes none); the
     # caching allocator recycles it.
@@ -409,7 +412,9 @@ def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False
     [1, H, T] and ``stats`` as :func:`tile_stats` returns them.  Every call
     gets its statistics from the attention launch itself (per query row and
     key tile), which a short second launch combines per cell; no second QK
-    pass runs.
+    pass runs.  ``deterministic`` as in :func:`bsa_fwd`: without it (and
+    without torch's deterministic mode) a routed call's output, mass and
+    centroids can differ in the last bits from run to run.
     """
     lib = _lib.load()
     q = _kernel_view("q", q, attention=True)
@@ -436,6 +441,7 @@ def bsa_fwd_tile_stats(q, k, v, csr, tile_shape, scale=None, deterministic=False
         entries = heads * tiles * tiles
     if scale is None:
         scale = head_dim ** -0.5
+    deterministic = bool(deterministic) or torch.are_deterministic_algorithms_enabled()
     out = torch.empty((1, tokens, heads, head_dim), dtype=q.dtype, device=q.device)
     lse = torch.empty((1, heads, tokens), dtype=torch.float32, device=q.device)
     shape = (heads, tiles, tiles)

@@ -261,3 +261,52 @@ def test_config4_denoising_loop_at_full_shape(cuda_device, threshold, expected):
     assert summary["released_routes"] == 58 and not backend.state
     assert summary["dense_dispatched_routes"] == (58 if threshold else 0)
     context.reset_runtime_state()
+
+
+def _config4_latents(cuda_device):
+    """The config-4 loop without dense dispatch (every routed step runs the
+    block-sparse kernel), from fixed seeds; returns the final latents."""
+    from dit_sparse_atten_amd.attention_backends import context
+    from dit_sparse_atten_amd.attention_backends.flex import FlexReuseBackend, FlexReuseConfig
+    from dit_sparse_atten_amd.wan_dit import WanDiT, denoise
+    context.reset_runtime_state()
+    model = WanDiT(device=cuda_device, seed=11)
+    gen = torch.Generator(device=cuda_device).manual_seed(12)
+    latents = torch.randn(1, 16, 16, 90, 160, device=cuda_device, generator=gen).bfloat16()
+    cond = torch.randn(1, 512, 4096, device=cuda_device, generator=gen).bfloat16()
+    uncond = torch.randn(1, 512, 4096, device=cuda_device, generator=gen).bfloat16()
+    backend = FlexReuseBackend(FlexReuseConfig(
+        bootstrap_mode="sampled", prefetch_sampled_bootstrap=True, sampled_update_interval=2,
+        prefetch_sampled_update=False, route_samples=16, route_persistence=0.5,
+        mass_target=0.95, keep=0.625, dense_route_threshold=None, total_steps=5,
+        spatial_reorder=True))
+    out = denoise(model, backend, latents, cond, uncond, steps=5)
+    torch.cuda.synchronize()
+    context.reset_runtime_state()
+    assert backend.phase_counts["sparse_reuse"] == 232
+    return out
+
+
+def test_config4_loop_reproducibility(cuda_device):
+    """Two runs of the config-4 loop from the same seeds.  Under
+    torch.use_deterministic_algorithms(True) every routed call walks its key
+    blocks in CSR order, and the latents are identical bit for bit.  By
+    default routed calls take the aligned walk, whose accumulation order
+    depends on timing: the test reports whether those two runs agreed (they
+    may not, and in a multi-step loop the last-bit differences can reach
+    later layers' routes)."""
+    torch.use_deterministic_algorithms(True, warn_only=True)
+    try:
+        first = _config4_latents(cuda_device)
+        second = _config4_latents(cuda_device)
+    finally:
+        torch.use_deterministic_algorithms(False)
+    assert torch.equal(first, second)
+    plain = [_config4_latents(cuda_device) for _ in range(2)]
+    assert all(bool(torch.isfinite(x.float()).all()) for x in plain)
+    differ = (plain[0].float() - plain[1].float()).abs()
+    print(f"default (aligned walk) runs identical: {torch.equal(plain[0], plain[1])}; "
+          f"max |difference| {differ.max().item():.3e}, "
+          f"elements that differ {int((differ > 0).sum().item())} of {differ.numel()}; "
+          f"deterministic vs default max |difference| "
+          f"{(first.float() - plain[0].float()).abs().max().item():.3e}")
