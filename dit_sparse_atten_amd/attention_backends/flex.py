@@ -419,6 +419,9 @@ class FlexReuseBackend:
             and dropout_p == 0
             and not causal
             and window_size == (-1, -1)
+            # The route estimates (sampled and exact block mass) take head
+            # dims up to 128; wider heads run dense.
+            and q.shape[-1] <= ops.HEAD_DIM
         )
         if not supported:
             return self.dense(q, k, v, **dense_kwargs)

@@ -278,7 +278,8 @@ class MatrixSparseBackend:
         })
 
     def __call__(self, q, k, v, softmax_scale=None, **kwargs):
-        if q.shape[1] == k.shape[1] and q.shape[0] == 1:
+        # The tile statistics take head dims up to 128; wider heads run dense.
+        if q.shape[1] == k.shape[1] and q.shape[0] == 1 and q.shape[-1] <= ops.HEAD_DIM:
             attention_id, _, _, grid = routing_context(include_grid=True)
             if self.config.first_layer_dense and attention_id == 0:
                 return self.dense(q, k, v, softmax_scale=softmax_scale, **kwargs)

@@ -28,9 +28,9 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                           dtype);
   if (batch <= 0 || heads <= 0 || q_tokens <= 0 || kv_tokens <= 0)
     return dsa::set_error(DSA_EINVAL, "%s: batch/heads/tokens must be positive", who);
-  if (head_dim <= 0 || head_dim > kHeadDim || head_dim % 8 != 0)
+  if (head_dim <= 0 || head_dim > 2 * kHeadDim || head_dim % 8 != 0)
     return dsa::set_error(DSA_EUNSUPPORTED,
-                          "%s: head_dim %d unsupported (a multiple of 8 up to 128)", who, head_dim);
+                          "%s: head_dim %d unsupported (a multiple of 8 up to 256)", who, head_dim);
   if (causal != 0 && causal != 1)
     return dsa::set_error(DSA_EINVAL, "%s: causal must be 0 or 1", who);
   if (deterministic != 0 && deterministic != 1)
@@ -99,8 +99,10 @@ int prepare(const void* q, const void* k, const void* v, void* o, int32_t dtype,
 // (launch order, then split partials; see launch_typed).
 int launch(int32_t dtype, BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
            const char* who) {
-  // fp32 inputs and dropout run the fp32-compute kernel (no scratch).
-  if (dtype == DSA_F32 || p.drop_thresh != 0) return bsa_launch_f32(p, dtype, stream, who);
+  // fp32 inputs, dropout and head dims above 128 run the fp32-compute kernel
+  // (no scratch).
+  if (dtype == DSA_F32 || p.drop_thresh != 0 || p.head_dim > kHeadDim)
+    return bsa_launch_f32(p, dtype, stream, who);
   return dtype == DSA_F16 ? bsa_launch_f16(p, scratch, scratch_bytes, stream, who)
                           : launch_typed<__bf16>(p, scratch, scratch_bytes, stream, who);
 }
@@ -403,6 +405,9 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
     return dsa::set_error(DSA_EINVAL, "%s: %d tokens are not whole %d-token tiles", who, tokens,
                           tile);
   if (entries < 0) return dsa::set_error(DSA_EINVAL, "%s: entries must be >= 0", who);
+  if (head_dim > kHeadDim)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: head_dim %d unsupported (statistics: up to 128)",
+                          who, head_dim);
   const int32_t tiles = tokens / tile;
   const bool dense = row_ptr == nullptr;
   if (dense && entries < (int64_t)heads * tiles * tiles)
@@ -481,6 +486,9 @@ extern "C" int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* 
   if (dtype == DSA_F32 && tokens % 128 != 0)
     return dsa::set_error(DSA_EUNSUPPORTED, "%s: fp32 needs tokens a multiple of 128, got %d", who,
                           tokens);
+  if (head_dim > kHeadDim)
+    return dsa::set_error(DSA_EUNSUPPORTED, "%s: head_dim %d unsupported (up to 128)", who,
+                          head_dim);
   BsaParams p;
   int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim, 128,
                        nullptr, nullptr, 1, scale, 0, 1, lse, who, &p);

@@ -1,6 +1,6 @@
 // Attention forward in fp32 arithmetic on the matrix cores (gfx950): the
-// float32 calls (fp32 in and out), and dense calls with attention dropout for
-// every input type.
+// float32 calls (fp32 in and out), dense calls with attention dropout, and
+// calls of head dims 136..256, for every input type.
 //
 // Replaces, for those calls, the SDPA of the reference's DenseBackend
 // (attention_backends/dense.py:34-47, which computes in the `dtype` it is
@@ -14,7 +14,7 @@
 //    query rows are the B operand's columns, so each lane's 16 accumulators
 //    belong to one query row, as in the 16-bit kernels (lane (g, i) holds
 //    key 8 (r >> 2) + 4 g + (r & 3) of accumulator r, for row i).  In step s
-//    of S^T, lane half g supplies dim 64 g + s: its row's Q from 64
+//    of S^T, lane half g supplies dim (kD / 2) g + s: its row's Q from kD / 2
 //    registers, key row i's K from LDS.  In O^T, step r takes each lane
 //    half's own probability of accumulator r as B, and as A the four dims
 //    4 i .. 4 i + 3 of that key's V row (one LDS read, one element per output
@@ -29,6 +29,10 @@
 //    unnormalised mass log2 sum 2^(scale_log2 s) and its mass-weighted mean
 //    key offsets, in the format the 16-bit kernels write (rs_logm, rs_mean)
 //    for tile_stats_reduce_kernel;
+//  * kD = 256 (head dims 136..256): S^T runs over all 256 dims (128 Q
+//    registers per lane), and O is computed in two launches of 128 output
+//    dims each (`dim0` = 0, 128), each staging only its half of V, so the O
+//    accumulators stay at 64 registers; the second launch recomputes S;
 //  * kDropout (dense only): each probability enters P V as keep * p /
 //    (1 - dropout_p); the normaliser counts every key, as dropout applied
 //    after the softmax does.  keep = (u >= drop_thresh) for a uniform 32-bit
@@ -43,8 +47,8 @@
 namespace bsa {
 namespace {
 
-constexpr int kSubKeys = 32;                       // keys per staged sub-tile
-constexpr int kSubFloats = kSubKeys * kHeadDim;    // 16 KB of K or V in fp32
+constexpr int kSubKeys = 32;  // keys per staged sub-tile (16 KB of V in fp32, 16 or 32 KB of K)
+constexpr int kMaxHeadDim = 256;
 
 template <typename T>
 __device__ __forceinline__ dsa_f32x4 load4(const T* ptr) {
@@ -90,11 +94,17 @@ __device__ __forceinline__ dsa_u32x4 philox4x32_10(dsa_u32x4 c, uint32_t k0, uin
   return c;
 }
 
-template <typename T, bool kRouted, bool kStats, bool kDropout>
-__global__ void __launch_bounds__(256, 2) bsa_fwd_f32_kernel(BsaParams p) {
+// kD: the dims S^T runs over (128, or 256 for head dims 136..256); dim0: the
+// first of the 128 output dims this launch computes.
+template <typename T, int kD, bool kRouted, bool kStats, bool kDropout>
+__global__ void __launch_bounds__(256, kD == 128 ? 2 : 1) bsa_fwd_f32_kernel(BsaParams p,
+                                                                            int dim0) {
   static_assert(!(kDropout && (kRouted || kStats)), "dropout: dense attention only");
-  __shared__ __attribute__((aligned(16))) float ks[2][kSubFloats];
-  __shared__ __attribute__((aligned(16))) float vs[2][kSubFloats];
+  static_assert(!(kStats && kD != 128), "statistics: head dims up to 128");
+  constexpr int kHalfD = kD / 2;      // dims per lane half in S^T
+  constexpr int kRowChunks = kD / 4;  // 16-byte chunks of a staged K row
+  __shared__ __attribute__((aligned(16))) float ks[2][kSubKeys * kD];
+  __shared__ __attribute__((aligned(16))) float vs[2][kSubKeys * kHeadDim];
   __shared__ dsa_f32x2 offs[kStats ? 128 : 1];
 
   const int tid = threadIdx.x;
@@ -129,14 +139,16 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_f32_kernel(BsaParams p) {
   const bool wave_active = wave * 32 < p.block;
   const int tq_c = tq < p.q_tokens ? tq : p.q_tokens - 1;
 
-  // Dims 64 g .. 64 g + 63 of the lane's query row (zeros past head_dim).
-  float qreg[64];
+  // Dims kHalfD g .. kHalfD g + kHalfD - 1 of the lane's query row (zeros
+  // past head_dim).
+  float qreg[kHalfD];
   {
     const T* qrow = static_cast<const T*>(p.q) + b * p.q_sb + h * p.q_sh +
-                    (int64_t)tq_c * p.q_st + 64 * g;
+                    (int64_t)tq_c * p.q_st + kHalfD * g;
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const dsa_f32x4 x = 64 * g + 4 * u < p.head_dim ? load4(qrow + 4 * u) : dsa_f32x4{0, 0, 0, 0};
+    for (int u = 0; u < kHalfD / 4; ++u) {
+      const dsa_f32x4 x =
+          kHalfD * g + 4 * u < p.head_dim ? load4(qrow + 4 * u) : dsa_f32x4{0, 0, 0, 0};
 #pragma unroll
       for (int e = 0; e < 4; ++e) qreg[4 * u + e] = x[e];
     }
@@ -165,25 +177,37 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_f32_kernel(BsaParams p) {
   auto keys_of = [&](int kb) -> int { return min(p.block, p.kv_tokens - kb * p.block); };
 
   // Sub-tile staging: thread t moves elements 4 c .. 4 c + 3 of key rows
-  // r = (256 u + t) / 32 (u = 0..3), c = t % 32; rows past the sequence and
-  // dims past head_dim stage zeros.
-  dsa_f32x4 kreg[4], vreg[4];
+  // r = (256 u + t) / (row chunks), c = t % (row chunks): every dim of K, and
+  // dims dim0 .. dim0 + 127 of V; rows past the sequence and dims past
+  // head_dim stage zeros.
+  constexpr int kKLoads = kSubKeys * kRowChunks / 256, kVLoads = kSubKeys * 32 / 256;
+  dsa_f32x4 kreg[kKLoads], vreg[kVLoads];
   auto fetch = [&](int kb, int st) {
     const int key0 = kb * p.block + st * kSubKeys;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int idx = u * 256 + tid, r = idx >> 5, c = idx & 31;
+    for (int u = 0; u < kKLoads; ++u) {
+      const int idx = u * 256 + tid, r = idx / kRowChunks, c = idx % kRowChunks;
       const int key = key0 + r;
       const bool ok = key < p.kv_tokens && 4 * c < p.head_dim;
       kreg[u] = ok ? load4(kbase + (int64_t)key * p.k_st + 4 * c) : dsa_f32x4{0, 0, 0, 0};
-      vreg[u] = ok ? load4(vbase + (int64_t)key * p.v_st + 4 * c) : dsa_f32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < kVLoads; ++u) {
+      const int idx = u * 256 + tid, r = idx >> 5, c = idx & 31;
+      const int key = key0 + r;
+      const bool ok = key < p.kv_tokens && dim0 + 4 * c < p.head_dim;
+      vreg[u] = ok ? load4(vbase + (int64_t)key * p.v_st + dim0 + 4 * c) : dsa_f32x4{0, 0, 0, 0};
     }
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kKLoads; ++u) {
+      const int idx = u * 256 + tid, r = idx / kRowChunks, c = idx % kRowChunks;
+      *reinterpret_cast<dsa_f32x4*>(&ks[buf][r * kD + 4 * (c ^ (r & 15))]) = kreg[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kVLoads; ++u) {
       const int idx = u * 256 + tid, r = idx >> 5, c = idx & 31;
-      *reinterpret_cast<dsa_f32x4*>(&ks[buf][r * kHeadDim + 4 * (c ^ (r & 15))]) = kreg[u];
       *reinterpret_cast<dsa_f32x4*>(&vs[buf][r * kHeadDim + 4 * c]) = vreg[u];
     }
   };
@@ -204,11 +228,11 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_f32_kernel(BsaParams p) {
     dsa_f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
-    const float* krow = &ks[buf][qi * kHeadDim];
+    const float* krow = &ks[buf][qi * kD];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const dsa_f32x4 kv =
-          *reinterpret_cast<const dsa_f32x4*>(krow + 4 * ((16 * g + u) ^ (qi & 15)));
+    for (int u = 0; u < kHalfD / 4; ++u) {
+      const dsa_f32x4 kv = *reinterpret_cast<const dsa_f32x4*>(
+          krow + 4 * (((kHalfD / 4) * g + u) ^ (qi & 15)));
 #pragma unroll
       for (int e = 0; e < 4; ++e) s = mfma_f32(kv[e], qreg[4 * u + e], s);
     }
@@ -337,11 +361,11 @@ __global__ void __launch_bounds__(256, 2) bsa_fwd_f32_kernel(BsaParams p) {
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
       const int m = 8 * (rr >> 2) + 4 * g + (rr & 3);
-      if (4 * m < p.head_dim)
-        store4(orow + 4 * m, dsa_f32x4{oacc[0][rr] * inv, oacc[1][rr] * inv, oacc[2][rr] * inv,
-                                       oacc[3][rr] * inv});
+      if (dim0 + 4 * m < p.head_dim)
+        store4(orow + dim0 + 4 * m, dsa_f32x4{oacc[0][rr] * inv, oacc[1][rr] * inv,
+                                              oacc[2][rr] * inv, oacc[3][rr] * inv});
     }
-    if (p.lse && g == 0)
+    if (p.lse && g == 0 && dim0 == 0)
       p.lse[((int64_t)b * p.heads + h) * p.q_tokens + tq] =
           l_tot > 0.f ? m_run * 0.6931471805599453f + logf(l_tot) : -INFINITY;
   }
@@ -351,18 +375,35 @@ template <typename T>
 int launch_f32_typed(const BsaParams& p, hipStream_t stream, const char* who) {
   const int64_t grid = (int64_t)p.batch * p.heads * p.q_blocks;
   const dim3 blocks((unsigned)grid), threads(256);
-  auto run = [&](auto kernel) { hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p); };
-  if (p.drop_thresh != 0) {
+  auto run = [&](auto kernel, int dim0) {
+    hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p, dim0);
+  };
+  if (p.head_dim > kHeadDim) {
+    // Head dims 136..256: two launches of 128 output dims each.
+    if (p.rs_logm)
+      return dsa::set_error(DSA_EUNSUPPORTED, "%s: statistics take head dims up to 128", who);
+    for (int dim0 = 0; dim0 < p.head_dim; dim0 += kHeadDim) {
+      if (p.drop_thresh != 0) {
+        if (p.row_ptr)
+          return dsa::set_error(DSA_EUNSUPPORTED, "%s: dropout takes dense attention only", who);
+        run(bsa_fwd_f32_kernel<T, kMaxHeadDim, false, false, true>, dim0);
+      } else if (p.row_ptr) {
+        run(bsa_fwd_f32_kernel<T, kMaxHeadDim, true, false, false>, dim0);
+      } else {
+        run(bsa_fwd_f32_kernel<T, kMaxHeadDim, false, false, false>, dim0);
+      }
+    }
+  } else if (p.drop_thresh != 0) {
     if (p.row_ptr || p.rs_logm)
       return dsa::set_error(DSA_EUNSUPPORTED, "%s: dropout takes dense attention only", who);
-    run(bsa_fwd_f32_kernel<T, false, false, true>);
+    run(bsa_fwd_f32_kernel<T, kHeadDim, false, false, true>, 0);
   } else if constexpr (std::is_same<T, float>::value) {
     if (p.row_ptr) {
-      if (p.rs_logm) run(bsa_fwd_f32_kernel<float, true, true, false>);
-      else run(bsa_fwd_f32_kernel<float, true, false, false>);
+      if (p.rs_logm) run(bsa_fwd_f32_kernel<float, kHeadDim, true, true, false>, 0);
+      else run(bsa_fwd_f32_kernel<float, kHeadDim, true, false, false>, 0);
     } else {
-      if (p.rs_logm) run(bsa_fwd_f32_kernel<float, false, true, false>);
-      else run(bsa_fwd_f32_kernel<float, false, false, false>);
+      if (p.rs_logm) run(bsa_fwd_f32_kernel<float, kHeadDim, false, true, false>, 0);
+      else run(bsa_fwd_f32_kernel<float, kHeadDim, false, false, false>, 0);
     }
   } else {
     return dsa::set_error(DSA_EUNSUPPORTED, "%s: 16-bit inputs run the 16-bit kernels", who);
@@ -372,8 +413,8 @@ int launch_f32_typed(const BsaParams& p, hipStream_t stream, const char* who) {
 
 }  // namespace bsa
 
-// fp32-compute launches: every call of fp32 inputs (dtype DSA_F32), and
-// dense calls with dropout of any input type.
+// fp32-compute launches: every call of fp32 inputs (dtype DSA_F32), dense
+// calls with dropout, and calls of head dims 136..256 of any input type.
 int bsa_launch_f32(bsa::BsaParams p, int32_t dtype, hipStream_t stream, const char* who) {
   if (dtype == DSA_F32) return bsa::launch_f32_typed<float>(p, stream, who);
   if (dtype == DSA_F16) return bsa::launch_f32_typed<_Float16>(p, stream, who);

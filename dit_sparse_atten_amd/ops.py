@@ -123,9 +123,10 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
     block and per key block that the route addresses: 128 for ``flex_reuse``,
     the spatial tile size for the matrix-sparse backend.
 
-    q: [B,Tq,H,D], k/v: [B,Tk,H,D], D a multiple of 8 up to 128, all bf16,
-    all fp16 or all fp32 (the compute type; fp32 runs the fp32 matrix-core
-    kernel), on a HIP device, any strides with a contiguous head dim.
+    q: [B,Tq,H,D], k/v: [B,Tk,H,D], D a multiple of 8 up to 256, all bf16,
+    all fp16 or all fp32 (the compute type; fp32, and D above 128 for every
+    type, run the fp32 matrix-core kernel), on a HIP device, any strides with
+    a contiguous head dim.
     ``causal`` (dense calls only): query t attends keys k <= t, as SDPA's
     is_causal.  ``deterministic`` (or
     ``torch.use_deterministic_algorithms(True)``): results reproducible bit

@@ -49,8 +49,10 @@ const char* dsa_last_error(void);
  * SDPA (attention_backends/dense.py:14-48).
  *   strides[12]: q (b,t,h), k (b,t,h), v (b,t,h), o (b,t,h), in elements,
  *                each a multiple of 8; pointers 16-byte aligned.
- *   head_dim: a multiple of 8 up to 128 (dims past it are zero-filled in the
- *                kernel; the matrix products run at 128).  block_size: 1..128
+ *   head_dim: a multiple of 8 up to 256 (dims past it are zero-filled in the
+ *                kernel; the matrix products run at 128).  Head dims 136..256
+ *                run the fp32-compute kernel for every dtype: S over 256
+ *                dims, O in two launches of 128 dims.  block_size: 1..128
  *                tokens per query block and per key
  *                block (128 for the flex_reuse route; the spatial tile size of
  *                the matrix-sparse backend, sparse.py:51-103, 670-751).

@@ -73,7 +73,7 @@ def test_invalid_arguments_are_reported_before_any_launch(lib):
     with pytest.raises(ValueError, match="null"):
         _lib.check(status, "dsa_bsa_fwd")
     fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
-    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 136, 128,
+    status = lib.dsa_bsa_fwd(fake, fake, fake, fake, 0, strides, 1, 128, 128, 1, 264, 128,
                              None, None, 1, 0.1, 0, 0, None, fake, 1 << 20, None)
     assert status == _lib.DSA_EUNSUPPORTED and "head_dim" in _lib.last_error()
     misaligned = ctypes.c_void_p(24)

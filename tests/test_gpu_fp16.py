@@ -166,19 +166,19 @@ def test_fp16_through_every_backend(cuda_device, name):
 
 
 @pytest.mark.parametrize("name", ["dense", "flex_reuse", "sparse"])
-def test_float32_compute_is_rejected_alike(cuda_device, name):
-    """float32 compute has no kernel: every backend raises the same
-    ValueError (dense and flex_reuse for dtype=float32, sparse for float32
+def test_float64_compute_is_rejected_alike(cuda_device, name):
+    """float64 compute has no kernel: every backend raises the same
+    ValueError (dense and flex_reuse for dtype=float64, sparse for float64
     inputs, since it computes in the input dtype)."""
     from dit_sparse_atten_amd.attention_backends import BACKENDS, context
     context.reset_runtime_state()
     try:
         backend = BACKENDS[name]()
         grid = (2, 16, 32)
-        q, k, v = (torch.randn(1, math.prod(grid), 2, 128, device=cuda_device)
-                   for _ in range(3))
+        q, k, v = (torch.randn(1, math.prod(grid), 2, 128, device=cuda_device,
+                               dtype=torch.float64) for _ in range(3))
         context.set_routing_context(attention_id=1, step=0, branch=0, grid=grid)
-        with pytest.raises(ValueError, match="bfloat16 or float16"):
-            backend(q, k, v, dtype=torch.float32)
+        with pytest.raises(ValueError, match="bfloat16, float16 or float32"):
+            backend(q, k, v, dtype=torch.float64)
     finally:
         context.reset_runtime_state()
