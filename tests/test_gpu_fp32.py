@@ -193,3 +193,23 @@ def test_fp32_through_the_dense_and_flex_backends(cuda_device):
                                          route.cpu().numpy(), 128)
     np.testing.assert_allclose(out1.double().cpu().numpy(), routed, atol=OUT_ATOL, rtol=0)
     assert not route.cpu().numpy().all()
+
+
+def test_fp32_batched_routes_and_strided_views(ops, cuda_device):
+    """Two batch items with their own routes (route_batches 2), read through
+    the transposed views of BHSD storage the Diffusers processor passes, with
+    a partial last block, against the float64 closed form."""
+    batch, heads, tokens, block = 2, 3, 700, 128
+    generator = torch.Generator().manual_seed(12)
+    bhsd = [torch.randn(batch, heads, tokens, 64, generator=generator) for _ in range(3)]
+    q, k, v = (x.to(cuda_device).transpose(1, 2) for x in bhsd)
+    assert not q.is_contiguous()
+    blocks = math.ceil(tokens / block)
+    route = np.stack([random_route(heads, blocks, seed=20 + b, keep=0.6).numpy()
+                      for b in range(batch)])
+    csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=block)
+    out, lse = ops.bsa_fwd(q, k, v, csr, return_lse=True, block_size=block)
+    torch.cuda.synchronize()
+    want, want_lse = A.block_sparse_attention(*(x.transpose(1, 2).numpy() for x in bhsd),
+                                              route, block)
+    _check(out, lse, want, want_lse)
