@@ -274,6 +274,39 @@ def test_fused_step_every_tile_size(ops, cuda_device, routed):
     assert not failures, failures
 
 
+@pytest.mark.parametrize("routed", [True, False])
+def test_fused_step_fp16_tile_sizes(ops, cuda_device, routed):
+    """The fp16 instances of every statistics variant (2 or 4 waves, one or
+    two half-tiles, the gathered stream, the dense token stream) at
+    representative tile sizes, against the oracle on the same fp16 inputs."""
+    import types
+    failures = []
+    for t in (1, 16, 33, 48, 64, 72, 81, 96, 100, 121, 128):
+        tiles = 5
+        q, k, v = clustered_qkv(tiles * t, 2, 128, group=t, seed=t, dtype=torch.float16)
+        case = types.SimpleNamespace(tile=t, tile_shape=(1, t))
+        qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+        route = None
+        csr = None
+        if routed:
+            route = random_route(2, tiles, seed=t, keep=0.6).numpy()
+            route[..., tiles - 1] = True
+            csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=t)
+        out, _, got = ops.bsa_fwd_tile_stats(qd, kd, vd, csr, (1, t), deterministic=True)
+        torch.cuda.synchronize()
+        assert out.dtype == torch.float16
+        expected, expected_out = _oracle_stats(case, q, k, v, route)
+        try:
+            # fp16 probabilities: 2^-11 per term.
+            _compare_stats(got, expected, rtol=2e-3)
+            metrics = A.summarize(out.float().cpu().numpy(), expected_out)
+            assert metrics["max_absolute_error"] <= 2e-2, metrics
+            assert metrics["cosine_similarity"] >= 0.9995, metrics
+        except AssertionError as error:
+            failures.append((t, str(error)[:200]))
+    assert not failures, failures
+
+
 def test_fused_step_at_720p_tile_shape(ops, cuda_device):
     """The bench's 720p matrix-sparse step shape (9 x 8 tiles, 800 tiles
     per head) at 4 heads: fused statistics against the two-pass statistics on
