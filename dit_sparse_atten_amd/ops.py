@@ -204,9 +204,11 @@ def bsa_fwd(q, k, v, csr=None, scale=None, out=None, return_lse=False, block_siz
         raise ValueError(f"block_size {block_size} unsupported (1..128)")
     deterministic = bool(deterministic) or torch.are_deterministic_algorithms_enabled()
     # Room for the split partials of the last round of workgroups (none when
-    # the key range is too short to split; the fp32 kernel takes none); the
-    # caching allocator recycles it.
-    workspace_bytes = 0 if q.dtype == torch.float32 else lib.dsa_bsa_workspace_bytes_block(
+    # the key range is too short to split; the fp32-compute kernel, which
+    # also takes head dims above 128, uses none); the caching allocator
+    # recycles it.
+    fp32_kernel = q.dtype == torch.float32 or head_dim > HEAD_DIM
+    workspace_bytes = 0 if fp32_kernel else lib.dsa_bsa_workspace_bytes_block(
         batch, heads, kv_tokens, head_dim, block_size)
     workspace = (torch.empty(workspace_bytes, dtype=torch.uint8, device=q.device)
                  if workspace_bytes else None)
