@@ -176,7 +176,8 @@ struct ReduceParams {
   __half* ckx;
   int32_t tokens, tiles, tile, tile_h, tile_w;
   int32_t dense;  // 1: every key tile, rows at (h * tiles + kt) * tokens + token
-  int32_t raw;    // 1: mass32 holds the plain sum (the exact block mass), not sum / tokens
+  int32_t raw;    // 1: mass32 holds the plain sum (the exact block mass), not sum / tokens,
+                  // and rs_mean is absent
 };
 
 __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) {
@@ -229,7 +230,7 @@ __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) 
 #pragma unroll
       for (int u = 0; u < kCells; ++u) {
         lg[u] = ok[u] ? p.rs_logm[at0[u] + r] : -INFINITY;
-        mn[u] = ok[u] ? p.rs_mean[at0[u] + r] : 0u;
+        mn[u] = ok[u] && !p.raw ? p.rs_mean[at0[u] + r] : 0u;
       }
 #pragma unroll
       for (int u = 0; u < kCells; ++u) {
@@ -269,6 +270,11 @@ __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) 
 // query rows (fp32 log-mass and two fp16 means each), rounded up to 256.
 size_t row_stats_bytes(int64_t entries, int32_t tile) {
   return ((size_t)entries * tile * 2 * sizeof(float) + 255) & ~(size_t)255;
+}
+
+// The same with the log-masses only (the exact block mass).
+size_t row_mass_bytes(int64_t entries, int32_t tile) {
+  return ((size_t)entries * tile * sizeof(float) + 255) & ~(size_t)255;
 }
 
 // Dense statistics calls of 64..128-token tiles that are a multiple of 8 run
@@ -469,7 +475,7 @@ extern "C" size_t dsa_bsa_fwd_block_mass_workspace_bytes(int32_t heads, int32_t 
   const size_t attention = dsa_bsa_workspace_bytes_block(1, heads, tokens, head_dim, 128);
   if (tokens % 128 != 0) return attention;
   const int64_t blocks = tokens / 128;
-  return attention + row_stats_bytes((int64_t)heads * blocks * blocks, 128);
+  return attention + row_mass_bytes((int64_t)heads * blocks * blocks, 128);
 }
 
 extern "C" int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* v, void* o,
@@ -510,9 +516,9 @@ extern "C" int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* 
   }
   const int32_t blocks = tokens / 128;
   const int64_t entries = (int64_t)heads * blocks * blocks;
-  const size_t rs = row_stats_bytes(entries, 128);
+  const size_t rs = row_mass_bytes(entries, 128);
   p.rs_logm = reinterpret_cast<float*>(base);
-  p.rs_mean = reinterpret_cast<uint32_t*>(base + (size_t)entries * 128 * sizeof(float));
+  p.rs_mean = nullptr;  // the mean key offsets are not needed
   p.rs_entries = entries;
   p.tile_h = 1;
   p.tile_w = 128;

@@ -314,10 +314,13 @@ __global__ void __launch_bounds__(256, kD == 128 ? 2 : 1) bsa_fwd_f32_kernel(Bsa
         at = ((int64_t)h * p.kv_blocks + kb) * p.q_tokens + tq;
       }
       if (ok) {
-        const float inv = tm > 0.f ? 1.f / tm : 0.f;
-        const dsa_f16x2 mean = __builtin_convertvector(dsa_f32x2{ty * inv, tx * inv}, dsa_f16x2);
         p.rs_logm[at] = tm > 0.f ? log2f(tm) + m_run : -INFINITY;
-        p.rs_mean[at] = __builtin_bit_cast(uint32_t, mean);
+        if (p.rs_mean != nullptr) {
+          const float inv = tm > 0.f ? 1.f / tm : 0.f;
+          const dsa_f16x2 mean =
+              __builtin_convertvector(dsa_f32x2{ty * inv, tx * inv}, dsa_f16x2);
+          p.rs_mean[at] = __builtin_bit_cast(uint32_t, mean);
+        }
       }
     }
     cm = cy = cx = 0.f;

@@ -89,7 +89,8 @@ struct BsaParams {
   // Fused tile statistics (the kStats instances), per query row and key tile
   // of stat_tile = tile_h * tile_w tokens: rs_logm = log2 of the row's
   // unnormalised probability mass on the key tile, sum 2^(scale_log2 s), and
-  // rs_mean = its mass-weighted mean key offsets (y, x) as two fp16.  Routed:
+  // rs_mean = its mass-weighted mean key offsets (y, x) as two fp16 (null:
+  // not written, the exact block mass needs only the mass).  Routed:
   // at e * block + r for CSR entry e and query row r of the tile, entries at
   // or past rs_entries not written.  Dense: at (h * tiles + key tile) *
   // q_tokens + query token.
@@ -691,11 +692,13 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     if (g == par) {
       if (ok) {
         const float mass = carry[0];
-        const float inv = mass > 0.f ? 1.f / mass : 0.f;
-        const dsa_f32x2 mean = {(carry[1] + carry[3]) * inv, (carry[2] + carry[4]) * inv};
-        const dsa_f16x2 hm = __builtin_convertvector(mean, dsa_f16x2);
         p.rs_logm[at] = mass > 0.f ? __log2f(mass) + m_run : -INFINITY;
-        p.rs_mean[at] = __builtin_bit_cast(uint32_t, hm);
+        if (p.rs_mean != nullptr) {
+          const float inv = mass > 0.f ? 1.f / mass : 0.f;
+          const dsa_f32x2 mean = {(carry[1] + carry[3]) * inv, (carry[2] + carry[4]) * inv};
+          const dsa_f16x2 hm = __builtin_convertvector(mean, dsa_f16x2);
+          p.rs_mean[at] = __builtin_bit_cast(uint32_t, hm);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 5; ++i) carry[i] = 0.f;

@@ -279,8 +279,8 @@ size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t tokens, int
  * per query row and key block, then a short second launch); otherwise the
  * call runs the attention and then dsa_block_mass.
  *   workspace: dsa_bsa_fwd_block_mass_workspace_bytes(...) bytes, 16-byte
- *            aligned: heads * blocks^2 * 128 * 8 bytes of per-row sums when
- *            fused (rounded up to 256), then dsa_bsa_fwd's workspace.
+ *            aligned: heads * blocks^2 * 128 * 4 bytes of per-row log-masses
+ *            when fused (rounded up to 256), then dsa_bsa_fwd's workspace.
  */
 int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* v, void* o, int32_t dtype,
                            const int64_t* strides, int32_t tokens, int32_t heads,
