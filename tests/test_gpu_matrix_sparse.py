@@ -307,6 +307,60 @@ def test_fused_step_fp16_tile_sizes(ops, cuda_device, routed):
     assert not failures, failures
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_reference_statistics_case(ops, cuda_device, fused):
+    """The reference's own statistics known-answer case
+    (tests/test_sparse_triton_stats.py:15-50): 3,600 tokens on a 1 x 60 x 60
+    grid (6 x 10 tiles of 60 tokens, 60 tiles), 4 heads, head dim 128, unit
+    normal bf16 Q/K/V, route ``rand < 0.625`` plus the diagonal, the query
+    chunk 0..240 through the oracle's sparse_chunk and the reference's
+    tolerances: output atol 2e-3 / rtol 2e-2, raw mass atol 2e-3 / rtol 2e-3,
+    centroids atol 2e-3 / rtol 2e-2. The whole sequence is also checked
+    against the oracle at the same tolerances."""
+    torch.manual_seed(0)
+    tokens, heads, head_dim, grid = 3600, 4, 128, (1, 60, 60)
+    q = torch.randn(1, tokens, heads, head_dim).to(torch.bfloat16)
+    k = torch.randn_like(q)
+    v = torch.randn_like(q)
+    tile_shape = S.sparse_tile_shape(grid, 64, tokens)
+    tile = tile_shape[0] * tile_shape[1]
+    tiles = tokens // tile
+    assert (tile_shape, tiles) == ((6, 10), 60)
+    route = torch.rand(heads, tiles, tiles) < 0.625
+    route[:, torch.arange(tiles), torch.arange(tiles)] = True
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    csr = ops.route_to_csr(route.to(cuda_device), block_size=tile)
+    if fused:
+        out, _, got = ops.bsa_fwd_tile_stats(qd, kd, vd, csr, tile_shape)
+    else:
+        out, lse = ops.bsa_fwd(qd, kd, vd, csr, return_lse=True, block_size=tile)
+        got = ops.tile_stats(qd, kd, lse, tile_shape, csr=csr)
+    torch.cuda.synchronize()
+    out = out.float().cpu().numpy()
+    raw_mass = got["mass"].cpu().numpy() * np.float32(tokens)
+    centroids = {n: got[f"centroid_{n}"].float().cpu().numpy() for n in ("q_y", "q_x", "k_y", "k_x")}
+
+    qf, kf, vf = (x.float().numpy() for x in (q, k, v))
+    route_np = route.numpy()
+    offsets = S.spatial_offsets(tile_shape, tiles)
+    scale = head_dim ** -0.5
+    for stop in (240, tokens):
+        stats = S.empty_stats(heads, tiles)
+        expected = np.concatenate([
+            S.sparse_chunk(qf, kf, vf, route_np, tile, start, min(start + 240, stop), scale,
+                           stats, offsets)
+            for start in range(0, stop, 240)], axis=1)
+        rows = stop // tile
+        np.testing.assert_allclose(out[:, :stop], expected, atol=2e-3, rtol=2e-2)
+        np.testing.assert_allclose(raw_mass[:, :rows], stats["mass"][:, :rows], atol=2e-3,
+                                   rtol=2e-3)
+        den = np.maximum(stats["mass"], np.float32(1e-12))
+        for name, value in centroids.items():
+            np.testing.assert_allclose(value[:, :rows], (stats[name] / den)[:, :rows],
+                                       atol=2e-3, rtol=2e-2, err_msg=name)
+    assert (raw_mass[~route_np] == 0).all()
+
+
 def test_fused_step_at_720p_tile_shape(ops, cuda_device):
     """The bench's 720p matrix-sparse step shape (9 x 8 tiles, 800 tiles
     per head) at 4 heads: fused statistics against the two-pass statistics on
