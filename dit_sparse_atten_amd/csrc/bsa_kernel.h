@@ -438,6 +438,21 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     for (int dt = 0; dt < 4; ++dt)
       vfrag[dt] = row * kRowBytes + v_swz(row, 4 * dt + sub) * 16 + (c & 1) * 8;
   }
+  // K fragment of chunk dc (row kt 32 + qi): the chunk index 2 dc + g XOR
+  // (qi & 15) times 16 is (dc << 5) ^ ((g ^ (qi & 15)) << 4), and the row's
+  // 256 bytes leave the low 8 address bits to it, so every offset is
+  // kt 8192 + (kfrag ^ (dc << 5)); likewise vfrag[dt] = vfrag[0] ^ (dt << 6).
+  // kLeanAddr instances rebuild the offsets from these two registers each
+  // step (an empty asm keeps the compiler from hoisting them back out): the
+  // 4-wave statistics instances, which otherwise spill the eight K offsets to
+  // scratch and reload them inside the QK chain (720p 9 x 8 tiles 85.2 ->
+  // 84.0 ms).  kDeferSums: the plain-stream 4-wave statistics instances add
+  // a chunk's key-side sums in the next chunk's softmax (see wprev): dense
+  // 9 x 8 tiles 81.6 -> 80.1 ms, routed 9 x 10 75.2 -> 73.5 ms.  Same-box A/B;
+  // the gathered stream and the 2-wave instances ran 0-5% slower with it.
+  constexpr bool kLeanAddr = kStats && kNh == 2;
+  constexpr bool kDeferSums = kStats && kNh == 2 && !kGather;
+  const int kfrag = qi * kRowBytes + ((g ^ (qi & 15)) << 4);
 
   auto block_of = [&](int j) -> int {
     const int kb = kRouted ? cidx[walked(j)] : start + j;
@@ -497,7 +512,15 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // 12-15, so the eight keys a lane half supplies (P^T slot order) are one
   // 16-byte read.
   const T* wrow = wtab;
+  // carry: the lane's five sums of its parity's open tile, up to the chunk
+  // before the current one; wprev: the last chunk's sums, which its MFMAs
+  // leave for the next chunk's softmax to add (reading them in the same step
+  // would hold the wave until the whole PV chain has drained).  A tile that
+  // ends in a chunk is therefore closed one step later (pend_par, pend_idx),
+  // or after the walk.
   float carry[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  float wprev[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  int pend_par = -1, pend_idx = 0;
   if constexpr (kStats) {
     const int bp = p.stat_pad;
     for (int i = tid; i < kStatRows * kStatCols; i += kWaves * 64) {
@@ -545,13 +568,17 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.f;
+    [[maybe_unused]] int kf = kfrag, vf = vfrag[0];
+    if constexpr (kLeanAddr) asm volatile("" : "+v"(kf), "+v"(vf));
 #pragma unroll
     for (int dc = 0; dc < 8; ++dc) {
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt) {
         const int row = kt * 32 + qi;
-        const x8 a = *reinterpret_cast<const x8*>(
-            kt_lds + row * kRowBytes + k2_swz(row, dc * 2 + g) * 16);
+        const unsigned char* at =
+            kLeanAddr ? kt_lds + kt * 32 * kRowBytes + (kf ^ (dc << 5))
+                      : kt_lds + row * kRowBytes + k2_swz(row, dc * 2 + g) * 16;
+        const x8 a = *reinterpret_cast<const x8*>(at);
         sacc[kt] = E::mfma32(a, qf[dc], sacc[kt]);
       }
     }
@@ -567,6 +594,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     }
     if constexpr (kPrioSoftmax) __builtin_amdgcn_s_setprio(1);
+    if constexpr (kStats && kDeferSums) {
+#pragma unroll
+      for (int i = 0; i < 5; ++i) carry[i] += wprev[i];
+    }
     if constexpr (kGather) {
       if (invalid != 0) {
         const uint64_t mine = invalid >> (4 * g);
@@ -652,7 +683,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         // Key rows 16 j + 4 g + r (slots 0..3) and 16 j + 8 + 4 g + r (4..7).
-        const unsigned char* at = v_lds + vfrag[dt] + j * 16 * kRowBytes;
+        const unsigned char* at =
+            v_lds + (kLeanAddr ? vf ^ (dt << 6) : vfrag[dt]) + j * 16 * kRowBytes;
         const typename E::x4 lo = lds_read_tr<T>(at);
         const typename E::x4 hi = lds_read_tr<T>(at + 8 * kRowBytes);
         const x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -681,7 +713,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         wacc = E::mfma32(a, pf[j], wacc);
       }
 #pragma unroll
-      for (int i = 0; i < 5; ++i) carry[i] += wacc[i];
+      for (int i = 0; i < 5; ++i) {
+        if constexpr (kDeferSums) wprev[i] = wacc[i];
+        else carry[i] += wacc[i];
+      }
     }
   };
 
@@ -703,6 +738,22 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
 #pragma unroll
       for (int i = 0; i < 5; ++i) carry[i] = 0.f;
     }
+  };
+  // The pending close, once the sums of the chunk it ended in are in carry:
+  // pend_idx is the walk index j (routed), the key block (dense tile blocks)
+  // or the tile index (dense token stream).  Chunks of 64 keys end at most
+  // one tile each (tiles hold 64 or more stream slots).
+  auto close_pending = [&]() __attribute__((always_inline)) {
+    if (pend_par < 0) return;
+    if constexpr (kRouted) {
+      const int64_t e = walked(pend_idx);
+      close_tile(pend_par, e * p.block + local_row, row_ok && e < p.rs_entries);
+    } else {
+      const bool tokens = kTokenStream && p.stat_tile != p.block;
+      const int64_t per_head = tokens ? p.kv_tokens / p.stat_tile : p.kv_blocks;
+      close_tile(pend_par, ((int64_t)h * per_head + pend_idx) * p.q_tokens + tq, row_ok);
+    }
+    pend_par = -1;
   };
   // One pipelined step: wait for the current stage, prefetch the next
   // half-tile (next_kb == -2: none), then compute on the current one
@@ -733,24 +784,22 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       else
         compute(kc, vc, valid, lim, 0ull, wbase, std::integral_constant<int, 2>{});
       if constexpr (kStats) {
+        if constexpr (kDeferSums) close_pending();
         if (tile_blocks) {
           // Block kb is tile j of the walk: it ends with its last half-tile.
           if (half == kNh - 1) {
-            if constexpr (kRouted) {
-              const int64_t e = walked(j);
-              close_tile(j & 1, e * p.block + local_row, row_ok && e < p.rs_entries);
-            } else {
-              close_tile(j & 1, ((int64_t)h * p.kv_blocks + kb) * p.q_tokens + tq, row_ok);
-            }
+            pend_par = j & 1;
+            pend_idx = kRouted ? j : kb;
           }
         } else {
           // The tile ending in (pos, pos + 64] (the sequence end included), if any.
           const int m = min(pos + kHalfKeys, p.kv_tokens) / p.stat_tile;
-          if (m >= 1 && m * p.stat_tile > pos)
-            close_tile((m - 1) & 1,
-                       ((int64_t)h * (p.kv_tokens / p.stat_tile) + (m - 1)) * p.q_tokens + tq,
-                       row_ok);
+          if (m >= 1 && m * p.stat_tile > pos) {
+            pend_par = (m - 1) & 1;
+            pend_idx = m - 1;
+          }
         }
+        if constexpr (!kDeferSums) close_pending();
       }
     }
   };
@@ -791,7 +840,12 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         compute(kc, vc, 0, kHalfKeys, invalid, wbase, std::integral_constant<int, 2>{});
       // Block j0 ends in this chunk (the row's last block closes after the walk).
       if constexpr (kStats) {
-        if (second <= 64 && j0 + 1 < nblk) close_stream_tile(j0);
+        if constexpr (kDeferSums) close_pending();
+        if (second <= 64 && j0 + 1 < nblk) {
+          pend_par = j0 & 1;
+          pend_idx = j0;
+        }
+        if constexpr (!kDeferSums) close_pending();
       }
     }
   };
@@ -831,9 +885,6 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       j0 = j2; o0 = o2; kb0 = kb0m; kb1 = kb1m;
       w0 = next_w(w1);
     }
-    if constexpr (kStats) {
-      if (wave_active) close_stream_tile(nblk - 1);
-    }
   } else if (!kGather && nblk > 0) {
     int kb = block_of(0);
     issue(kb, 0, lds_k0, lds_v0);
@@ -855,6 +906,18 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         step(kb1, 0, kb2, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip, j + 1);
         kb = kb2;
       }
+    }
+  }
+  if constexpr (kStats) {
+    // The last chunk's sums, the pending close, and the gathered stream's
+    // last tile (closed after the walk).
+    if (wave_active && nblk > 0) {
+      if constexpr (kDeferSums) {
+#pragma unroll
+        for (int i = 0; i < 5; ++i) carry[i] += wprev[i];
+      }
+      close_pending();
+      if constexpr (kGather) close_stream_tile(nblk - 1);
     }
   }
 
