@@ -779,7 +779,13 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       int wbase = 0;
       if constexpr (kStats)
         wbase = tile_blocks ? (j & 1) * p.stat_pad + half * kHalfKeys : pos % (2 * p.stat_pad);
-      if (decltype(skip_c)::value && valid <= 32)
+      // A skip step holds at most 32 valid keys: the kSkip instances run
+      // blocks whose last half-tile has 1..32 keys (65..96-key blocks, or
+      // blocks of at most 32), and only that half-tile is a skip step.  One
+      // compute instance per call site keeps the O accumulators in place
+      // (two, chosen at run time, made the register allocator copy them
+      // on every step).
+      if constexpr (decltype(skip_c)::value)
         compute(kc, vc, valid, lim, 0ull, wbase, std::integral_constant<int, 1>{});
       else
         compute(kc, vc, valid, lim, 0ull, wbase, std::integral_constant<int, 2>{});
@@ -834,10 +840,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       }
       if (kb0 < 0) invalid |= second >= 64 ? ~0ull : (1ull << second) - 1;
       if (kb1 < 0 && second < 64) invalid |= ~0ull << second;
-      if (left <= 32)
-        compute(kc, vc, 0, kHalfKeys, invalid, wbase, std::integral_constant<int, 1>{});
-      else
-        compute(kc, vc, 0, kHalfKeys, invalid, wbase, std::integral_constant<int, 2>{});
+      // One compute instance only: a second, 32-key one (for a row's last
+      // chunk) made the register allocator copy the O accumulators on every
+      // step; the masked slots of that rare chunk cost less.
+      compute(kc, vc, 0, kHalfKeys, invalid, wbase, std::integral_constant<int, 2>{});
       // Block j0 ends in this chunk (the row's last block closes after the walk).
       if constexpr (kStats) {
         if constexpr (kDeferSums) close_pending();
