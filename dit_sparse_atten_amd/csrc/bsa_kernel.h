@@ -480,22 +480,38 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       kbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.k_st * 2 + p.head_dim * 2));
   const __amdgpu_buffer_rsrc_t v_all_rsrc = make_rsrc(
       vbase, (uint32_t)((int64_t)(p.kv_tokens - 1) * p.v_st * 2 + p.head_dim * 2));
-  auto issue_gather = [&](int kb0, int kb1, int o0, unsigned char* kdst, unsigned char* vdst)
-      __attribute__((always_inline)) {
+  // Lane (wave, lane) stages the 16-byte chunk (lane & 15) of the chunk's
+  // stream rows g_r0 + 4 j, j = 0..3.  Row r holds token base0 + r while
+  // o0 + r < block_pad (block kb0) and base1 + r after (block kb1), with
+  // base0 = kb0 block + o0 and base1 = kb1 block + o0 - block_pad, so its
+  // byte offset is a per-lane constant (gk / gv: row stride plus chunk, with
+  // the dead-dims bit added, as no valid offset on this path reaches 2^31)
+  // plus base0 or base1 times the stride, uniform per block.
+  const int g_r0 = wave * 16 + (lane >> 4);
+  uint32_t gk[4] = {0u, 0u, 0u, 0u}, gv[4] = {0u, 0u, 0u, 0u};
+  if constexpr (kGather) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int row = (wave * 4 + j) * 4 + (lane >> 4);  // stream position o0 + row
-      const int o = o0 + row;
-      const bool first = o < p.block_pad;
-      const uint32_t token =
-          (uint32_t)((first ? kb0 : kb1) * p.block + (first ? o : o - p.block_pad));
+      const int row = g_r0 + 4 * j;
       const int kc = k2_swz(row, lane & 15), vc = v_swz(row, lane & 15);
-      lds_load16(k_all_rsrc, kdst + (wave * 4 + j) * 1024,
-                 (token * (uint32_t)(p.k_st * 2) + (uint32_t)(kc * 16)) |
-                     dsa::dead_bits(kc, p.head_dim), 0);
-      lds_load16(v_all_rsrc, vdst + (wave * 4 + j) * 1024,
-                 (token * (uint32_t)(p.v_st * 2) + (uint32_t)(vc * 16)) |
-                     dsa::dead_bits(vc, p.head_dim), 0);
+      gk[j] = (uint32_t)row * (uint32_t)(p.k_st * 2) + (uint32_t)(kc * 16) +
+              dsa::dead_bits(kc, p.head_dim);
+      gv[j] = (uint32_t)row * (uint32_t)(p.v_st * 2) + (uint32_t)(vc * 16) +
+              dsa::dead_bits(vc, p.head_dim);
+    }
+  }
+  auto issue_gather = [&](int kb0, int kb1, int o0, unsigned char* kdst, unsigned char* vdst)
+      __attribute__((always_inline)) {
+    const int base0 = kb0 * p.block + o0, base1 = kb1 * p.block + o0 - p.block_pad;
+    const uint32_t ks = (uint32_t)(p.k_st * 2), vs = (uint32_t)(p.v_st * 2);
+    const uint32_t k0 = (uint32_t)base0 * ks, kd = (uint32_t)(base1 - base0) * ks;
+    const uint32_t v0 = (uint32_t)base0 * vs, vd = (uint32_t)(base1 - base0) * vs;
+    const int first_end = p.block_pad - o0;  // rows below it are in block kb0
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool first = g_r0 + 4 * j < first_end;
+      lds_load16(k_all_rsrc, kdst + (wave * 4 + j) * 1024, gk[j] + k0 + (first ? 0u : kd), 0);
+      lds_load16(v_all_rsrc, vdst + (wave * 4 + j) * 1024, gv[j] + v0 + (first ? 0u : vd), 0);
     }
   };
   // Valid keys of half-tile `half` of block kb (0 for an invalid block).
