@@ -739,16 +739,24 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // Fused statistics: a tile of parity par has ended; the lanes of that parity
   // write their query row's entry at `at` (when `ok`) and start the next tile
   // of that parity from zero.
+  // The lane's part of an entry's index (its query row: local_row for
+  // routed entries e * block + local_row, tq for dense ones) is folded into
+  // per-lane pointers once; a close adds the uniform part `at`.
+  float* const logm_lane = kStats ? p.rs_logm + (kRouted ? local_row : tq) : nullptr;
+  uint32_t* const mean_lane =
+      kStats && p.rs_mean != nullptr ? p.rs_mean + (kRouted ? local_row : tq) : nullptr;
   auto close_tile = [&](int par, int64_t at, bool ok) __attribute__((always_inline)) {
     if (g == par) {
       if (ok) {
         const float mass = carry[0];
-        p.rs_logm[at] = mass > 0.f ? __log2f(mass) + m_run : -INFINITY;
-        if (p.rs_mean != nullptr) {
-          const float inv = mass > 0.f ? 1.f / mass : 0.f;
+        logm_lane[at] = mass > 0.f ? __log2f(mass) + m_run : -INFINITY;
+        if (mean_lane != nullptr) {
+          // The means are stored in fp16: the hardware reciprocal (1 ulp in
+          // fp32) is exact enough.
+          const float inv = mass > 0.f ? __builtin_amdgcn_rcpf(mass) : 0.f;
           const dsa_f32x2 mean = {(carry[1] + carry[3]) * inv, (carry[2] + carry[4]) * inv};
           const dsa_f16x2 hm = __builtin_convertvector(mean, dsa_f16x2);
-          p.rs_mean[at] = __builtin_bit_cast(uint32_t, hm);
+          mean_lane[at] = __builtin_bit_cast(uint32_t, hm);
         }
       }
 #pragma unroll
@@ -763,11 +771,11 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     if (pend_par < 0) return;
     if constexpr (kRouted) {
       const int64_t e = walked(pend_idx);
-      close_tile(pend_par, e * p.block + local_row, row_ok && e < p.rs_entries);
+      close_tile(pend_par, e * p.block, row_ok && e < p.rs_entries);
     } else {
       const bool tokens = kTokenStream && p.stat_tile != p.block;
       const int64_t per_head = tokens ? p.kv_tokens / p.stat_tile : p.kv_blocks;
-      close_tile(pend_par, ((int64_t)h * per_head + pend_idx) * p.q_tokens + tq, row_ok);
+      close_tile(pend_par, ((int64_t)h * per_head + pend_idx) * p.q_tokens, row_ok);
     }
     pend_par = -1;
   };
@@ -832,7 +840,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // Gathered stream: stream tile j closes into its CSR entry.
   auto close_stream_tile = [&](int j) __attribute__((always_inline)) {
     const int64_t e = walked(j);
-    close_tile(j & 1, e * p.block + local_row, row_ok && e < p.rs_entries);
+    close_tile(j & 1, e * p.block, row_ok && e < p.rs_entries);
   };
   auto step_gather = [&](int kb0, int kb1, int o0, int left, int next_kb0, int next_kb1,
                          int next_o0, const unsigned char* kc, const unsigned char* vc,
