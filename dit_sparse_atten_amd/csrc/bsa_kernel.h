@@ -256,8 +256,13 @@ __device__ __forceinline__ int walk_start(const uint64_t* tab, int lane, int bh,
 constexpr int kStatRows = 11;    // 2 parities x 5 kinds, then a zero row
 constexpr int kStatCols = 392;   // >= 2 * 120 + 64 positions; = 8 mod 128 spreads the rows' banks
 
+//
+// kMassOnly (with kStats, tile blocks, no rs_mean: the exact block mass):
+// a tile is a key block, so its mass is the part of the row sum its own
+// half-tiles add; each lane keeps its half of that sum and the close adds
+// the two halves.  No weight table, no key-side MFMAs.
 template <typename T, bool kRouted, int kNh, bool kSkip, bool kGather = false, int kWaves = 4,
-          bool kStats = false>
+          bool kStats = false, bool kMassOnly = false>
 __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     bsa_fwd_kernel(BsaParams p) {
   typedef dsa::Elem<T> E;
@@ -286,7 +291,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v1[kKStage];
-  __shared__ __attribute__((aligned(16))) T wtab[kStats ? kStatRows * kStatCols : 8];
+  static_assert(!kMassOnly || (kStats && !kGather), "mass-only statistics are tile blocks");
+  __shared__ __attribute__((aligned(16))) T wtab[kStats && !kMassOnly ? kStatRows * kStatCols : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -451,7 +457,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // 9 x 8 tiles 81.6 -> 80.1 ms, routed 9 x 10 75.2 -> 73.5 ms.  Same-box A/B;
   // the gathered stream and the 2-wave instances ran 0-5% slower with it.
   constexpr bool kLeanAddr = kStats && kNh == 2;
-  constexpr bool kDeferSums = kStats && kNh == 2 && !kGather;
+  constexpr bool kDeferSums = kStats && kNh == 2 && !kGather && !kMassOnly;
   const int kfrag = qi * kRowBytes + ((g ^ (qi & 15)) << 4);
 
   auto block_of = [&](int j) -> int {
@@ -537,7 +543,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   float carry[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
   float wprev[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
   int pend_par = -1, pend_idx = 0;
-  if constexpr (kStats) {
+  if constexpr (kStats && !kMassOnly) {
     const int bp = p.stat_pad;
     for (int i = tid; i < kStatRows * kStatCols; i += kWaves * 64) {
       const int r = i / kStatCols, si = i % kStatCols;
@@ -692,6 +698,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       }
     }
     l_run += sum0 + sum1;
+    if constexpr (kMassOnly) carry[0] += sum0 + sum1;
     if constexpr (kPrioSoftmax) __builtin_amdgcn_s_setprio(0);
     if constexpr (kPrioPv) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -718,7 +725,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     }
-    if constexpr (kStats) {
+    if constexpr (kStats && !kMassOnly) {
       // The key-side sums of this chunk (weights from stream position wbase).
       dsa_f32x16 wacc;
 #pragma unroll
@@ -746,6 +753,14 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   uint32_t* const mean_lane =
       kStats && p.rs_mean != nullptr ? p.rs_mean + (kRouted ? local_row : tq) : nullptr;
   auto close_tile = [&](int par, int64_t at, bool ok) __attribute__((always_inline)) {
+    if constexpr (kMassOnly) {
+      // Both lane halves hold part of the tile's mass (their keys of each
+      // half-tile): the sum of the two, written by one half.
+      const float mass = dsa::pair32_sum(carry[0]);
+      if (g == par && ok) logm_lane[at] = mass > 0.f ? __log2f(mass) + m_run : -INFINITY;
+      carry[0] = 0.f;
+      return;
+    }
     if (g == par) {
       if (ok) {
         const float mass = carry[0];
@@ -1325,7 +1340,9 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
   } else if (p.rs_logm) {
     // Dense statistics: 128-token blocks (the token stream, or tiles of 128),
     // or blocks of one tile each, in 2-wave workgroups up to 64 tokens.
-    if (nh == 2)
+    if (nh == 2 && !skip && p.rs_mean == nullptr && p.stat_tile == p.block)
+      four(bsa_fwd_kernel<T, false, 2, false, false, 4, true, true>);
+    else if (nh == 2)
       skip ? four(bsa_fwd_kernel<T, false, 2, true, false, 4, true>)
            : four(bsa_fwd_kernel<T, false, 2, false, false, 4, true>);
     else skip ? two(bsa_fwd_kernel<T, false, 1, true, false, 2, true>)
