@@ -272,20 +272,18 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // statistics instance has one tile per key block.
   constexpr bool kTokenStream = kStats && !kRouted && kNh == 2 && !kSkip;
   // The key-norm bound (compute), except in the plain-stream instances that
-  // skip empty sub-tiles (65..96-key blocks): there the extra live value made
-  // the register allocator copy the O accumulators around the rescale branch
-  // on every step.  (The gathered stream lost the same way until the wave
-  // priority below freed its registers: 720p 67.4 -> 66.0 ms with it now.)
+  // skip empty sub-tiles (65..96-key blocks, blocks of at most 32): there it
+  // ran slower (same-box A/B: 9 x 10 tiles 66.9 -> 70.9 ms, 3 x 8 tiles
+  // 382 -> 411 ms).
   constexpr bool kNormBound = kGather || !kSkip;
   // Wave priority (s_setprio) over one phase of each step, so that the two
   // waves sharing a SIMD fall into opposite phases and one's VALU work runs
   // beside the other's MFMAs: the gathered stream raises it for the softmax,
   // the dense 128-token kernel for the PV products.  Same-box A/B, kernel
-  // time: 720p tiles 70.2 -> 68.9 ms, with fused statistics 87.9 -> 83.5 ms,
-  // dense config-2 shape 56.5 -> 55.2 ms.  The routed 128-token kernel and
-  // the dense kernel with fused statistics ran slower with either placement
-  // and set none.
-  constexpr bool kPrioSoftmax = kGather;
+  // time: 720p tiles 58.6 -> 58.2 ms, dense config-2 shape 56.5 -> 55.2 ms.
+  // The routed 128-token kernel and the statistics instances (720p tiles
+  // with statistics 74.4 -> 75.2 ms with it) ran slower and set none.
+  constexpr bool kPrioSoftmax = kGather && !kStats;
   constexpr bool kPrioPv = !kRouted && !kStats && !kSkip && kNh == 2;
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
