@@ -263,7 +263,7 @@ constexpr int kStatCols = 392;   // >= 2 * 120 + 64 positions; = 8 mod 128 sprea
 // the two halves.  No weight table, no key-side MFMAs.
 template <typename T, bool kRouted, int kNh, bool kSkip, bool kGather = false, int kWaves = 4,
           bool kStats = false, bool kMassOnly = false>
-__global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
+__global__ void __launch_bounds__(kWaves * 64, 2)
     bsa_fwd_kernel(BsaParams p) {
   typedef dsa::Elem<T> E;
   typedef typename E::x8 x8;
@@ -285,12 +285,22 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   // with statistics 74.4 -> 75.2 ms with it) ran slower and set none.
   constexpr bool kPrioSoftmax = kGather && !kStats;
   constexpr bool kPrioPv = !kRouted && !kStats && !kSkip && kNh == 2;
+  // 2-wave workgroups (blocks of at most 64 keys) stage one block at a time:
+  // 32 KB of LDS lets four of them share a CU (two waves per SIMD) where the
+  // double-buffered 64 KB allowed two; the next block's loads start after
+  // every wave has finished with the current one, and the other workgroups
+  // of the CU cover their latency.
+  constexpr bool kSingleStage = kWaves == 2;
+  static_assert(!kSingleStage || kNh == 1, "2-wave workgroups take blocks of at most 64 keys");
   __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kSingleStage ? 16 : kKStage];
   __shared__ __attribute__((aligned(1024))) unsigned char lds_v0[kKStage];
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_v1[kKStage];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_v1[kSingleStage ? 16 : kKStage];
   static_assert(!kMassOnly || (kStats && !kGather), "mass-only statistics are tile blocks");
-  __shared__ __attribute__((aligned(16))) T wtab[kStats && !kMassOnly ? kStatRows * kStatCols : 8];
+  // Blocks of at most 64 keys read table positions below 2 * 64 only, and a
+  // narrower table keeps four 2-wave workgroups within a CU's LDS.
+  constexpr int kCols = kNh == 1 ? 136 : kStatCols;
+  __shared__ __attribute__((aligned(16))) T wtab[kStats && !kMassOnly ? kStatRows * kCols : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -543,8 +553,8 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
   int pend_par = -1, pend_idx = 0;
   if constexpr (kStats && !kMassOnly) {
     const int bp = p.stat_pad;
-    for (int i = tid; i < kStatRows * kStatCols; i += kWaves * 64) {
-      const int r = i / kStatCols, si = i % kStatCols;
+    for (int i = tid; i < kStatRows * kCols; i += kWaves * 64) {
+      const int r = i / kCols, si = i % kCols;
       const int pos = (si & ~12) | ((si & 4) << 1) | ((si & 8) >> 1);
       const int q2 = pos % (2 * bp);
       const int par = q2 / bp, off = q2 % bp;
@@ -560,7 +570,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     }
     dsa::lds_barrier();
     // C row of lane qi's A row: 0-3 and 8 even kinds, 4-7 and 12 odd, else zero.
-    wrow = wtab + (qi < 4 ? qi : qi < 8 ? qi + 1 : qi == 8 ? 4 : qi == 12 ? 9 : 10) * kStatCols;
+    wrow = wtab + (qi < 4 ? qi : qi < 8 ? qi + 1 : qi == 8 ? 4 : qi == 12 ? 9 : 10) * kCols;
   }
 
   float m_run = -INFINITY;
@@ -801,7 +811,7 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
                   auto skip_c, int j) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    if (next_kb != -2) issue(next_kb, next_half, kn, vn);
+    if (!kSingleStage && next_kb != -2) issue(next_kb, next_half, kn, vn);
     if (walk_at != nullptr && half == 0 && kb >= 0)
       __hip_atomic_store(walk_at, walk_entry(bh, kb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (wave_active) {
@@ -844,6 +854,10 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
         }
         if constexpr (!kDeferSums) close_pending();
       }
+    }
+    if constexpr (kSingleStage) {
+      __syncthreads();  // every wave is done with the stage
+      if (next_kb != -2) issue(next_kb, next_half, kn, vn);
     }
   };
   // Gathered stream step: chunk at slot o0 of stream block j0 (whose block
@@ -943,10 +957,12 @@ __global__ void __launch_bounds__(kWaves * 64, kWaves == 4 ? 2 : 1)
     } else {
       for (int j = 0; j < nblk; j += 2) {
         const int kb1 = j + 1 < nblk ? block_of(j + 1) : -2;
-        step(kb, 0, kb1, 0, lds_k0, lds_v0, lds_k1, lds_v1, may_skip, j);
+        step(kb, 0, kb1, 0, lds_k0, lds_v0, kSingleStage ? lds_k0 : lds_k1,
+             kSingleStage ? lds_v0 : lds_v1, may_skip, j);
         if (kb1 == -2) break;
         const int kb2 = j + 2 < nblk ? block_of(j + 2) : -2;
-        step(kb1, 0, kb2, 0, lds_k1, lds_v1, lds_k0, lds_v0, may_skip, j + 1);
+        step(kb1, 0, kb2, 0, kSingleStage ? lds_k0 : lds_k1, kSingleStage ? lds_v0 : lds_v1,
+             lds_k0, lds_v0, may_skip, j + 1);
         kb = kb2;
       }
     }
