@@ -1291,6 +1291,10 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
   const int rem = p.block % kHalfKeys;
   const bool skip = rem != 0 && rem <= 32;
   const bool gather = p.row_ptr && use_gather(p.block, p.kv_tokens, p.k_st, p.v_st);
+  // Resident workgroups: two per CU, four for the single-stage 2-wave ones
+  // (routed blocks, or dense statistics, of at most 64 keys).
+  const bool two_wave = nh == 1 && (p.row_ptr || p.rs_logm);
+  const int slots = device_slots(stream) * (two_wave ? 2 : 1);
   if (lead > 0 && scratch_bytes >= lead) {
     unsigned char* base = static_cast<unsigned char*>(scratch);
     used = lead;
@@ -1303,7 +1307,7 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
     }
     // Calls of more than one round of workgroups take their slots from the
     // work queue.
-    if (grid > device_slots(stream)) p.queue = reinterpret_cast<int32_t*>(base);
+    if (grid > slots) p.queue = reinterpret_cast<int32_t*>(base);
     if (p.row_ptr) {
       int32_t* order = reinterpret_cast<int32_t*>(base + kQueueBytes);
       p.order = order;
@@ -1329,7 +1333,7 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
                                   ? 0
                                   : (int64_t)((scratch_bytes - used) / kPartBytes);
   int parts = 1;
-  const int split = choose_split(grid, device_slots(stream), max_parts_for(p.kv_blocks),
+  const int split = choose_split(grid, slots, max_parts_for(p.kv_blocks),
                                  std::min<int64_t>(part_groups, kMaxPartGroups), &parts);
   p.split_from = (int32_t)(grid - split);
   p.parts = parts;
