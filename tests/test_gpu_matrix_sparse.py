@@ -361,6 +361,52 @@ def test_reference_statistics_case(ops, cuda_device, fused):
     assert (raw_mass[~route_np] == 0).all()
 
 
+@pytest.mark.parametrize("tile_shape,tiles", [((5, 8), 400), ((8, 8), 250), ((3, 8), 666)])
+def test_small_tiles_at_scale(ops, cuda_device, tile_shape, tiles):
+    """Tiles of at most 64 tokens (2-wave workgroups, one staged block at a
+    time) over several rounds of workgroups, so the work queue and the split
+    tail run: fused statistics against the separate deterministic passes on
+    every cell, attention against an fp32 softmax over the routed keys on
+    sampled query tiles."""
+    heads, head_dim = 8, 128
+    tile = tile_shape[0] * tile_shape[1]
+    tokens = tiles * tile
+    generator = torch.Generator().manual_seed(tiles)
+    q, k, v = (torch.randn(1, tokens, heads, head_dim, generator=generator).to(torch.bfloat16)
+               for _ in range(3))
+    route = random_route(heads, tiles, seed=tile, keep=0.6)
+    route[..., 0] = True
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    csr = ops.route_to_csr(route.to(cuda_device), block_size=tile)
+    out, lse, got = ops.bsa_fwd_tile_stats(qd, kd, vd, csr, tile_shape)
+    _, ref_lse = ops.bsa_fwd(qd, kd, vd, csr, return_lse=True, block_size=tile,
+                             deterministic=True)
+    two_pass = ops.tile_stats(qd, kd, ref_lse, tile_shape, csr=csr)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse.cpu().numpy(), atol=1e-4)
+    for name in ("mass", "mass_f16"):
+        np.testing.assert_allclose(got[name].float().cpu().numpy(),
+                                   two_pass[name].float().cpu().numpy(), atol=STAT_ATOL,
+                                   rtol=2e-3, err_msg=name)
+    for name in ("centroid_q_y", "centroid_q_x", "centroid_k_y", "centroid_k_x"):
+        np.testing.assert_allclose(got[name].float().cpu().numpy(),
+                                   two_pass[name].float().cpu().numpy(), atol=CENTROID_ATOL,
+                                   err_msg=name)
+    assert (got["mass"].cpu().numpy()[~route.numpy()] == 0).all()
+    scale = head_dim ** -0.5
+    for h in (0, heads - 1):
+        for qt in (0, 1, tiles // 2, tiles - 1):
+            rows = slice(qt * tile, (qt + 1) * tile)
+            keys = torch.repeat_interleave(route[h, qt], tile)
+            qf = q[0, rows, h].float()
+            kf, vf = k[0, keys, h].float(), v[0, keys, h].float()
+            p = torch.softmax(qf @ kf.T * scale, dim=-1)
+            expected = (p @ vf).numpy()
+            metrics = A.summarize(out[0, rows, h].float().cpu().numpy(), expected)
+            assert metrics["max_absolute_error"] <= 2e-2, (h, qt, metrics)
+            assert metrics["cosine_similarity"] >= 0.9995, (h, qt, metrics)
+
+
 def test_fused_step_at_720p_tile_shape(ops, cuda_device):
     """The bench's 720p matrix-sparse step shape (9 x 8 tiles, 800 tiles
     per head) at 4 heads: fused statistics against the two-pass statistics on
