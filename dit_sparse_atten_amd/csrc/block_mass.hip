@@ -33,18 +33,20 @@ struct BlockMassParams {
   float* mass;       // [heads, blocks, blocks]
   int64_t q_st, q_sh, k_st, k_sh, lse_sh;
   int32_t tokens, heads, blocks;
-  int32_t head_dim;  // 8..128, a multiple of 8
+  int32_t head_dim;  // 8..256, a multiple of 8
   float scale_log2;  // scale * log2(e)
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
 
 
-template <typename T>
+// kHalves: head dims up to 128 * kHalves; above 128 each half-tile is staged
+// as two 128-dim halves whose products add into one fp32 accumulator.
+template <typename T, int kHalves = 1>
 __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
   typedef dsa::Elem<T> E;
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage];
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k0[kKStage * kHalves];
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_k1[kKStage * kHalves];
   __shared__ float part[2][4];
 
   const int tid = threadIdx.x;
@@ -61,18 +63,27 @@ __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
   const bool row_ok = tq < p.tokens;
   const int tq_c = row_ok ? tq : p.tokens - 1;
   const T* qrow = static_cast<const T*>(p.q) + h * p.q_sh + (int64_t)tq_c * p.q_st;
-  typename E::x8 qf[8];
-  dsa::load_q_fragments(qrow, g, p.head_dim, qf);
+  typename E::x8 qf[8 * kHalves];
+#pragma unroll
+  for (int hf = 0; hf < kHalves; ++hf)
+    dsa::load_q_fragments(qrow + 128 * hf, g, p.head_dim - 128 * hf, qf + 8 * hf);
   // Rows past the sequence end get lse = +inf, so every p of theirs is 0.
   const float lse2 = row_ok ? p.lse[h * p.lse_sh + tq] * kLog2e : INFINITY;
 
   const T* kbase = static_cast<const T*>(p.k) + h * p.k_sh;
-  uint32_t koff[4];
-  dsa::k_tile_offsets(wave, lane, p.k_st, p.head_dim, koff);
-  auto issue = [&](int key0, unsigned char* dst) __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t rsrc = dsa::k_tile_rsrc(kbase, p.k_st, key0, p.tokens, p.head_dim);
+  uint32_t koff[kHalves][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dsa::lds_load16(rsrc, dst + (wave * 4 + j) * 1024, koff[j], 0);
+  for (int hf = 0; hf < kHalves; ++hf)
+    dsa::k_tile_offsets(wave, lane, p.k_st, p.head_dim - 128 * hf, koff[hf]);
+  auto issue = [&](int key0, unsigned char* dst) __attribute__((always_inline)) {
+#pragma unroll
+    for (int hf = 0; hf < kHalves; ++hf) {
+      const __amdgpu_buffer_rsrc_t rsrc =
+          dsa::k_tile_rsrc(kbase + 128 * hf, p.k_st, key0, p.tokens, p.head_dim - 128 * hf);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        dsa::lds_load16(rsrc, dst + hf * kKStage + (wave * 4 + j) * 1024, koff[hf][j], 0);
+    }
   };
 
   float* mrow = p.mass + ((int64_t)h * p.blocks + qb) * p.blocks;
@@ -100,11 +111,13 @@ __global__ void __launch_bounds__(256, 2) block_mass_kernel(BlockMassParams p) {
       for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
       const int row = kt * 32 + qi;
 #pragma unroll
-      for (int dc = 0; dc < 8; ++dc) {
-        const typename E::x8 a = *reinterpret_cast<const typename E::x8*>(
-            cur + row * kRowBytes + dsa::k2_swz(row, dc * 2 + g) * 16);
-        sacc = E::mfma32(a, qf[dc], sacc);
-      }
+      for (int hf = 0; hf < kHalves; ++hf)
+#pragma unroll
+        for (int dc = 0; dc < 8; ++dc) {
+          const typename E::x8 a = *reinterpret_cast<const typename E::x8*>(
+              cur + hf * kKStage + row * kRowBytes + dsa::k2_swz(row, dc * 2 + g) * 16);
+          sacc = E::mfma32(a, qf[8 * hf + dc], sacc);
+        }
       if (valid < kHalfKeys) {
 #pragma unroll
         for (int r = 0; r < 16; ++r)
@@ -150,9 +163,9 @@ extern "C" int dsa_block_mass(const void* q, const void* k, int32_t dtype, const
                           dtype);
   if (tokens <= 0 || heads <= 0)
     return dsa::set_error(DSA_EINVAL, "dsa_block_mass: tokens and heads must be positive");
-  if (head_dim <= 0 || head_dim > dsa::kHeadDim || head_dim % 8 != 0)
+  if (head_dim <= 0 || head_dim > 2 * dsa::kHeadDim || head_dim % 8 != 0)
     return dsa::set_error(DSA_EUNSUPPORTED,
-                          "dsa_block_mass: head_dim %d unsupported (a multiple of 8 up to 128)",
+                          "dsa_block_mass: head_dim %d unsupported (a multiple of 8 up to 256)",
                           head_dim);
   if (block_size != 128)
     return dsa::set_error(DSA_EUNSUPPORTED,
@@ -191,9 +204,15 @@ extern "C" int dsa_block_mass(const void* q, const void* k, int32_t dtype, const
   p.blocks = blocks;
   p.head_dim = head_dim;
   p.scale_log2 = scale * kLog2e;
-  if (dtype == DSA_F16)
-    hipLaunchKernelGGL(block_mass_kernel<_Float16>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+  const bool wide = head_dim > dsa::kHeadDim;
+  const dim3 blocks_dim((unsigned)grid), threads(256);
+  if (dtype == DSA_F16 && wide)
+    hipLaunchKernelGGL((block_mass_kernel<_Float16, 2>), blocks_dim, threads, 0, stream, p);
+  else if (dtype == DSA_F16)
+    hipLaunchKernelGGL((block_mass_kernel<_Float16, 1>), blocks_dim, threads, 0, stream, p);
+  else if (wide)
+    hipLaunchKernelGGL((block_mass_kernel<__bf16, 2>), blocks_dim, threads, 0, stream, p);
   else
-    hipLaunchKernelGGL(block_mass_kernel<__bf16>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((block_mass_kernel<__bf16, 1>), blocks_dim, threads, 0, stream, p);
   return dsa::check_launch("dsa_block_mass");
 }

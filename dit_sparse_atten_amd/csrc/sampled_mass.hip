@@ -33,7 +33,7 @@ struct MassParams {
   float* mass;  // [heads, blocks, blocks]
   int64_t q_st, q_sh, k_st, k_sh;
   int32_t tokens, heads, blocks, block_size, samples;  // samples: S (real)
-  int32_t head_dim;  // 8..128, a multiple of 8
+  int32_t head_dim;  // 8..256, a multiple of 8
   float scale;      // score scale (d^-1/2 unless given)
   float logw_full;  // log(block_size / S)
   float logw_last;  // log(size of the last block / S)
@@ -80,14 +80,20 @@ __device__ __forceinline__ void round_pair(float a, float b, float& ra, float& r
 // sequence's last sampled keys (every tile with padding slots) pays the
 // per-score checks.  Sampled key rows are gathered straight into LDS (buffer
 // loads with a per-lane row offset), double-buffered one 64-key tile ahead.
-template <typename T, int SP, bool kPad>
+//
+// kHalves: head dims up to 128 * kHalves.  Head dims above 128 stage each
+// tile as two 128-dim halves (dims 0..127, then 128..) and add both halves'
+// products into one fp32 accumulator before the score is rounded, as one
+// matmul over all dims does.
+template <typename T, int SP, bool kPad, int kHalves = 1>
 __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
   typedef dsa::Elem<T> E;
   constexpr int kTileKeys = 64;
+  constexpr int kHalfBytes = kTileKeys * 256;  // one 128-dim half of a tile
   constexpr bool kWide = SP >= 64;
   constexpr int KBS = kWide ? 1 : 32 / SP;  // key blocks of one 32-key sub-tile
-  __shared__ __attribute__((aligned(1024))) unsigned char st0[kTileKeys * 256];
-  __shared__ __attribute__((aligned(1024))) unsigned char st1[kTileKeys * 256];
+  __shared__ __attribute__((aligned(1024))) unsigned char st0[kHalfBytes * kHalves];
+  __shared__ __attribute__((aligned(1024))) unsigned char st1[kHalfBytes * kHalves];
   __shared__ float wide_part[2][4];  // kWide: per-wave block sums, by block parity
 
   const int tid = threadIdx.x;
@@ -106,13 +112,18 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
   qs = qs < ns ? qs : ns - 1;
   const T* qrow = static_cast<const T*>(p.q) + h * p.q_sh +
                   (int64_t)sampled_token<SP>(qs, p.tokens, p.block_size, S) * p.q_st;
-  typename E::x8 qf[8];
-  dsa::load_q_fragments(qrow, g, p.head_dim, qf);
+  typename E::x8 qf[8 * kHalves];
+#pragma unroll
+  for (int hf = 0; hf < kHalves; ++hf)
+    dsa::load_q_fragments(qrow + 128 * hf, g, p.head_dim - 128 * hf, qf + 8 * hf);
 
   // The head's K rows as one raw buffer (the host keeps them within 2^31 bytes).
   const T* kbase = static_cast<const T*>(p.k) + h * p.k_sh;
-  const __amdgpu_buffer_rsrc_t k_rsrc =
-      dsa::make_rsrc(kbase, (uint32_t)(((int64_t)(p.tokens - 1) * p.k_st + kHeadDim) * 2));
+  __amdgpu_buffer_rsrc_t k_rsrc[kHalves];
+#pragma unroll
+  for (int hf = 0; hf < kHalves; ++hf)
+    k_rsrc[hf] = dsa::make_rsrc(kbase + 128 * hf,
+                                (uint32_t)(((int64_t)(p.tokens - 1) * p.k_st + kHeadDim) * 2));
   // This lane's 4 chunks of tile t: LDS slot idx = (wave * 4 + j) * 64 + lane
   // holds chunk (idx & 15) ^ (row & 15) of tile row idx >> 4.
   auto issue = [&](int t, unsigned char* dst) __attribute__((always_inline)) {
@@ -124,10 +135,12 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
       const int c = (idx & 15) ^ (row & 15);
       int key = kt0 + row;
       key = key < ns ? key : ns - 1;
-      const uint32_t off = (uint32_t)(
-          ((int64_t)sampled_token<SP>(key, p.tokens, p.block_size, S) * p.k_st + c * 8) * 2) |
-                           dsa::dead_bits(c, p.head_dim);
-      dsa::lds_load16(k_rsrc, dst + (wave * 4 + j) * 1024, off, 0);
+      const uint32_t base = (uint32_t)(
+          ((int64_t)sampled_token<SP>(key, p.tokens, p.block_size, S) * p.k_st + c * 8) * 2);
+#pragma unroll
+      for (int hf = 0; hf < kHalves; ++hf)
+        dsa::lds_load16(k_rsrc[hf], dst + hf * kHalfBytes + (wave * 4 + j) * 1024,
+                        base | dsa::dead_bits(c, p.head_dim - 128 * hf), 0);
     }
   };
 
@@ -148,13 +161,15 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll
-      for (int dc = 0; dc < 8; ++dc) {
-        const int key = sub * 32 + qi;
-        const int c = dc * 2 + g;
-        const typename E::x8 a = *reinterpret_cast<const typename E::x8*>(
-            lds_k + key * 256 + ((c ^ (key & 15)) << 4));
-        acc = E::mfma32(a, qf[dc], acc);
-      }
+      for (int hf = 0; hf < kHalves; ++hf)
+#pragma unroll
+        for (int dc = 0; dc < 8; ++dc) {
+          const int key = sub * 32 + qi;
+          const int c = dc * 2 + g;
+          const typename E::x8 a = *reinterpret_cast<const typename E::x8*>(
+              lds_k + hf * kHalfBytes + key * 256 + ((c ^ (key & 15)) << 4));
+          acc = E::mfma32(a, qf[8 * hf + dc], acc);
+        }
       // Score = T(T(q.k) * scale), as a matmul and a scale multiply in T;
       // the softmax input in log2 units is score * log2e + c with
       // c = log(block size / S) * log2e.
@@ -302,10 +317,10 @@ __global__ void __launch_bounds__(256) sampled_mass_kernel(MassParams p) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-template <typename T>
+template <typename T, int kHalves>
 void launch_mass(const MassParams& p, int sp, bool pad, dim3 grid, hipStream_t stream) {
 #define DSA_MASS(SPV, PADV) \
-  hipLaunchKernelGGL((sampled_mass_kernel<T, SPV, PADV>), grid, dim3(256), 0, stream, p)
+  hipLaunchKernelGGL((sampled_mass_kernel<T, SPV, PADV, kHalves>), grid, dim3(256), 0, stream, p)
   if (!pad) {
     switch (sp) {
       case 1: DSA_MASS(1, false); break;
@@ -342,9 +357,9 @@ extern "C" int dsa_sampled_mass(const void* q, const void* k, int32_t dtype,
                           dtype);
   if (tokens <= 0 || heads <= 0 || block_size <= 0)
     return dsa::set_error(DSA_EINVAL, "dsa_sampled_mass: tokens/heads/block must be positive");
-  if (head_dim <= 0 || head_dim > kHeadDim || head_dim % 8 != 0)
+  if (head_dim <= 0 || head_dim > 2 * kHeadDim || head_dim % 8 != 0)
     return dsa::set_error(DSA_EUNSUPPORTED,
-                          "dsa_sampled_mass: head_dim %d unsupported (a multiple of 8 up to 128)",
+                          "dsa_sampled_mass: head_dim %d unsupported (a multiple of 8 up to 256)",
                           head_dim);
   if (block_size > 128)
     return dsa::set_error(DSA_EUNSUPPORTED, "dsa_sampled_mass: block_size %d unsupported (<= 128)",
@@ -386,9 +401,12 @@ extern "C" int dsa_sampled_mass(const void* q, const void* k, int32_t dtype,
   // Padded instances for sample counts that are not a power of two, and for
   // 64 and 128 samples (key and query blocks wider than a sub-tile or wave).
   const bool pad = sp != samples || sp > 32;
+  const bool wide = head_dim > kHeadDim;
   if (dtype == DSA_F16)
-    launch_mass<_Float16>(p, sp, pad, grid, stream);
+    wide ? launch_mass<_Float16, 2>(p, sp, pad, grid, stream)
+         : launch_mass<_Float16, 1>(p, sp, pad, grid, stream);
   else
-    launch_mass<__bf16>(p, sp, pad, grid, stream);
+    wide ? launch_mass<__bf16, 2>(p, sp, pad, grid, stream)
+         : launch_mass<__bf16, 1>(p, sp, pad, grid, stream);
   return dsa::check_launch("dsa_sampled_mass");
 }

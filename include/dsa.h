@@ -180,7 +180,8 @@ int dsa_bsa_fwd_dropout(const void* q, const void* k, const void* v, void* o, in
  * fp32 softmax over all sampled keys plus log(block size / samples),
  * mass[h, qb, kb] = mean over query samples of the sum over key samples.
  * strides[4]: q (t, h), k (t, h) in elements.  samples: 1..block_size;
- * block_size <= 128.  mass: [heads, blocks, blocks], deterministic.
+ * block_size <= 128; head_dim a multiple of 8 up to 256.  mass: [heads,
+ * blocks, blocks], deterministic.
  */
 int dsa_sampled_mass(const void* q, const void* k, int32_t dtype, const int64_t* strides,
                      int32_t tokens, int32_t heads, int32_t head_dim, int32_t block_size,
@@ -195,8 +196,9 @@ int dsa_sampled_mass(const void* q, const void* k, int32_t dtype, const int64_t*
  * exp(scale * <q_t, k_s> - lse[h, t]).  lse: [heads, tokens] fp32 natural-log
  * normaliser of the same Q/K and scale (dsa_bsa_fwd's lse output), head
  * stride lse_head_stride >= tokens.  strides[4]: q (t, h), k (t, h) in
- * elements.  head_dim 128, block_size 128.  mass: [heads, blocks, blocks],
- * every entry written (no initialisation needed); deterministic.
+ * elements.  head_dim a multiple of 8 up to 256, block_size 128.  mass:
+ * [heads, blocks, blocks], every entry written (no initialisation needed);
+ * deterministic.
  */
 int dsa_block_mass(const void* q, const void* k, int32_t dtype, const int64_t* strides,
                    int32_t tokens,
@@ -274,10 +276,11 @@ size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t tokens, int
  * kv_tokens = tokens), with lse required (written: [heads, tokens] fp32) and
  * mass [heads, blocks, blocks] fp32 (blocks = ceil(tokens / 128)): the sum of
  * exp(scale * <q, k> - lse) over each pair of 128-token blocks, as
- * dsa_block_mass writes it.  When tokens is a multiple of 128 the mass comes
- * from the attention launch's own probabilities (the key-side sums beside P V
- * per query row and key block, then a short second launch); otherwise the
- * call runs the attention and then dsa_block_mass.
+ * dsa_block_mass writes it.  When tokens is a multiple of 128 and head_dim
+ * at most 128, the mass comes from the attention launch's own row sums per
+ * query row and key block (then a short second launch); otherwise the call
+ * runs the attention and then dsa_block_mass.  fp32 takes head_dim up to 128
+ * and tokens a multiple of 128.
  *   workspace: dsa_bsa_fwd_block_mass_workspace_bytes(...) bytes, 16-byte
  *            aligned: heads * blocks^2 * 128 * 4 bytes of per-row log-masses
  *            when fused (rounded up to 256), then dsa_bsa_fwd's workspace.

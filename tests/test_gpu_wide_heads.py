@@ -1,7 +1,10 @@
 """GPU parity for head dims above 128 (136..256): SDPA takes any head dim
 (the reference's DenseBackend, attention_backends/dense.py:34-47); here such
 calls run the fp32-compute kernel for every input type (S over 256 dims, O in
-two launches of 128 dims), against the float64 closed form."""
+two launches of 128 dims), against the float64 closed form.  The route
+estimates (sampled and exact block mass, bf16 and fp16) take them too, so
+`flex_reuse` runs its schedule on such heads as the reference's
+FlexAttention does."""
 
 import math
 
@@ -11,7 +14,9 @@ import torch
 
 from oracle import attention as A
 from oracle import dropout as D
-from tests.golden.inputs import random_route
+from oracle import exact as E
+from oracle import route as R
+from tests.golden.inputs import clustered_qkv, random_route
 
 pytestmark = pytest.mark.gpu
 
@@ -73,8 +78,9 @@ def test_wide_heads_dropout_matches_oracle_mask(ops, cuda_device):
 
 
 def test_wide_heads_through_the_backends(cuda_device):
-    """DenseBackend computes them; flex_reuse and sparse send them to dense
-    (their route estimates take head dims up to 128)."""
+    """DenseBackend computes them; the sparse backend sends them to dense
+    (its tile statistics take head dims up to 128), and flex_reuse's step-0
+    bootstrap is that same dense attention."""
     from dit_sparse_atten_amd.attention_backends import context
     from dit_sparse_atten_amd.attention_backends.dense import DenseBackend
     from dit_sparse_atten_amd.attention_backends.flex import FlexReuseBackend
@@ -92,5 +98,85 @@ def test_wide_heads_through_the_backends(cuda_device):
             out = backend(qd, kd, vd)
             torch.cuda.synchronize()
             assert torch.equal(out, dense), backend.name
+    finally:
+        context.reset_runtime_state()
+
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim,samples", [(192, 16), (256, 1), (256, 33), (136, 64)])
+def test_wide_heads_sampled_mass_match_oracle(ops, cuda_device, dtype, head_dim, samples):
+    tokens, heads, block = 1000, 2, 128
+    q, k, _ = clustered_qkv(tokens, heads, head_dim, group=block, seed=head_dim + samples,
+                            dtype=dtype)
+    got = ops.sampled_block_mass(q.to(cuda_device), k.to(cuda_device), block, samples)
+    torch.cuda.synchronize()
+    oracle = R.sampled_block_mass(q.float().numpy(), k.float().numpy(), block, samples,
+                                  score_dtype="bf16" if dtype == torch.bfloat16 else "fp16")
+    np.testing.assert_allclose(got.cpu().numpy(), oracle, atol=2e-3, rtol=2e-3)
+    np.testing.assert_allclose(got.sum(-1).cpu().numpy(), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("head_dim,tokens", [(256, 1024), (192, 1000), (136, 300)])
+def test_wide_heads_block_mass_match_oracle(ops, cuda_device, head_dim, tokens):
+    """dsa_block_mass over 256 dims against the fp64 restatement fed the same
+    LSE, and dsa_bsa_fwd_block_mass (the attention, then that pass) against
+    the two separate calls."""
+    q, k, v = clustered_qkv(tokens, 2, head_dim, group=64, seed=head_dim, dtype=torch.bfloat16)
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    out, lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
+    mass = ops.block_mass(qd, kd, lse)
+    fused_out, fused_lse, fused_mass = ops.bsa_fwd_block_mass(qd, kd, vd)
+    torch.cuda.synchronize()
+    expected = E.exact_block_mass(q.float().numpy(), k.float().numpy(), lse[0].cpu().numpy(), 128)
+    np.testing.assert_allclose(mass.cpu().numpy(), expected, rtol=1e-4, atol=1e-6)
+    assert torch.equal(fused_out, out) and torch.equal(fused_lse, lse)
+    assert torch.equal(fused_mass, mass)
+    valid = np.minimum(128, tokens - 128 * np.arange(mass.shape[1]))
+    np.testing.assert_allclose(mass.sum(-1).cpu().numpy(),
+                               np.broadcast_to(valid, mass.shape[:2]), rtol=1e-4)
+
+
+@pytest.mark.parametrize("bootstrap", ["exact", "sampled"])
+def test_wide_heads_flex_reuse_runs_sparse(ops, cuda_device, bootstrap):
+    """`flex_reuse` at head dim 256: step 0 dense with its route estimate,
+    step 1 sparse on that route, against the oracle's route and the float64
+    block-sparse attention."""
+    from dit_sparse_atten_amd.attention_backends import context, flex
+    context.reset_runtime_state()
+    tokens, heads, grid, head_dim = 2048, 2, (2, 16, 64), 256
+    q, k, v = clustered_qkv(tokens, heads, head_dim, group=128, seed=5, dtype=torch.bfloat16)
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    config = flex.FlexReuseConfig(keep=0.625, mass_target=0.95, total_steps=3,
+                                  bootstrap_mode=bootstrap, route_samples=16,
+                                  prefetch_sampled_bootstrap=False)
+    backend = flex.FlexReuseBackend(config)
+    try:
+        context.set_routing_context(attention_id=2, step=0, branch=0, grid=grid)
+        out0 = backend(qd, kd, vd)
+        torch.cuda.synchronize()
+        qf, kf, vf = (x.float().numpy() for x in (q, k, v))
+        dense, _ = A.block_sparse_attention(qf, kf, vf, None, 128)
+        metrics = A.summarize(out0.float().cpu().numpy(), dense)
+        assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
+        state = next(iter(backend.state.values()))
+        if bootstrap == "exact":
+            _, lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
+            mass = ops.block_mass(qd, kd, lse).cpu().numpy()
+            expected = E.exact_route(mass, 0.95, 0.625, grid=grid)
+        else:
+            mass = ops.sampled_block_mass(qd, kd, 128, 16).cpu().numpy()
+            expected = R.top_mass_route(mass, 0.95, 0.625)
+            expected = R.first_frame_sink(expected, grid, 128)
+        route = state["route"].cpu().numpy()
+        assert (route == expected).all()
+        assert not state["dense"]
+        context.set_routing_context(attention_id=2, step=1, branch=0, grid=grid)
+        out1 = backend(qd, kd, vd)
+        torch.cuda.synchronize()
+        sparse, _ = A.block_sparse_attention(qf, kf, vf, route, 128)
+        metrics = A.summarize(out1.float().cpu().numpy(), sparse)
+        assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
+        assert backend.phase_counts["sparse_reuse"] == 1
     finally:
         context.reset_runtime_state()
