@@ -278,8 +278,9 @@ class MatrixSparseBackend:
         })
 
     def __call__(self, q, k, v, softmax_scale=None, **kwargs):
-        # The tile statistics take head dims up to 128; wider heads run dense.
-        if q.shape[1] == k.shape[1] and q.shape[0] == 1 and q.shape[-1] <= ops.HEAD_DIM:
+        # The tile statistics take head dims up to 256 (136..256 on the
+        # fp32-compute kernel); wider heads run dense.
+        if q.shape[1] == k.shape[1] and q.shape[0] == 1 and q.shape[-1] <= 2 * ops.HEAD_DIM:
             attention_id, _, _, grid = routing_context(include_grid=True)
             if self.config.first_layer_dense and attention_id == 0:
                 return self.dense(q, k, v, softmax_scale=softmax_scale, **kwargs)

@@ -411,16 +411,14 @@ extern "C" int dsa_bsa_fwd_tile_stats(const void* q, const void* k, const void* 
     return dsa::set_error(DSA_EINVAL, "%s: %d tokens are not whole %d-token tiles", who, tokens,
                           tile);
   if (entries < 0) return dsa::set_error(DSA_EINVAL, "%s: entries must be >= 0", who);
-  if (head_dim > kHeadDim)
-    return dsa::set_error(DSA_EUNSUPPORTED, "%s: head_dim %d unsupported (statistics: up to 128)",
-                          who, head_dim);
   const int32_t tiles = tokens / tile;
   const bool dense = row_ptr == nullptr;
   if (dense && entries < (int64_t)heads * tiles * tiles)
     return dsa::set_error(DSA_EINVAL, "%s: dense statistics need entries >= heads * tiles^2",
                           who);
-  // (The fp32-compute kernel always runs blocks of one tile.)
-  const bool blocks128 = dense && dtype != DSA_F32 && token_stream(tile);
+  // (The fp32-compute kernel, which also runs head dims above 128, always
+  // runs blocks of one tile.)
+  const bool blocks128 = dense && dtype != DSA_F32 && head_dim <= kHeadDim && token_stream(tile);
   BsaParams p;
   int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim,
                        blocks128 ? 128 : tile, row_ptr, col_idx, 1, scale, 0, deterministic, lse, who,

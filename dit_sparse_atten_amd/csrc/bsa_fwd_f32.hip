@@ -28,7 +28,8 @@
 //  * kStats: per query row and key tile (one tile per key block), the row's
 //    unnormalised mass log2 sum 2^(scale_log2 s) and its mass-weighted mean
 //    key offsets, in the format the 16-bit kernels write (rs_logm, rs_mean)
-//    for tile_stats_reduce_kernel;
+//    for tile_stats_reduce_kernel; at kD = 256 the first of the two
+//    launches writes them;
 //  * kD = 256 (head dims 136..256): S^T runs over all 256 dims (128 Q
 //    registers per lane), and O is computed in two launches of 128 output
 //    dims each (`dim0` = 0, 128), each staging only its half of V, so the O
@@ -100,7 +101,6 @@ template <typename T, int kD, bool kRouted, bool kStats, bool kDropout>
 __global__ void __launch_bounds__(256, kD == 128 ? 2 : 1) bsa_fwd_f32_kernel(BsaParams p,
                                                                             int dim0) {
   static_assert(!(kDropout && (kRouted || kStats)), "dropout: dense attention only");
-  static_assert(!(kStats && kD != 128), "statistics: head dims up to 128");
   constexpr int kHalfD = kD / 2;      // dims per lane half in S^T
   constexpr int kRowChunks = kD / 4;  // 16-byte chunks of a staged K row
   __shared__ __attribute__((aligned(16))) float ks[2][kSubKeys * kD];
@@ -382,18 +382,22 @@ int launch_f32_typed(const BsaParams& p, hipStream_t stream, const char* who) {
     hipLaunchKernelGGL(kernel, blocks, threads, 0, stream, p, dim0);
   };
   if (p.head_dim > kHeadDim) {
-    // Head dims 136..256: two launches of 128 output dims each.
-    if (p.rs_logm)
-      return dsa::set_error(DSA_EUNSUPPORTED, "%s: statistics take head dims up to 128", who);
+    // Head dims 136..256: two launches of 128 output dims each; the first
+    // also writes the statistics (both see the same probabilities).
+    if (p.rs_logm && p.drop_thresh != 0)
+      return dsa::set_error(DSA_EUNSUPPORTED, "%s: dropout takes dense attention only", who);
     for (int dim0 = 0; dim0 < p.head_dim; dim0 += kHeadDim) {
+      const bool stats = p.rs_logm && dim0 == 0;
       if (p.drop_thresh != 0) {
         if (p.row_ptr)
           return dsa::set_error(DSA_EUNSUPPORTED, "%s: dropout takes dense attention only", who);
         run(bsa_fwd_f32_kernel<T, kMaxHeadDim, false, false, true>, dim0);
       } else if (p.row_ptr) {
-        run(bsa_fwd_f32_kernel<T, kMaxHeadDim, true, false, false>, dim0);
+        if (stats) run(bsa_fwd_f32_kernel<T, kMaxHeadDim, true, true, false>, dim0);
+        else run(bsa_fwd_f32_kernel<T, kMaxHeadDim, true, false, false>, dim0);
       } else {
-        run(bsa_fwd_f32_kernel<T, kMaxHeadDim, false, false, false>, dim0);
+        if (stats) run(bsa_fwd_f32_kernel<T, kMaxHeadDim, false, true, false>, dim0);
+        else run(bsa_fwd_f32_kernel<T, kMaxHeadDim, false, false, false>, dim0);
       }
     }
   } else if (p.drop_thresh != 0) {

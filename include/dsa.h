@@ -248,7 +248,8 @@ int dsa_tile_stats(const void* q, const void* k, int32_t dtype, const int64_t* s
  * launch; no second QK pass runs.  Routed calls attend over blocks of one
  * tile.  Dense calls with tiles of 64..128 tokens, a multiple of 8, attend
  * over 128-token blocks and run unsplit; other dense calls attend over
- * blocks of one tile.
+ * blocks of one tile.  Head dims 136..256 (and fp32 inputs) run the
+ * fp32-compute kernel on blocks of one tile.
  *   workspace: dsa_bsa_fwd_tile_stats_workspace_bytes(...) bytes, 16-byte
  *            aligned: entries * tile * 8 bytes of per-row statistics
  *            (rounded up to 256), then dsa_bsa_fwd's workspace.

@@ -28,10 +28,10 @@ def ops():
     return module
 
 
-def _tile_major_inputs(grid, heads, seed, tile=64):
+def _tile_major_inputs(grid, heads, seed, tile=64, head_dim=128):
     case = S.SparsePathCase(grid, tile=tile)
     tokens = grid[0] * grid[1] * grid[2]
-    q, k, v = clustered_qkv(tokens, heads, 128, group=case.tile, seed=seed,
+    q, k, v = clustered_qkv(tokens, heads, head_dim, group=case.tile, seed=seed,
                             permutation=torch.as_tensor(case.permutation, dtype=torch.long),
                             dtype=torch.bfloat16)
     # Tile-major order on both sides.
@@ -46,7 +46,7 @@ def _oracle_stats(case, q, k, v, route=None):
     tiles = tokens // case.tile
     stats = S.empty_stats(heads, tiles)
     offsets = S.spatial_offsets(case.tile_shape, tiles)
-    scale = 128 ** -0.5
+    scale = qf.shape[-1] ** -0.5
     if route is None:
         _, _, out = S.dense_route(qf, kf, vf, case.tile, 256, 0.95, 0.625, scale, stats, offsets)
     else:
@@ -233,6 +233,40 @@ def test_fused_dense_step_matches_oracle(ops, cuda_device, grid, tile):
     _compare_stats(got, expected)
     metrics = A.summarize(out.float().cpu().numpy(), expected_out)
     assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
+    np.testing.assert_allclose(got["mass"].sum(-1).cpu().numpy(), case.tile / q.shape[1],
+                               rtol=2e-3)
+
+
+@pytest.mark.parametrize("grid,tile,head_dim", [((2, 16, 16), 64, 256), ((2, 14, 21), 49, 256),
+                                                ((2, 16, 32), 128, 192), ((1, 22, 22), 121, 136)])
+@pytest.mark.parametrize("routed", [True, False])
+def test_fused_step_wide_heads(ops, cuda_device, grid, tile, head_dim, routed):
+    """Head dims 136..256 through dsa_bsa_fwd_tile_stats: the fp32-compute
+    kernel on blocks of one tile, whose first 128-dim launch also writes the
+    statistics (S runs over every dim in both), against the oracle's
+    sparse_chunk / _dense_route and against bsa_fwd on the same route."""
+    case, q, k, v = _tile_major_inputs(grid, 2, seed=head_dim + tile, tile=tile,
+                                       head_dim=head_dim)
+    tiles = q.shape[1] // case.tile
+    route = None
+    csr = None
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    if routed:
+        route = random_route(2, tiles, seed=tile, keep=0.55).numpy()
+        route[..., 0] = True
+        csr = ops.route_to_csr(torch.from_numpy(route).to(cuda_device), block_size=case.tile)
+    out, lse, got = ops.bsa_fwd_tile_stats(qd, kd, vd, csr, case.tile_shape, deterministic=True)
+    ref_out, ref_lse = ops.bsa_fwd(qd, kd, vd, csr, return_lse=True, block_size=case.tile,
+                                   deterministic=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse.cpu().numpy(), atol=1e-5)
+    expected, expected_out = _oracle_stats(case, q, k, v, route)
+    _compare_stats(got, expected)
+    metrics = A.summarize(out.float().cpu().numpy(), expected_out)
+    assert metrics["max_absolute_error"] <= 2e-2 and metrics["cosine_similarity"] >= 0.9995
+    if routed:
+        assert (got["mass"].cpu().numpy()[~route] == 0).all()
     np.testing.assert_allclose(got["mass"].sum(-1).cpu().numpy(), case.tile / q.shape[1],
                                rtol=2e-3)
 

@@ -2,9 +2,9 @@
 (the reference's DenseBackend, attention_backends/dense.py:34-47); here such
 calls run the fp32-compute kernel for every input type (S over 256 dims, O in
 two launches of 128 dims), against the float64 closed form.  The route
-estimates (sampled and exact block mass, bf16 and fp16) take them too, so
-`flex_reuse` runs its schedule on such heads as the reference's
-FlexAttention does."""
+estimates (sampled and exact block mass, bf16 and fp16) and the tile
+statistics take them too, so `flex_reuse` and `sparse` run their schedules
+on such heads as the reference's FlexAttention does."""
 
 import math
 
@@ -16,6 +16,7 @@ from oracle import attention as A
 from oracle import dropout as D
 from oracle import exact as E
 from oracle import route as R
+from oracle import sparse_path as S
 from tests.golden.inputs import clustered_qkv, random_route
 
 pytestmark = pytest.mark.gpu
@@ -78,13 +79,11 @@ def test_wide_heads_dropout_matches_oracle_mask(ops, cuda_device):
 
 
 def test_wide_heads_through_the_backends(cuda_device):
-    """DenseBackend computes them; the sparse backend sends them to dense
-    (its tile statistics take head dims up to 128), and flex_reuse's step-0
-    bootstrap is that same dense attention."""
+    """DenseBackend computes them, and flex_reuse's step-0 bootstrap is that
+    same dense attention."""
     from dit_sparse_atten_amd.attention_backends import context
     from dit_sparse_atten_amd.attention_backends.dense import DenseBackend
     from dit_sparse_atten_amd.attention_backends.flex import FlexReuseBackend
-    from dit_sparse_atten_amd.attention_backends.sparse import MatrixSparseBackend
     q, k, v = _qkv(1, 1024, 1024, 2, 192, seed=8, dtype=torch.bfloat16)
     qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
     dense = DenseBackend()(qd, kd, vd)
@@ -94,10 +93,58 @@ def test_wide_heads_through_the_backends(cuda_device):
     context.reset_runtime_state()
     try:
         context.set_routing_context(attention_id=1, step=0, branch=0, grid=(4, 16, 16))
-        for backend in (FlexReuseBackend(), MatrixSparseBackend()):
+        out = FlexReuseBackend()(qd, kd, vd)
+        torch.cuda.synchronize()
+        assert torch.equal(out, dense)
+    finally:
+        context.reset_runtime_state()
+
+
+@pytest.mark.parametrize("head_dim", [256, 192])
+def test_wide_heads_sparse_backend_steps(ops, cuda_device, head_dim):
+    """Two steps of MatrixSparseBackend at a wide head dim: step 0 is the
+    dense bootstrap whose tile statistics give the route (the oracle's
+    top-mass selection of the same mass plus the frame-0 sink), step 1 runs
+    sparse on that route; both outputs against the float64 attention over
+    the route used."""
+    from dit_sparse_atten_amd.attention_backends import context
+    from dit_sparse_atten_amd.attention_backends.sparse import MatrixSparseBackend, SparseConfig
+    grid, heads = (2, 16, 32), 2
+    case = S.SparsePathCase(grid, tile=64)
+    tokens = grid[0] * grid[1] * grid[2]
+    perm = torch.as_tensor(case.permutation, dtype=torch.long)
+    sink = case.block_h * case.block_w
+    grid_tiles = (grid[0], case.block_h, case.block_w)
+    backend = MatrixSparseBackend(SparseConfig(tile=64, keep=0.625, mass_target=0.95))
+    q, k, v = clustered_qkv(tokens, heads, head_dim, group=64, seed=head_dim, permutation=perm,
+                            dtype=torch.bfloat16)
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    qt, kt, vt = (x[:, perm].float().numpy() for x in (q, k, v))
+    context.reset_runtime_state()
+    try:
+        previous = None
+        for step in range(2):
+            context.set_routing_context(attention_id=2, step=step, branch=0, grid=grid)
             out = backend(qd, kd, vd)
             torch.cuda.synchronize()
-            assert torch.equal(out, dense), backend.name
+            state = {key: val.cpu().numpy() for key, val in
+                     next(iter(backend.state.values())).items() if torch.is_tensor(val)}
+            route_used = None if previous is None else S.expand(previous, "reuse", grid_tiles)
+            expected, _ = A.block_sparse_attention(qt, kt, vt, route_used, case.tile)
+            restored = np.empty_like(expected)
+            restored[:, perm.numpy()] = expected
+            metrics = A.summarize(out.float().cpu().numpy(), restored)
+            assert metrics["max_absolute_error"] <= 2e-2, (step, metrics)
+            assert metrics["cosine_similarity"] >= 0.9995, (step, metrics)
+            if previous is None:
+                tiled = [x[:, perm].to(cuda_device) for x in (q, k, v)]
+                _, _, stats = ops.bsa_fwd_tile_stats(*tiled, None, case.tile_shape)
+                mask = np.array(R.top_mass_route(stats["mass"].cpu().numpy(), 0.95, 0.625),
+                                copy=True)
+                mask[..., :sink] = True
+                np.testing.assert_array_equal(state["mask"], mask)
+                assert not state["mask"].all()
+            previous = state
     finally:
         context.reset_runtime_state()
 
