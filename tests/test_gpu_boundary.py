@@ -168,7 +168,7 @@ def test_head_dim_32_tile_stats(ops, cuda_device):
     _, lse = ops.bsa_fwd(qd, kd, vd, scale=scale, return_lse=True)
     got = ops.tile_stats(qd, kd, lse, case.tile_shape, scale=scale)
     torch.cuda.synchronize()
-    expected, _ = _oracle_stats(case, q, k, v)
+    expected, _ = _oracle_stats(case, q, k, v, scale=scale)
     _compare_stats(got, expected)
 
 

@@ -39,14 +39,16 @@ def _tile_major_inputs(grid, heads, seed, tile=64, head_dim=128):
     return case, q[:, perm], k[:, perm], v[:, perm]
 
 
-def _oracle_stats(case, q, k, v, route=None):
-    """Oracle statistics (fp32 numpy) of tile-major bf16 inputs."""
+def _oracle_stats(case, q, k, v, route=None, scale=None):
+    """Oracle statistics (fp32 numpy) of tile-major bf16 inputs; the softmax
+    scale defaults to head_dim ** -0.5, as the kernels' does."""
     qf, kf, vf = (x.float().numpy() for x in (q, k, v))
     tokens, heads = qf.shape[1:3]
     tiles = tokens // case.tile
     stats = S.empty_stats(heads, tiles)
     offsets = S.spatial_offsets(case.tile_shape, tiles)
-    scale = qf.shape[-1] ** -0.5
+    if scale is None:
+        scale = qf.shape[-1] ** -0.5
     if route is None:
         _, _, out = S.dense_route(qf, kf, vf, case.tile, 256, 0.95, 0.625, scale, stats, offsets)
     else:
