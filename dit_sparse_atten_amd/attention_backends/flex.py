@@ -420,9 +420,8 @@ class FlexReuseBackend:
             and not causal
             and window_size == (-1, -1)
             # The route estimates (sampled and exact block mass) take head
-            # dims up to 256 in bf16 and fp16, up to 128 in float32; wider
-            # heads run dense.
-            and q.shape[-1] <= (ops.HEAD_DIM if dtype == torch.float32 else 2 * ops.HEAD_DIM)
+            # dims up to 256; wider heads run dense.
+            and q.shape[-1] <= 2 * ops.HEAD_DIM
         )
         if not supported:
             return self.dense(q, k, v, **dense_kwargs)

@@ -471,7 +471,7 @@ extern "C" size_t dsa_bsa_fwd_block_mass_workspace_bytes(int32_t heads, int32_t 
                                                          int32_t head_dim) {
   if (heads <= 0 || tokens <= 0 || head_dim <= 0) return 0;
   const size_t attention = dsa_bsa_workspace_bytes_block(1, heads, tokens, head_dim, 128);
-  if (tokens % 128 != 0 || head_dim > kHeadDim) return attention;
+  if (tokens % 128 != 0) return attention;
   const int64_t blocks = tokens / 128;
   return attention + row_mass_bytes((int64_t)heads * blocks * blocks, 128);
 }
@@ -490,9 +490,6 @@ extern "C" int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* 
   if (dtype == DSA_F32 && tokens % 128 != 0)
     return dsa::set_error(DSA_EUNSUPPORTED, "%s: fp32 needs tokens a multiple of 128, got %d", who,
                           tokens);
-  if (dtype == DSA_F32 && head_dim > kHeadDim)
-    return dsa::set_error(DSA_EUNSUPPORTED, "%s: fp32 takes head_dim up to 128, got %d", who,
-                          head_dim);
   BsaParams p;
   int status = prepare(q, k, v, o, dtype, strides, 1, tokens, tokens, heads, head_dim, 128,
                        nullptr, nullptr, 1, scale, 0, 1, lse, who, &p);
@@ -504,9 +501,10 @@ extern "C" int dsa_bsa_fwd_block_mass(const void* q, const void* k, const void* 
     return dsa::set_error(DSA_EINVAL, "%s: workspace of %zu bytes, %zu needed", who,
                           workspace_bytes, need);
   unsigned char* base = static_cast<unsigned char*>(workspace);
-  if (tokens % 128 != 0 || head_dim > kHeadDim) {
-    // A partial last block, or heads wider than 128 (the attention runs on
-    // the fp32-compute kernel): the dense attention, then the block-mass pass.
+  if (tokens % 128 != 0) {
+    // A partial last block: the dense attention, then the block-mass pass.
+    // (Heads wider than 128 take the mass from the fp32-compute kernel's
+    // statistics below.)
     status = launch(dtype, p, base, workspace_bytes, stream, who);
     if (status != DSA_OK) return status;
     const int64_t mass_strides[4] = {strides[1], strides[2], strides[4], strides[5]};

@@ -1379,6 +1379,6 @@ int launch_typed(BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t s
 // fp16 instances (bsa_fwd_f16.hip).
 int bsa_launch_f16(bsa::BsaParams p, void* scratch, size_t scratch_bytes, hipStream_t stream,
                    const char* who);
-// fp32-compute kernel (bsa_fwd_f32.hip): fp32 inputs (dtype DSA_F32), and
-// dense calls with dropout of any input type.
+// fp32-compute kernel (bsa_fwd_f32.hip): fp32 inputs (dtype DSA_F32), dense
+// calls with dropout, and head dims 136..256, of any input type.
 int bsa_launch_f32(bsa::BsaParams p, int32_t dtype, hipStream_t stream, const char* who);

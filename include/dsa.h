@@ -277,11 +277,11 @@ size_t dsa_bsa_fwd_tile_stats_workspace_bytes(int32_t heads, int32_t tokens, int
  * kv_tokens = tokens), with lse required (written: [heads, tokens] fp32) and
  * mass [heads, blocks, blocks] fp32 (blocks = ceil(tokens / 128)): the sum of
  * exp(scale * <q, k> - lse) over each pair of 128-token blocks, as
- * dsa_block_mass writes it.  When tokens is a multiple of 128 and head_dim
- * at most 128, the mass comes from the attention launch's own row sums per
- * query row and key block (then a short second launch); otherwise the call
- * runs the attention and then dsa_block_mass.  fp32 takes head_dim up to 128
- * and tokens a multiple of 128.
+ * dsa_block_mass writes it.  When tokens is a multiple of 128, the mass
+ * comes from the attention launch's own row sums per query row and key
+ * block (then a short second launch; head dims above 128 on the
+ * fp32-compute kernel); otherwise the call runs the attention and then
+ * dsa_block_mass.  fp32 takes tokens a multiple of 128.
  *   workspace: dsa_bsa_fwd_block_mass_workspace_bytes(...) bytes, 16-byte
  *            aligned: heads * blocks^2 * 128 * 4 bytes of per-row log-masses
  *            when fused (rounded up to 256), then dsa_bsa_fwd's workspace.

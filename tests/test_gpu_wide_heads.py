@@ -164,11 +164,12 @@ def test_wide_heads_sampled_mass_match_oracle(ops, cuda_device, dtype, head_dim,
     np.testing.assert_allclose(got.sum(-1).cpu().numpy(), 1.0, atol=1e-5)
 
 
-@pytest.mark.parametrize("head_dim,tokens", [(256, 1024), (192, 1000), (136, 300)])
+@pytest.mark.parametrize("head_dim,tokens", [(256, 1024), (192, 1000), (136, 300), (192, 512)])
 def test_wide_heads_block_mass_match_oracle(ops, cuda_device, head_dim, tokens):
     """dsa_block_mass over 256 dims against the fp64 restatement fed the same
-    LSE, and dsa_bsa_fwd_block_mass (the attention, then that pass) against
-    the two separate calls."""
+    LSE, and dsa_bsa_fwd_block_mass against the same restatement: from the
+    fp32-compute kernel's own statistics at whole 128-token blocks, else the
+    attention and then dsa_block_mass (equal to the two separate calls)."""
     q, k, v = clustered_qkv(tokens, 2, head_dim, group=64, seed=head_dim, dtype=torch.bfloat16)
     qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
     out, lse = ops.bsa_fwd(qd, kd, vd, return_lse=True)
@@ -178,10 +179,49 @@ def test_wide_heads_block_mass_match_oracle(ops, cuda_device, head_dim, tokens):
     expected = E.exact_block_mass(q.float().numpy(), k.float().numpy(), lse[0].cpu().numpy(), 128)
     np.testing.assert_allclose(mass.cpu().numpy(), expected, rtol=1e-4, atol=1e-6)
     assert torch.equal(fused_out, out) and torch.equal(fused_lse, lse)
-    assert torch.equal(fused_mass, mass)
+    if tokens % 128:
+        assert torch.equal(fused_mass, mass)
+    else:
+        np.testing.assert_allclose(fused_mass.cpu().numpy(), expected, rtol=1e-4, atol=1e-6)
     valid = np.minimum(128, tokens - 128 * np.arange(mass.shape[1]))
-    np.testing.assert_allclose(mass.sum(-1).cpu().numpy(),
-                               np.broadcast_to(valid, mass.shape[:2]), rtol=1e-4)
+    for got in (mass, fused_mass):
+        np.testing.assert_allclose(got.sum(-1).cpu().numpy(),
+                                   np.broadcast_to(valid, mass.shape[:2]), rtol=1e-4)
+
+
+@pytest.mark.parametrize("head_dim", [256, 160])
+def test_wide_heads_fp32_exact_bootstrap(ops, cuda_device, head_dim):
+    """float32 at head dims above 128: dsa_bsa_fwd_block_mass against the fp64
+    mass of its own LSE, then `flex_reuse`'s exact bootstrap and a routed step
+    against the float64 attention over the route it chose."""
+    from dit_sparse_atten_amd.attention_backends import context
+    from dit_sparse_atten_amd.attention_backends.flex import FlexReuseBackend, FlexReuseConfig
+    q, k, v = clustered_qkv(1024, 2, head_dim, group=64, seed=head_dim + 1)
+    qd, kd, vd = (x.to(cuda_device) for x in (q, k, v))
+    out, lse, mass = ops.bsa_fwd_block_mass(qd, kd, vd)
+    torch.cuda.synchronize()
+    qf, kf, vf = (x.numpy() for x in (q, k, v))
+    want, want_lse = A.block_sparse_attention(qf, kf, vf, None, 128)
+    np.testing.assert_allclose(out.double().cpu().numpy(), want, atol=ATOL[torch.float32], rtol=0)
+    np.testing.assert_allclose(lse.double().cpu().numpy(), want_lse, atol=1e-4, rtol=0)
+    expected = E.exact_block_mass(qf, kf, lse[0].cpu().numpy(), 128)
+    np.testing.assert_allclose(mass.cpu().numpy(), expected, rtol=1e-4, atol=1e-6)
+    backend = FlexReuseBackend(FlexReuseConfig(keep=0.5))
+    context.reset_runtime_state()
+    try:
+        context.set_routing_context(attention_id=1, step=0, branch=0, grid=None)
+        out0 = backend(qd, kd, vd, dtype=torch.float32)
+        route = next(iter(backend.state.values()))["route"].clone()
+        context.set_routing_context(step=1)
+        out1 = backend(qd, kd, vd, dtype=torch.float32)
+        torch.cuda.synchronize()
+    finally:
+        context.reset_runtime_state()
+    np.testing.assert_allclose(out0.double().cpu().numpy(), want, atol=ATOL[torch.float32], rtol=0)
+    routed, _ = A.block_sparse_attention(qf, kf, vf, route.cpu().numpy(), 128)
+    np.testing.assert_allclose(out1.double().cpu().numpy(), routed, atol=ATOL[torch.float32],
+                               rtol=0)
+    assert not route.cpu().numpy().all()
 
 
 @pytest.mark.parametrize("bootstrap", ["exact", "sampled"])
