@@ -157,8 +157,8 @@ namespace {
 // w_r = 2^(rs_logm - lse_r log2 e), its probability mass on that key tile:
 //   mass = sum w_r, q_y = sum w_r y(r), q_x = sum w_r x(r),
 //   k_y = sum w_r mean_y, k_x = sum w_r mean_x,
-// each summed in a fixed order (one wave per listed tile, a fixed-shape wave
-// reduction).  Outputs as dsa_tile_stats writes them: mass / tokens (fp32,
+// each summed in a fixed order (eight lanes per listed tile, then a
+// three-step exchange).  Outputs as dsa_tile_stats writes them: mass / tokens (fp32,
 // fp16) and the centroids moment / max(mass, 1e-12) (fp16); cells the row
 // does not list are zero.
 struct ReduceParams {
@@ -183,85 +183,89 @@ struct ReduceParams {
 __global__ void __launch_bounds__(256) tile_stats_reduce_kernel(ReduceParams p) {
   __shared__ float lse2[128], uy[128], ux[128];
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row = blockIdx.x;
   const int h = row / p.tiles, qt = row % p.tiles;
-  for (int i = tid; i < p.tile; i += 256) {
-    lse2[i] = p.lse[(int64_t)h * p.tokens + (int64_t)qt * p.tile + i] * 1.4426950408889634f;
-    uy[i] = dsa::tile_axis(i / p.tile_w, p.tile_h);
-    ux[i] = dsa::tile_axis(i % p.tile_w, p.tile_w);
+  // Rows past the tile read zeros (their log-masses are -inf).
+  for (int i = tid; i < 128; i += 256) {
+    const bool in = i < p.tile;
+    lse2[i] = in ? p.lse[(int64_t)h * p.tokens + (int64_t)qt * p.tile + i] * 1.4426950408889634f
+                 : 0.f;
+    uy[i] = in ? dsa::tile_axis(i / p.tile_w, p.tile_h) : 0.f;
+    ux[i] = in ? dsa::tile_axis(i % p.tile_w, p.tile_w) : 0.f;
   }
   const int64_t cell0 = (int64_t)row * p.tiles;
-  const __half zero = __float2half(0.f);
-  for (int kt = tid; kt < p.tiles; kt += 256) {
-    p.mass32[cell0 + kt] = 0.f;
-    if (p.mass16) p.mass16[cell0 + kt] = zero;
-    if (p.cqy) p.cqy[cell0 + kt] = zero;
-    if (p.cqx) p.cqx[cell0 + kt] = zero;
-    if (p.cky) p.cky[cell0 + kt] = zero;
-    if (p.ckx) p.ckx[cell0 + kt] = zero;
+  if (p.dense) {
+    // Every cell of the row is listed and written below.
+    dsa::lds_barrier();
+  } else {
+    const __half zero = __float2half(0.f);
+    for (int kt = tid; kt < p.tiles; kt += 256) {
+      p.mass32[cell0 + kt] = 0.f;
+      if (p.mass16) p.mass16[cell0 + kt] = zero;
+      if (p.cqy) p.cqy[cell0 + kt] = zero;
+      if (p.cqx) p.cqx[cell0 + kt] = zero;
+      if (p.cky) p.cky[cell0 + kt] = zero;
+      if (p.ckx) p.ckx[cell0 + kt] = zero;
+    }
+    // The zeros land before the listed cells are written (vmcnt(0) barrier).
+    dsa::lds_barrier<true>();
   }
-  // The zeros land before the listed cells are written (vmcnt(0) barrier).
-  dsa::lds_barrier<true>();
   const int start = p.dense ? 0 : p.row_ptr[row];
   const int end = p.dense ? p.tiles : (int)min((int64_t)p.row_ptr[row + 1], p.entries);
-  // Each wave reduces kCells listed cells at a time (cells e, e + 4, ...), so
-  // that their row loads are in flight together: one cell at a time left the
-  // kernel waiting on load latency.
-  constexpr int kCells = 4;
-  for (int e0 = start + wave; e0 < end; e0 += 4 * kCells) {
-    int kt[kCells];
-    int64_t at0[kCells];
-    bool ok[kCells];
+  // kGroup lanes reduce one listed cell (lane j of the group takes the rows
+  // j, j + kGroup, ...), so a wave has 64 / kGroup cells' row loads in flight
+  // at once and combines each cell's five sums in log2(kGroup) exchange
+  // steps.  The summation order is fixed: per lane in row order, then the
+  // exchange tree.
+  constexpr int kGroup = 8;
+  constexpr int kRowsPerLane = 128 / kGroup;
+  const int sub = lane % kGroup;
+  const int groups = 256 / kGroup;
+  for (int e = start + tid / kGroup; e - (int)(tid / kGroup) < end; e += groups) {
+    const int kt = e < end ? (p.dense ? e : p.col_idx[e]) : -1;
+    const bool ok = (unsigned)kt < (unsigned)p.tiles;
+    const int64_t at0 = p.dense ? ((int64_t)h * p.tiles + kt) * p.tokens + (int64_t)qt * p.tile
+                                : (int64_t)e * p.tile;
+    // Every row load of the lane is issued before the first is used.
+    float lg[kRowsPerLane];
+    uint32_t mn[kRowsPerLane];
 #pragma unroll
-    for (int u = 0; u < kCells; ++u) {
-      const int e = e0 + 4 * u;
-      kt[u] = e < end ? (p.dense ? e : p.col_idx[e]) : -1;
-      ok[u] = (unsigned)kt[u] < (unsigned)p.tiles;
-      at0[u] = p.dense ? ((int64_t)h * p.tiles + kt[u]) * p.tokens + (int64_t)qt * p.tile
-                       : (int64_t)e * p.tile;
+    for (int i = 0; i < kRowsPerLane; ++i) {
+      const int r = sub + i * kGroup;
+      const bool in = ok && r < p.tile;
+      lg[i] = in ? p.rs_logm[at0 + r] : -INFINITY;
+      mn[i] = in && !p.raw ? p.rs_mean[at0 + r] : 0u;
     }
-    float m[kCells], qy[kCells], qx[kCells], ky[kCells], kx[kCells];
+    float m = 0.f, qy = 0.f, qx = 0.f, ky = 0.f, kx = 0.f;
 #pragma unroll
-    for (int u = 0; u < kCells; ++u) m[u] = qy[u] = qx[u] = ky[u] = kx[u] = 0.f;
-    for (int r = lane; r < p.tile; r += 64) {
-      float lg[kCells];
-      uint32_t mn[kCells];
-#pragma unroll
-      for (int u = 0; u < kCells; ++u) {
-        lg[u] = ok[u] ? p.rs_logm[at0[u] + r] : -INFINITY;
-        mn[u] = ok[u] && !p.raw ? p.rs_mean[at0[u] + r] : 0u;
-      }
-#pragma unroll
-      for (int u = 0; u < kCells; ++u) {
-        const float w = __builtin_amdgcn_exp2f(lg[u] - lse2[r]);
-        const dsa_f16x2 mean = __builtin_bit_cast(dsa_f16x2, mn[u]);
-        m[u] += w;
-        qy[u] = fmaf(w, uy[r], qy[u]);
-        qx[u] = fmaf(w, ux[r], qx[u]);
-        ky[u] = fmaf(w, (float)mean[0], ky[u]);
-        kx[u] = fmaf(w, (float)mean[1], kx[u]);
-      }
+    for (int i = 0; i < kRowsPerLane; ++i) {
+      const int r = sub + i * kGroup;
+      const float w = __builtin_amdgcn_exp2f(lg[i] - lse2[r]);
+      const dsa_f16x2 mean = __builtin_bit_cast(dsa_f16x2, mn[i]);
+      m += w;
+      qy = fmaf(w, uy[r], qy);
+      qx = fmaf(w, ux[r], qx);
+      ky = fmaf(w, (float)mean[0], ky);
+      kx = fmaf(w, (float)mean[1], kx);
     }
 #pragma unroll
-    for (int u = 0; u < kCells; ++u) {
-      if (!ok[u]) continue;
-      const float mu = dsa::wave_total(m[u]);
-      const float qyu = dsa::wave_total(qy[u]);
-      const float qxu = dsa::wave_total(qx[u]);
-      const float kyu = dsa::wave_total(ky[u]);
-      const float kxu = dsa::wave_total(kx[u]);
-      if (lane == 0) {
-        const int64_t cell = cell0 + kt[u];
-        const float normalized = p.raw ? mu : mu / (float)p.tokens;
-        const float den = fmaxf(mu, 1e-12f);
-        p.mass32[cell] = normalized;
-        if (p.mass16) p.mass16[cell] = __float2half(normalized);
-        if (p.cqy) p.cqy[cell] = __float2half(qyu / den);
-        if (p.cqx) p.cqx[cell] = __float2half(qxu / den);
-        if (p.cky) p.cky[cell] = __float2half(kyu / den);
-        if (p.ckx) p.ckx[cell] = __float2half(kxu / den);
-      }
+    for (int off = 1; off < kGroup; off <<= 1) {
+      m += __shfl_xor(m, off);
+      qy += __shfl_xor(qy, off);
+      qx += __shfl_xor(qx, off);
+      ky += __shfl_xor(ky, off);
+      kx += __shfl_xor(kx, off);
+    }
+    if (ok && sub == 0) {
+      const int64_t cell = cell0 + kt;
+      const float normalized = p.raw ? m : m / (float)p.tokens;
+      const float den = fmaxf(m, 1e-12f);
+      p.mass32[cell] = normalized;
+      if (p.mass16) p.mass16[cell] = __float2half(normalized);
+      if (p.cqy) p.cqy[cell] = __float2half(qy / den);
+      if (p.cqx) p.cqx[cell] = __float2half(qx / den);
+      if (p.cky) p.cky[cell] = __float2half(ky / den);
+      if (p.ckx) p.ckx[cell] = __float2half(kx / den);
     }
   }
 }
