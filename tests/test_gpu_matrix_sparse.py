@@ -239,16 +239,19 @@ def test_fused_dense_step_matches_oracle(ops, cuda_device, grid, tile):
                                rtol=2e-3)
 
 
-@pytest.mark.parametrize("grid,tile,head_dim", [((2, 16, 16), 64, 256), ((2, 14, 21), 49, 256),
-                                                ((2, 16, 32), 128, 192), ((1, 22, 22), 121, 136)])
+@pytest.mark.parametrize("grid,tile,head_dim,dtype", [
+    ((2, 16, 16), 64, 256, torch.bfloat16), ((2, 14, 21), 49, 256, torch.bfloat16),
+    ((2, 16, 32), 128, 192, torch.bfloat16), ((1, 22, 22), 121, 136, torch.bfloat16),
+    ((2, 18, 32), 72, 256, torch.float16)])
 @pytest.mark.parametrize("routed", [True, False])
-def test_fused_step_wide_heads(ops, cuda_device, grid, tile, head_dim, routed):
+def test_fused_step_wide_heads(ops, cuda_device, grid, tile, head_dim, dtype, routed):
     """Head dims 136..256 through dsa_bsa_fwd_tile_stats: the fp32-compute
     kernel on blocks of one tile, whose first 128-dim launch also writes the
     statistics (S runs over every dim in both), against the oracle's
     sparse_chunk / _dense_route and against bsa_fwd on the same route."""
     case, q, k, v = _tile_major_inputs(grid, 2, seed=head_dim + tile, tile=tile,
                                        head_dim=head_dim)
+    q, k, v = (x.to(dtype) for x in (q, k, v))
     tiles = q.shape[1] // case.tile
     route = None
     csr = None
